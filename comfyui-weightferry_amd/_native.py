@@ -1,0 +1,90 @@
+"""ctypes binding of libweightferry_hip.so, the gfx950 kernels behind the C ABI of ``include/weightferry.h``.
+
+The library is built in-tree by ``csrc/Makefile`` into ``lib/libweightferry_hip.so``. There is no other
+implementation: when the library is missing every GPU entry point raises ``NativeMissing`` (the drop-in never
+falls back to a CPU or torch computation of its own).
+
+torch is imported before the library is loaded so that the library binds to torch's HIP runtime (both carry the
+SONAME libamdhip64.so.7): one runtime per process, and torch's stream handles are valid in every call.
+"""
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  -- first: the library must bind to torch's HIP runtime
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libweightferry_hip.so")
+
+OK, EINVAL, EUNSUPPORTED, EHIP = 0, -1, -2, -3
+
+_p, _i64, _int, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
+
+# every symbol of include/weightferry.h: name -> (restype, argtypes)
+EXPORTS = {
+    "wf_abi_version": (_int, []),
+    "wf_last_error": (ctypes.c_char_p, []),
+    "wf_dequant": (_int, [_p, _i64, _int, _int, _int, _p, _i64, _p]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class NativeMissing(RuntimeError):
+    """libweightferry_hip.so is not built (or does not load): the HIP path cannot run."""
+
+
+def available():
+    try:
+        lib()
+        return True
+    except NativeMissing:
+        return False
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise NativeMissing(f"{LIB_PATH} is not built: run `make -C {os.path.join(_HERE, 'csrc')}` "
+                                    "(or __graft_entry__.build()) first")
+            try:
+                handle = ctypes.CDLL(LIB_PATH)
+            except OSError as exc:
+                raise NativeMissing(f"{LIB_PATH} does not load: {exc}") from exc
+            for name, (res, args) in EXPORTS.items():
+                fn = getattr(handle, name, None)
+                if fn is None:
+                    raise NativeMissing(f"{LIB_PATH} does not export {name}")
+                fn.restype = res
+                fn.argtypes = args
+            _lib = handle
+    return _lib
+
+
+def last_error():
+    msg = lib().wf_last_error()
+    return msg.decode(errors="replace") if msg else ""
+
+
+class NativeError(RuntimeError):
+    pass
+
+
+def check(rc, what):
+    """True on WF_OK, False on WF_EUNSUPPORTED ("not my case": the caller returns None), raises otherwise."""
+    if rc == OK:
+        return True
+    if rc == EUNSUPPORTED:
+        return False
+    raise NativeError(f"{what} failed ({rc}): {last_error()}")
+
+
+def stream_of(device):
+    """Raw hipStream_t of torch's current stream on ``device`` (the convention of the reference's int8 path,
+    enhancers/fused_int8.py:151)."""
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,22 @@
+"""The hot path's flags, with the reference's names and defaults (core/env.py:16-92 of the reference): an
+environment variable overrides the default (core/env.py:130-135; the reference also reads a settings file in
+ComfyUI's user directory, which is part of the host application and not of this path)."""
+import os
+
+DEFAULTS = {
+    "WEIGHTFERRY_GGUF_TRITON": "1",        # GGUF dequantisation on the GPU kernel (the name is the reference's)
+    "WEIGHTFERRY_GGUF_KQUANTS": "1",       # K-quants too
+    "WEIGHTFERRY_GGUF_LORA_FACTORS": "pin",
+    "WEIGHTFERRY_FUSED_BLOCK": "1",
+    "WEIGHTFERRY_PROFILE": None,           # "1": per-block event timeline of block streaming
+    "WEIGHTFERRY_SLOTS": None,             # number of GPU slots of block streaming (>= 2)
+    # the reference's experimental prefetch-stream priority; every stream here keeps the default priority, so
+    # the flag is read and ignored (streaming/state.py)
+    "WEIGHTFERRY_PREFETCH_PRIORITY": None,
+}
+
+
+def get(name):
+    if name in os.environ:
+        return os.environ[name]
+    return DEFAULTS.get(name)

@@ -1,0 +1,421 @@
+// GGUF block dequantisation for gfx950: the role of the Triton kernels `_deq` / `_deq_k` of the reference
+// (enhancers/gguf_dequant.py:136-256), with the same rounding chain -- every product and sum rounded to the dequant
+// dtype MID, then the cast to OUT -- and no FMA contraction (built with -ffp-contract=off).
+//
+// Layout of the work: each lane owns whole 16-byte output chunks (8 values of a 2-byte OUT), so a wave's store is
+// 1 KiB of contiguous output. K-quant super-blocks (256 values) are handled by 16 lanes; the 16-byte header of a
+// Q4_K / Q5_K super-block (d, dmin, 12 scale bytes) is one 128-bit load per lane, the quants one 64-bit load.
+// Q8_0 (34 B) and Q6_K (210 B) blocks are not dword-aligned: their quants are read as aligned dwords and shifted
+// into place with v_alignbit (funnel8), every load inside the block's own bytes.
+//
+// MID = float16 runs on packed half math. That gives the reference's bits exactly: each product d*q, d*sc is
+// exact in float32 (at most 11 + 8 significant bits), so rounding it to float16 is what v_pk_mul_f16 computes;
+// each sum of two float16 values rounded to float32 and then to float16 equals the directly rounded sum, because
+// float32 carries 24 >= 2 * 11 + 2 bits (double rounding is innocuous then). The quants enter as float16 through
+// the exponent trick: the bits 0x6400 | b are the float16 1024 + b exactly for a byte b, and subtracting 1024 (or
+// 1024 + bias) is exact.
+//
+// MID = bfloat16 / float32 run on float32 math with explicit rounding (round_to<MID>). No value on these paths is
+// a float32 subnormal (every non-zero value is at least 2^-24 in magnitude), so the hardware's round-to-nearest-even
+// conversions equal the reference's bit rule for every finite value.
+
+#include "wf_common.h"
+
+namespace wf {
+
+// ------------------------------------------------------------------------------------------------- stores
+template <int OUT>
+__device__ __forceinline__ void store8(void* out, int64_t e0, const float (&v)[8]) {
+    if constexpr (OUT == WF_F32) {
+        float4* o = reinterpret_cast<float4*>(static_cast<float*>(out) + e0);
+        o[0] = make_float4(v[0], v[1], v[2], v[3]);
+        o[1] = make_float4(v[4], v[5], v[6], v[7]);
+    } else {
+        uint4 r;
+        if constexpr (OUT == WF_BF16) {
+            r.x = pack_bf16(v[0], v[1]); r.y = pack_bf16(v[2], v[3]);
+            r.z = pack_bf16(v[4], v[5]); r.w = pack_bf16(v[6], v[7]);
+        } else {
+            r.x = pack_f16(v[0], v[1]); r.y = pack_f16(v[2], v[3]);
+            r.z = pack_f16(v[4], v[5]); r.w = pack_f16(v[6], v[7]);
+        }
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + e0) = r;
+    }
+}
+
+// 8 float16 values (MID = f16) -> OUT
+template <int OUT>
+__device__ __forceinline__ void store8h(void* out, int64_t e0, const h2 (&v)[4]) {
+    if constexpr (OUT == WF_F16) {
+        uint4 r = {h2_bits(v[0]), h2_bits(v[1]), h2_bits(v[2]), h2_bits(v[3])};
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + e0) = r;
+    } else {
+        float f[8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) { f[2 * i] = (float)v[i][0]; f[2 * i + 1] = (float)v[i][1]; }
+        store8<OUT>(out, e0, f);
+    }
+}
+
+// ------------------------------------------------------------------------------------------- quant helpers
+// bytes b0..b3 of w -> float16 pairs (1024 + b0, 1024 + b1), (1024 + b2, 1024 + b3)
+__device__ __forceinline__ h2 biased_lo(uint32_t w) { return as_h2(__builtin_amdgcn_perm(0x64646464u, w, 0x04010400u)); }
+__device__ __forceinline__ h2 biased_hi(uint32_t w) { return as_h2(__builtin_amdgcn_perm(0x64646464u, w, 0x04030402u)); }
+
+__device__ __forceinline__ h2 h2s(float a) { h2 r; r[0] = (_Float16)a; r[1] = (_Float16)a; return r; }
+__device__ __forceinline__ h2 lo2(h2 v) { h2 r; r[0] = v[0]; r[1] = v[0]; return r; }
+__device__ __forceinline__ h2 hi2(h2 v) { h2 r; r[0] = v[1]; r[1] = v[1]; return r; }
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
+
+// get_scale_min of sub-block sub (0..7) from the scale bytes s0 = s[0..3], s1 = s[4..7], s2 = s[8..11]
+// (enhancers/gguf_dequant.py:170-185)
+__device__ __forceinline__ void scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int sub, uint32_t& sc,
+                                          uint32_t& m) {
+    const int j = sub & 3;
+    const uint32_t a = byte_of(s0, j), b = byte_of(s1, j), c = byte_of(s2, j);
+    if (sub < 4) {
+        sc = a & 63u;
+        m = b & 63u;
+    } else {
+        sc = (c & 0xfu) | ((a >> 2) & 0x30u);
+        m = (c >> 4) | ((b >> 2) & 0x30u);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------- Q8_0
+// 34-byte blocks of 32 values: d (f16) at 0, int8 quants at 2. Lane = 8 values (4 lanes per block).
+// x = OUT(MID(MID(d) * q)), enhancers/gguf_dequant.py:145-160.
+template <int MID, int OUT>
+__global__ __launch_bounds__(256) void deq_q8_0(const uint8_t* __restrict__ src, void* __restrict__ out,
+                                                int64_t nlanes) {
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < nlanes;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t blk = t >> 2;
+        const int c = (int)(t & 3);
+        const uint32_t dbits = *reinterpret_cast<const uint16_t*>(src + blk * 34);
+        const int64_t o = blk * 34 + 2 + 8 * c;               // first quant byte of this lane
+        const int64_t a = o & ~(int64_t)3;
+        const uint32_t sh = (uint32_t)(o & 3) * 8u;           // 0 or 16
+        const uint32_t* wp = reinterpret_cast<const uint32_t*>(src + a);
+        const uint32_t w0 = wp[0], w1 = wp[1];
+        const uint32_t w2 = *reinterpret_cast<const uint16_t*>(src + a + (sh ? 8 : 6));  // inside [o, o + 8)
+        const uint2 q = funnel8(w0, w1, w2, sh);
+        const int64_t e0 = t * 8;
+        if constexpr (MID == WF_F16) {
+            const h2 d2 = as_h2(dbits | (dbits << 16));
+            const h2 bias = h2s(-1152.0f);                     // 1024 + 128: int8 as unsigned byte ^ 0x80
+            const uint32_t u0 = q.x ^ 0x80808080u, u1 = q.y ^ 0x80808080u;
+            h2 v[4];
+            v[0] = d2 * (biased_lo(u0) + bias);
+            v[1] = d2 * (biased_hi(u0) + bias);
+            v[2] = d2 * (biased_lo(u1) + bias);
+            v[3] = d2 * (biased_hi(u1) + bias);
+            store8h<OUT>(out, e0, v);
+        } else {
+            const float d = round_to<MID>(f16_bits_to_f32(dbits));
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[i] = round_to<MID>(d * (float)(int8_t)byte_of(q.x, i));
+                v[4 + i] = round_to<MID>(d * (float)(int8_t)byte_of(q.y, i));
+            }
+            store8<OUT>(out, e0, v);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------ Q4_K / Q5_K
+// Q4_K (144 B): d @0, dmin @2, scales[12] @4, qs[128] @16. Q5_K (176 B): the same plus qh[32] @16, qs @48.
+// Lane j (16 per super-block): pair p = j / 4, chunk c = j % 4 -> qs bytes [32p + 8c, +8). Their low nibbles are
+// values 64p + 8c + i (sub-block 2p), their high nibbles values 64p + 32 + 8c + i (sub-block 2p + 1); Q5_K adds
+// bit 2p / 2p + 1 of qh[8c + i] as bit 4. x = MID(MID(MID(d * sc) * q) - MID(dmin * m)), :195-212.
+template <int QT, int MID, int OUT>
+__global__ __launch_bounds__(256) void deq_q45_k(const uint8_t* __restrict__ src, void* __restrict__ out,
+                                                 int64_t nlanes) {
+    constexpr int TS = QT == 12 ? 144 : 176;
+    constexpr int QS = QT == 12 ? 16 : 48;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < nlanes;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t sb = t >> 4;
+        const int j = (int)(t & 15), p = j >> 2, c = j & 3;
+        const uint8_t* base = src + sb * TS;
+        const uint4 hdr = *reinterpret_cast<const uint4*>(base);
+        const uint2 qs = *reinterpret_cast<const uint2*>(base + QS + 32 * p + 8 * c);
+        uint32_t lo[2], hi[2];
+        lo[0] = qs.x & 0x0f0f0f0fu; hi[0] = (qs.x >> 4) & 0x0f0f0f0fu;
+        lo[1] = qs.y & 0x0f0f0f0fu; hi[1] = (qs.y >> 4) & 0x0f0f0f0fu;
+        if constexpr (QT == 13) {
+            const uint2 qh = *reinterpret_cast<const uint2*>(base + 16 + 8 * c);
+            lo[0] |= ((qh.x >> (2 * p)) & 0x01010101u) << 4;
+            hi[0] |= ((qh.x >> (2 * p + 1)) & 0x01010101u) << 4;
+            lo[1] |= ((qh.y >> (2 * p)) & 0x01010101u) << 4;
+            hi[1] |= ((qh.y >> (2 * p + 1)) & 0x01010101u) << 4;
+        }
+        uint32_t scA, mA, scB, mB;
+        scale_min(hdr.y, hdr.z, hdr.w, 2 * p, scA, mA);
+        scale_min(hdr.y, hdr.z, hdr.w, 2 * p + 1, scB, mB);
+        const int64_t eA = sb * 256 + 64 * p + 8 * c, eB = eA + 32;
+        if constexpr (MID == WF_F16) {
+            const h2 dd = as_h2(hdr.x);                         // (d, dmin)
+            h2 smA, smB;
+            smA[0] = (_Float16)scA; smA[1] = (_Float16)mA;
+            smB[0] = (_Float16)scB; smB[1] = (_Float16)mB;
+            const h2 pA = dd * smA, pB = dd * smB;              // (d * sc, dmin * m), each rounded to f16
+            const h2 dsA = lo2(pA), dmA = hi2(pA), dsB = lo2(pB), dmB = hi2(pB);
+            const h2 bias = h2s(-1024.0f);
+            h2 va[4], vb[4];
+#pragma unroll
+            for (int w = 0; w < 2; w++) {
+                va[2 * w] = dsA * (biased_lo(lo[w]) + bias) - dmA;
+                va[2 * w + 1] = dsA * (biased_hi(lo[w]) + bias) - dmA;
+                vb[2 * w] = dsB * (biased_lo(hi[w]) + bias) - dmB;
+                vb[2 * w + 1] = dsB * (biased_hi(hi[w]) + bias) - dmB;
+            }
+            store8h<OUT>(out, eA, va);
+            store8h<OUT>(out, eB, vb);
+        } else {
+            const float d = round_to<MID>(f16_bits_to_f32(hdr.x & 0xffffu));
+            const float dmin = round_to<MID>(f16_bits_to_f32(hdr.x >> 16));
+            const float dsA = round_to<MID>(d * (float)scA), dmA = round_to<MID>(dmin * (float)mA);
+            const float dsB = round_to<MID>(d * (float)scB), dmB = round_to<MID>(dmin * (float)mB);
+            float va[8], vb[8];
+#pragma unroll
+            for (int w = 0; w < 2; w++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    va[4 * w + i] = round_to<MID>(round_to<MID>(dsA * (float)byte_of(lo[w], i)) - dmA);
+                    vb[4 * w + i] = round_to<MID>(round_to<MID>(dsB * (float)byte_of(hi[w], i)) - dmB);
+                }
+            store8<OUT>(out, eA, va);
+            store8<OUT>(out, eB, vb);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------- Q6_K
+// 210 B: ql[128] @0, qh[64] @128, int8 scales[16] @192, d @208. Lane j (16 per super-block): half h = j / 8,
+// chunk c = j % 8 -> ql bytes [64h + 8c, +8): low nibbles are values 128h + 8c + i, high nibbles 128h + 64 + 8c + i;
+// their 2 high bits come from qh[32h + 8(c % 4) + i] at shift 2(c / 4) and 2(2 + c / 4); scales 8h + c / 2 and
+// 8h + 4 + c / 2. x = MID(MID(MID(d) * sc) * q), q = (lo | hi << 4) - 32, :213-224.
+__device__ __forceinline__ uint2 load8_a2(const uint8_t* base, int64_t o) {
+    // 8 bytes at byte offset o (o even): reads [o, o + 8) plus, when o is 2 (mod 4), the 2 bytes before o (the
+    // end of the previous block, or of this block's earlier field; never before the buffer, since block 0 starts
+    // dword-aligned)
+    const int64_t a = o & ~(int64_t)3;
+    const uint32_t sh = (uint32_t)(o & 3) * 8u;
+    const uint32_t* wp = reinterpret_cast<const uint32_t*>(base + a);
+    const uint32_t w0 = wp[0], w1 = wp[1];
+    const uint32_t w2 = *reinterpret_cast<const uint16_t*>(base + a + (sh ? 8 : 6));
+    return funnel8(w0, w1, w2, sh);
+}
+
+template <int MID, int OUT>
+__global__ __launch_bounds__(256) void deq_q6_k(const uint8_t* __restrict__ src, void* __restrict__ out,
+                                                int64_t nlanes) {
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < nlanes;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t sb = t >> 4;
+        const int j = (int)(t & 15), h = j >> 3, c = j & 7;
+        const int64_t b0 = sb * 210;
+        const uint2 ql = load8_a2(src, b0 + 64 * h + 8 * c);
+        const uint2 qh = load8_a2(src, b0 + 128 + 32 * h + 8 * (c & 3));
+        const uint32_t sl = src[b0 + 192 + 8 * h + (c >> 1)];
+        const uint32_t shv = src[b0 + 192 + 8 * h + 4 + (c >> 1)];
+        const uint32_t dbits = *reinterpret_cast<const uint16_t*>(src + b0 + 208);
+        const uint32_t s1 = 2u * (uint32_t)(c >> 2), s2 = s1 + 4u;
+        uint32_t lo[2], hi[2];   // 6-bit codes 0..63, one per byte
+        lo[0] = (ql.x & 0x0f0f0f0fu) | (((qh.x >> s1) & 0x03030303u) << 4);
+        hi[0] = ((ql.x >> 4) & 0x0f0f0f0fu) | (((qh.x >> s2) & 0x03030303u) << 4);
+        lo[1] = (ql.y & 0x0f0f0f0fu) | (((qh.y >> s1) & 0x03030303u) << 4);
+        hi[1] = ((ql.y >> 4) & 0x0f0f0f0fu) | (((qh.y >> s2) & 0x03030303u) << 4);
+        const int64_t eA = sb * 256 + 128 * h + 8 * c, eB = eA + 64;
+        if constexpr (MID == WF_F16) {
+            const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)dbits);
+            h2 dsc;
+            dsc[0] = (_Float16)(float)(int8_t)sl;
+            dsc[1] = (_Float16)(float)(int8_t)shv;
+            h2 dd; dd[0] = d; dd[1] = d;
+            const h2 pd = dd * dsc;                              // (d * sc_lo, d * sc_hi), rounded to f16
+            const h2 dA = lo2(pd), dB = hi2(pd);
+            const h2 bias = h2s(-1056.0f);                       // 1024 + 32
+            h2 va[4], vb[4];
+#pragma unroll
+            for (int w = 0; w < 2; w++) {
+                va[2 * w] = dA * (biased_lo(lo[w]) + bias);
+                va[2 * w + 1] = dA * (biased_hi(lo[w]) + bias);
+                vb[2 * w] = dB * (biased_lo(hi[w]) + bias);
+                vb[2 * w + 1] = dB * (biased_hi(hi[w]) + bias);
+            }
+            store8h<OUT>(out, eA, va);
+            store8h<OUT>(out, eB, vb);
+        } else {
+            const float d = round_to<MID>(f16_bits_to_f32(dbits));
+            const float dA = round_to<MID>(d * (float)(int8_t)sl), dB = round_to<MID>(d * (float)(int8_t)shv);
+            float va[8], vb[8];
+#pragma unroll
+            for (int w = 0; w < 2; w++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    va[4 * w + i] = round_to<MID>(dA * (float)((int)byte_of(lo[w], i) - 32));
+                    vb[4 * w + i] = round_to<MID>(dB * (float)((int)byte_of(hi[w], i) - 32));
+                }
+            store8<OUT>(out, eA, va);
+            store8<OUT>(out, eB, vb);
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------- other formats (byte gathers)
+// The legacy formats Q4_0 / Q4_1 / Q5_0 / Q5_1 and the K-quants Q2_K / Q3_K: one lane per 8 values, the
+// reference's per-value formulas with byte loads (enhancers/gguf_dequant.py:136-167,225-249).
+template <int QT>
+struct Fmt;
+template <> struct Fmt<2> { static constexpr int TS = 18, PER = 32, HAS_M = 0, QH = -1, QS = 2, SUB = 8; };
+template <> struct Fmt<3> { static constexpr int TS = 20, PER = 32, HAS_M = 1, QH = -1, QS = 4, SUB = 0; };
+template <> struct Fmt<6> { static constexpr int TS = 22, PER = 32, HAS_M = 0, QH = 2, QS = 6, SUB = 16; };
+template <> struct Fmt<7> { static constexpr int TS = 24, PER = 32, HAS_M = 1, QH = 4, QS = 8, SUB = 0; };
+template <> struct Fmt<10> { static constexpr int TS = 84, PER = 256; };
+template <> struct Fmt<11> { static constexpr int TS = 110, PER = 256; };
+
+__device__ __forceinline__ float ld_f16(const uint8_t* p) {
+    return f16_bits_to_f32((uint32_t)p[0] | ((uint32_t)p[1] << 8));
+}
+
+template <int QT, int MID>
+__device__ __forceinline__ float deq_value(const uint8_t* b, int v) {
+    if constexpr (QT == 2 || QT == 3 || QT == 6 || QT == 7) {
+        using F = Fmt<QT>;
+        const float d = round_to<MID>(ld_f16(b));
+        int nib = (b[F::QS + (v & 15)] >> ((v >> 4) * 4)) & 0xF;
+        if constexpr (F::QH >= 0) nib |= ((b[F::QH + (v >> 3)] >> (v & 7)) & 1) << 4;
+        float x = round_to<MID>(d * (float)(nib - F::SUB));
+        if constexpr (F::HAS_M) x = round_to<MID>(x + round_to<MID>(ld_f16(b + 2)));
+        return x;
+    } else if constexpr (QT == 11) {
+        const int i = v >> 4;
+        const int ls = (b[96 + (i & 7)] >> ((i >> 3) * 4)) & 0xF;
+        const int hs = (b[104 + (i & 3)] >> ((i >> 2) * 2)) & 3;
+        const int sc = (ls | (hs << 4)) - 32;
+        const float d = round_to<MID>(round_to<MID>(ld_f16(b + 108)) * (float)sc);
+        const int r = v & 127;
+        const int ql = (b[32 + (v >> 7) * 32 + (r & 31)] >> ((r >> 5) * 2)) & 3;
+        const int hb = ((b[v & 31] >> (v >> 5)) & 1) ^ 1;
+        return round_to<MID>(d * (float)(ql - (hb << 2)));
+    } else {  // Q2_K
+        const int sb = b[v >> 4];
+        const float dl = round_to<MID>(round_to<MID>(ld_f16(b + 80)) * (float)(sb & 0xF));
+        const float ml = round_to<MID>(round_to<MID>(ld_f16(b + 82)) * (float)(sb >> 4));
+        const int r = v & 127;
+        const int q = (b[16 + (v >> 7) * 32 + (r & 31)] >> ((r >> 5) * 2)) & 3;
+        return round_to<MID>(round_to<MID>(dl * (float)q) - ml);
+    }
+}
+
+template <int QT, int MID, int OUT>
+__global__ __launch_bounds__(256) void deq_gather(const uint8_t* __restrict__ src, void* __restrict__ out,
+                                                  int64_t nlanes) {
+    constexpr int TS = Fmt<QT>::TS, PER = Fmt<QT>::PER, LPB = PER / 8;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < nlanes;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t blk = t / LPB;
+        const int v0 = (int)(t % LPB) * 8;
+        const uint8_t* b = src + blk * TS;
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = deq_value<QT, MID>(b, v0 + i);
+        store8<OUT>(out, t * 8, v);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------- launch
+struct Launch {
+    int64_t nlanes;
+    dim3 grid;
+};
+
+static Launch plan(int64_t nlanes) {
+    // one lane-iteration per thread up to 2^20 workgroups; beyond that the kernels loop
+    int64_t wgs = (nlanes + 255) / 256;
+    if (wgs > (1 << 20)) wgs = 1 << 20;
+    if (wgs < 1) wgs = 1;
+    return {nlanes, dim3((unsigned)wgs)};
+}
+
+template <int MID, int OUT>
+static void launch_fmt(int qtype, const uint8_t* src, void* out, int64_t nblocks, hipStream_t s) {
+    switch (qtype) {
+    case 8: { Launch L = plan(nblocks * 4); deq_q8_0<MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
+    case 12: { Launch L = plan(nblocks * 16); deq_q45_k<12, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
+    case 13: { Launch L = plan(nblocks * 16); deq_q45_k<13, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
+    case 14: { Launch L = plan(nblocks * 16); deq_q6_k<MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
+    case 2: { Launch L = plan(nblocks * 4); deq_gather<2, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
+    case 3: { Launch L = plan(nblocks * 4); deq_gather<3, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
+    case 6: { Launch L = plan(nblocks * 4); deq_gather<6, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
+    case 7: { Launch L = plan(nblocks * 4); deq_gather<7, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
+    case 10: { Launch L = plan(nblocks * 32); deq_gather<10, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
+    case 11: { Launch L = plan(nblocks * 32); deq_gather<11, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
+    default: break;
+    }
+}
+
+template <int MID>
+static void launch_mid(int out_dt, int qtype, const uint8_t* src, void* out, int64_t nblocks, hipStream_t s) {
+    if (out_dt == WF_F16) launch_fmt<MID, WF_F16>(qtype, src, out, nblocks, s);
+    else if (out_dt == WF_BF16) launch_fmt<MID, WF_BF16>(qtype, src, out, nblocks, s);
+    else launch_fmt<MID, WF_F32>(qtype, src, out, nblocks, s);
+}
+
+// bytes per block and values per block of a supported GGML type (0 when unsupported)
+int block_bytes(int qtype, int* per) {
+    switch (qtype) {
+    case 2: *per = 32; return 18;
+    case 3: *per = 32; return 20;
+    case 6: *per = 32; return 22;
+    case 7: *per = 32; return 24;
+    case 8: *per = 32; return 34;
+    case 10: *per = 256; return 84;
+    case 11: *per = 256; return 110;
+    case 12: *per = 256; return 144;
+    case 13: *per = 256; return 176;
+    case 14: *per = 256; return 210;
+    default: *per = 0; return 0;
+    }
+}
+
+}  // namespace wf
+
+extern "C" int wf_dequant(const void* src, int64_t src_bytes, int qtype, int mid_dt, int out_dt, void* out,
+                          int64_t n_values, void* stream) {
+    using namespace wf;
+    int per = 0;
+    const int ts = block_bytes(qtype, &per);
+    if (!ts) { set_error("wf_dequant: GGML type %d is not handled", qtype); return WF_EUNSUPPORTED; }
+    if (mid_dt < 0 || mid_dt > 2 || out_dt < 0 || out_dt > 2) {
+        set_error("wf_dequant: dtype codes %d / %d", mid_dt, out_dt);
+        return WF_EUNSUPPORTED;
+    }
+    if (src_bytes < 0 || n_values < 0 || src_bytes % ts) {
+        set_error("wf_dequant: %lld bytes is not a whole number of %d-byte blocks", (long long)src_bytes, ts);
+        return WF_EUNSUPPORTED;
+    }
+    const int64_t nblocks = src_bytes / ts;
+    if (nblocks * per != n_values) {
+        set_error("wf_dequant: %lld blocks hold %lld values, not %lld", (long long)nblocks,
+                  (long long)(nblocks * per), (long long)n_values);
+        return WF_EUNSUPPORTED;
+    }
+    if (n_values == 0) return WF_OK;
+    if (!src || !out) { set_error("wf_dequant: null pointer"); return WF_EINVAL; }
+    if (!aligned(src, 16) || !aligned(out, 16)) {
+        set_error("wf_dequant: src and out must be 16-byte aligned");
+        return WF_EUNSUPPORTED;
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint8_t* p = static_cast<const uint8_t*>(src);
+    if (mid_dt == WF_F16) launch_mid<WF_F16>(out_dt, qtype, p, out, nblocks, s);
+    else if (mid_dt == WF_BF16) launch_mid<WF_BF16>(out_dt, qtype, p, out, nblocks, s);
+    else launch_mid<WF_F32>(out_dt, qtype, p, out, nblocks, s);
+    WF_LAUNCH_CHECK("wf_dequant launch");
+    return WF_OK;
+}

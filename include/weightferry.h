@@ -1,0 +1,54 @@
+/*
+ * weightferry.h -- C ABI of the MI355X (gfx950) quantized-weight hot path.
+ *
+ * One shared library, libweightferry_hip.so, built from comfyui-weightferry_amd/csrc/. Plain pointers and sizes
+ * only; every device pointer is memory the caller allocated (the library never allocates or frees device memory
+ * on these paths). `stream` is a hipStream_t (NULL = the default stream); every call is asynchronous on it and
+ * never synchronises the host.
+ *
+ * Return codes: WF_OK (0) on success; WF_EUNSUPPORTED (-2) when the call is "not my case" (the reference's
+ * Python returns None there and the host application's own code runs); WF_EINVAL (-1) for malformed arguments;
+ * WF_EHIP (-3) when a HIP runtime call failed. wf_last_error() gives a thread-local message for the last failure
+ * on the calling thread.
+ *
+ * Dtype codes follow enhancers/gguf_dequant.py:58 of the reference: 0 float16, 1 bfloat16, 2 float32.
+ * GGML type ids follow enhancers/gguf_dequant.py:52-56: 2 Q4_0, 3 Q4_1, 6 Q5_0, 7 Q5_1, 8 Q8_0, 10 Q2_K, 11 Q3_K,
+ * 12 Q4_K, 13 Q5_K, 14 Q6_K.
+ */
+#ifndef WEIGHTFERRY_H
+#define WEIGHTFERRY_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WF_OK 0
+#define WF_EINVAL (-1)
+#define WF_EUNSUPPORTED (-2)
+#define WF_EHIP (-3)
+
+#define WF_F16 0
+#define WF_BF16 1
+#define WF_F32 2
+
+/* ABI version (bumped on any signature change) and the last error message of the calling thread. */
+int wf_abi_version(void);
+const char* wf_last_error(void);
+
+/* ---------------------------------------------------------------------------------------------- dequantisation
+ * Replaces the Triton launches of `dequantize` / `_dequantize_k` (enhancers/gguf_dequant.py:277-326; kernels
+ * `_deq` :136-167 and `_deq_k` :188-256). `src` holds src_bytes of GGUF blocks of type `qtype`; `out` receives
+ * n_values values of dtype out_dt, each computed with the reference's rounding chain in the dequant dtype mid_dt.
+ * WF_EUNSUPPORTED when qtype / dtypes are not handled or src_bytes does not hold exactly n_values values (the
+ * reference returns None there, :280-286,312-320), or when src / out are not 16-byte aligned. */
+int wf_dequant(const void* src, int64_t src_bytes, int qtype, int mid_dt, int out_dt, void* out, int64_t n_values,
+               void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WEIGHTFERRY_H */
