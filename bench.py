@@ -36,27 +36,10 @@ def _log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-class LaunchTimer:
-    """Start / end events around every launch on torch's current stream (the stream the kernels run on)."""
-
-    def __init__(self, torch):
-        self.torch = torch
-        self.pairs = []
-
-    def __call__(self, fn):
-        t = self.torch
-        a, b = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
-        a.record()
-        fn()
-        b.record()
-        self.pairs.append((a, b))
-
-    def mean_ms(self):
-        return sum(a.elapsed_time(b) for a, b in self.pairs) / max(1, len(self.pairs))
-
-
-def dequant_leg(torch, native, raws, shapes, qtype, mid, out_dt, steps, warmup, timer=True):
-    """Time `steps` steps of dequantising every matrix once; returns (ms per step, mean kernel ms, bytes/step)."""
+def dequant_leg(torch, native, raws, shapes, qtype, mid, out_dt, steps, warmup):
+    """Time `steps` steps of dequantising every matrix once, launched back to back on torch's current stream with
+    events at both ends of the timed region on that stream. Returns (ms per step, mean ms per launch, bytes/step);
+    the launches are all of one kernel, so the mean per launch is that kernel's average duration."""
     lib = native.lib()
     dev = torch.device("cuda:0")
     stream = native.stream_of(dev)
@@ -76,21 +59,17 @@ def dequant_leg(torch, native, raws, shapes, qtype, mid, out_dt, steps, warmup, 
         for m in range(len(shapes)):
             launch(i % ROTATE, m)
     torch.cuda.synchronize()
-    lt = LaunchTimer(torch)
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record()
     for i in range(steps):
         for m in range(len(shapes)):
-            if timer:
-                lt(lambda: launch(i % ROTATE, m))
-            else:
-                launch(i % ROTATE, m)
+            launch(i % ROTATE, m)
     t1.record()
     torch.cuda.synchronize()
     ms_step = t0.elapsed_time(t1) / steps
     del ins, outs
     torch.cuda.empty_cache()
-    return ms_step, lt.mean_ms(), algo
+    return ms_step, ms_step / len(shapes), algo
 
 
 def cpu_baseline_dequant(torch, raw, qtype, rows, cols, budget_s=12.0):
@@ -180,7 +159,7 @@ def main():
                    "bytes_per_step": algo, "rotating_copies": ROTATE},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "wf::deq_q45_k<12, f16, bf16>", "kernel_us": round(kern_ms * 1e3, 2),
+                     "kernel": "wf::deq_items<wf::Q45_K<12, f16, bf16>>", "kernel_us": round(kern_ms * 1e3, 2),
                      "bytes_per_launch": per_launch},
         "cpu_baseline": cpu,
         "also": also,

@@ -21,15 +21,37 @@
 
 #include "wf_common.h"
 
+// Launch shape of the streaming kernels: each thread handles DEQ_ITEMS lane-items with every load issued before any
+// arithmetic; DEQ_NT_STORE writes the output with non-temporal stores (it is read by a later kernel, not this one).
+// Measured on MI355X: 1 item per thread and non-temporal stores are the fastest (a persistent, grid-capped launch
+// and more items per thread were slower).
+#ifndef DEQ_ITEMS
+#define DEQ_ITEMS 1
+#endif
+#ifndef DEQ_NT_STORE
+#define DEQ_NT_STORE 1
+#endif
+
 namespace wf {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void st(uint4* p, const uint4& v) {
+#if DEQ_NT_STORE
+    u32x4 w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
+#else
+    *p = v;
+#endif
+}
 
 // ------------------------------------------------------------------------------------------------- stores
 template <int OUT>
-__device__ __forceinline__ void store8(void* out, int64_t e0, const float (&v)[8]) {
+__device__ __forceinline__ void store8(void* out, int64_t e0, const float (&v)[8]) {  // e0: element index
     if constexpr (OUT == WF_F32) {
-        float4* o = reinterpret_cast<float4*>(static_cast<float*>(out) + e0);
-        o[0] = make_float4(v[0], v[1], v[2], v[3]);
-        o[1] = make_float4(v[4], v[5], v[6], v[7]);
+        uint4* o = reinterpret_cast<uint4*>(static_cast<float*>(out) + e0);
+        st(o, make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])));
+        st(o + 1, make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])));
     } else {
         uint4 r;
         if constexpr (OUT == WF_BF16) {
@@ -39,7 +61,7 @@ __device__ __forceinline__ void store8(void* out, int64_t e0, const float (&v)[8
             r.x = pack_f16(v[0], v[1]); r.y = pack_f16(v[2], v[3]);
             r.z = pack_f16(v[4], v[5]); r.w = pack_f16(v[6], v[7]);
         }
-        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + e0) = r;
+        st(reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + e0), r);
     }
 }
 
@@ -48,7 +70,7 @@ template <int OUT>
 __device__ __forceinline__ void store8h(void* out, int64_t e0, const h2 (&v)[4]) {
     if constexpr (OUT == WF_F16) {
         uint4 r = {h2_bits(v[0]), h2_bits(v[1]), h2_bits(v[2]), h2_bits(v[3])};
-        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + e0) = r;
+        st(reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + e0), r);
     } else {
         float f[8];
 #pragma unroll
@@ -83,29 +105,58 @@ __device__ __forceinline__ void scale_min(uint32_t s0, uint32_t s1, uint32_t s2,
     }
 }
 
+// Every fast kernel is a Format with load(src, t) -> Raw (only global loads) and emit(out, t, Raw) (arithmetic and
+// stores) for lane-item t of one workgroup's tile; the driver issues the loads of DEQ_ITEMS items before emitting
+// any of them. A tile is DEQ_ITEMS * 256 lane-items = whole blocks, so the workgroup's block and output bases are
+// scalar and each lane works with 32-bit offsets. The grid covers every lane-item (no loop).
+template <typename F>
+__global__ __launch_bounds__(256) void deq_items(const uint8_t* __restrict__ src, void* __restrict__ out,
+                                                 int64_t nlanes) {
+    constexpr int U = DEQ_ITEMS;
+    constexpr int TILE_BLOCKS = U * 256 / F::LANES_PER_BLOCK;
+    const int64_t t0 = (int64_t)blockIdx.x * (U * 256);
+    const uint8_t* tsrc = src + (int64_t)blockIdx.x * TILE_BLOCKS * F::TS;
+    void* tout = static_cast<char*>(out) + (int64_t)blockIdx.x * TILE_BLOCKS * F::PER * F::OUT_BYTES;
+    typename F::Raw r[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const uint32_t t = threadIdx.x + 256u * u;
+        if (t0 + t < nlanes) r[u] = F::load(tsrc, t);
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const uint32_t t = threadIdx.x + 256u * u;
+        if (t0 + t < nlanes) F::emit(tout, t, r[u]);
+    }
+}
+
 // ------------------------------------------------------------------------------------------------- Q8_0
-// 34-byte blocks of 32 values: d (f16) at 0, int8 quants at 2. Lane = 8 values (4 lanes per block).
+// 34-byte blocks of 32 values: d (f16) at 0, int8 quants at 2. Lane-item = 8 values (4 per block).
 // x = OUT(MID(MID(d) * q)), enhancers/gguf_dequant.py:145-160.
 template <int MID, int OUT>
-__global__ __launch_bounds__(256) void deq_q8_0(const uint8_t* __restrict__ src, void* __restrict__ out,
-                                                int64_t nlanes) {
-    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < nlanes;
-         t += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t blk = t >> 2;
-        const int c = (int)(t & 3);
-        const uint32_t dbits = *reinterpret_cast<const uint16_t*>(src + blk * 34);
-        const int64_t o = blk * 34 + 2 + 8 * c;               // first quant byte of this lane
-        const int64_t a = o & ~(int64_t)3;
+struct Q8_0 {
+    static constexpr int LANES_PER_BLOCK = 4, TS = 34, PER = 32, OUT_BYTES = OUT == WF_F32 ? 4 : 2;
+    struct Raw { uint32_t d; uint2 q; };
+    static __device__ __forceinline__ Raw load(const uint8_t* src, uint32_t t) {
+        const uint32_t blk = t >> 2;
+        const uint32_t c = t & 3;
+        Raw r;
+        r.d = *reinterpret_cast<const uint16_t*>(src + blk * 34);
+        const uint32_t o = blk * 34 + 2 + 8 * c;              // first quant byte of this lane
+        const uint32_t a = o & ~3u;
         const uint32_t sh = (uint32_t)(o & 3) * 8u;           // 0 or 16
         const uint32_t* wp = reinterpret_cast<const uint32_t*>(src + a);
         const uint32_t w0 = wp[0], w1 = wp[1];
         const uint32_t w2 = *reinterpret_cast<const uint16_t*>(src + a + (sh ? 8 : 6));  // inside [o, o + 8)
-        const uint2 q = funnel8(w0, w1, w2, sh);
-        const int64_t e0 = t * 8;
+        r.q = funnel8(w0, w1, w2, sh);
+        return r;
+    }
+    static __device__ __forceinline__ void emit(void* out, uint32_t t, const Raw& r) {
+        const uint32_t e0 = t * 8;
         if constexpr (MID == WF_F16) {
-            const h2 d2 = as_h2(dbits | (dbits << 16));
+            const h2 d2 = as_h2(r.d | (r.d << 16));
             const h2 bias = h2s(-1152.0f);                     // 1024 + 128: int8 as unsigned byte ^ 0x80
-            const uint32_t u0 = q.x ^ 0x80808080u, u1 = q.y ^ 0x80808080u;
+            const uint32_t u0 = r.q.x ^ 0x80808080u, u1 = r.q.y ^ 0x80808080u;
             h2 v[4];
             v[0] = d2 * (biased_lo(u0) + bias);
             v[1] = d2 * (biased_hi(u0) + bias);
@@ -113,97 +164,107 @@ __global__ __launch_bounds__(256) void deq_q8_0(const uint8_t* __restrict__ src,
             v[3] = d2 * (biased_hi(u1) + bias);
             store8h<OUT>(out, e0, v);
         } else {
-            const float d = round_to<MID>(f16_bits_to_f32(dbits));
+            const float d = round_to<MID>(f16_bits_to_f32(r.d));
             float v[8];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                v[i] = round_to<MID>(d * (float)(int8_t)byte_of(q.x, i));
-                v[4 + i] = round_to<MID>(d * (float)(int8_t)byte_of(q.y, i));
+                v[i] = round_to<MID>(d * (float)(int8_t)byte_of(r.q.x, i));
+                v[4 + i] = round_to<MID>(d * (float)(int8_t)byte_of(r.q.y, i));
             }
             store8<OUT>(out, e0, v);
         }
     }
-}
+};
 
 // ------------------------------------------------------------------------------------------ Q4_K / Q5_K
 // Q4_K (144 B): d @0, dmin @2, scales[12] @4, qs[128] @16. Q5_K (176 B): the same plus qh[32] @16, qs @48.
-// Lane j (16 per super-block): pair p = j / 4, chunk c = j % 4 -> qs bytes [32p + 8c, +8). Their low nibbles are
-// values 64p + 8c + i (sub-block 2p), their high nibbles values 64p + 32 + 8c + i (sub-block 2p + 1); Q5_K adds
-// bit 2p / 2p + 1 of qh[8c + i] as bit 4. x = MID(MID(MID(d * sc) * q) - MID(dmin * m)), :195-212.
+// Lane-item j (16 per super-block) writes values [8j, 8j + 8) and [128 + 8j, 128 + 8j + 8), so each of its two
+// store instructions covers whole 256-byte runs of output. With g = j / 4 and c = j % 4, those are sub-blocks g
+// and 4 + g; their quants are nibble g % 2 of qs bytes [32(g / 2) + 8c, +8) and [64 + 32(g / 2) + 8c, +8), and Q5_K
+// adds bit g / 4 + g of qh[8c + i] as bit 4. x = MID(MID(MID(d * sc) * q) - MID(dmin * m)), :195-212; sc / m of
+// sub-block g (< 4) and 4 + g from scale bytes g, g + 4, g + 8 (get_scale_min, :170-185).
 template <int QT, int MID, int OUT>
-__global__ __launch_bounds__(256) void deq_q45_k(const uint8_t* __restrict__ src, void* __restrict__ out,
-                                                 int64_t nlanes) {
-    constexpr int TS = QT == 12 ? 144 : 176;
-    constexpr int QS = QT == 12 ? 16 : 48;
-    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < nlanes;
-         t += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t sb = t >> 4;
-        const int j = (int)(t & 15), p = j >> 2, c = j & 3;
+struct Q45_K {
+    static constexpr int LANES_PER_BLOCK = 16, PER = 256, OUT_BYTES = OUT == WF_F32 ? 4 : 2;
+    static constexpr int TS = QT == 12 ? 144 : 176;
+    static constexpr int QS = QT == 12 ? 16 : 48;
+    struct Raw { uint4 hdr; uint2 q1, q2, qh; };
+    static __device__ __forceinline__ Raw load(const uint8_t* src, uint32_t t) {
+        const uint32_t sb = t >> 4;
+        const int j = (int)(t & 15), g = j >> 2, c = j & 3;
         const uint8_t* base = src + sb * TS;
-        const uint4 hdr = *reinterpret_cast<const uint4*>(base);
-        const uint2 qs = *reinterpret_cast<const uint2*>(base + QS + 32 * p + 8 * c);
-        uint32_t lo[2], hi[2];
-        lo[0] = qs.x & 0x0f0f0f0fu; hi[0] = (qs.x >> 4) & 0x0f0f0f0fu;
-        lo[1] = qs.y & 0x0f0f0f0fu; hi[1] = (qs.y >> 4) & 0x0f0f0f0fu;
+        const int o = QS + 32 * (g >> 1) + 8 * c;
+        Raw r;
+        r.hdr = *reinterpret_cast<const uint4*>(base);
+        r.q1 = *reinterpret_cast<const uint2*>(base + o);
+        r.q2 = *reinterpret_cast<const uint2*>(base + o + 64);
+        if constexpr (QT == 13) r.qh = *reinterpret_cast<const uint2*>(base + 16 + 8 * c);
+        return r;
+    }
+    static __device__ __forceinline__ void emit(void* out, uint32_t t, const Raw& r) {
+        const uint32_t sb = t >> 4;
+        const int j = (int)(t & 15), g = j >> 2;
+        const uint32_t ns = 4u * (uint32_t)(g & 1);
+        uint32_t n1[2], n2[2];
+        n1[0] = (r.q1.x >> ns) & 0x0f0f0f0fu; n1[1] = (r.q1.y >> ns) & 0x0f0f0f0fu;
+        n2[0] = (r.q2.x >> ns) & 0x0f0f0f0fu; n2[1] = (r.q2.y >> ns) & 0x0f0f0f0fu;
         if constexpr (QT == 13) {
-            const uint2 qh = *reinterpret_cast<const uint2*>(base + 16 + 8 * c);
-            lo[0] |= ((qh.x >> (2 * p)) & 0x01010101u) << 4;
-            hi[0] |= ((qh.x >> (2 * p + 1)) & 0x01010101u) << 4;
-            lo[1] |= ((qh.y >> (2 * p)) & 0x01010101u) << 4;
-            hi[1] |= ((qh.y >> (2 * p + 1)) & 0x01010101u) << 4;
+            n1[0] |= ((r.qh.x >> g) & 0x01010101u) << 4;
+            n1[1] |= ((r.qh.y >> g) & 0x01010101u) << 4;
+            n2[0] |= ((r.qh.x >> (g + 4)) & 0x01010101u) << 4;
+            n2[1] |= ((r.qh.y >> (g + 4)) & 0x01010101u) << 4;
         }
-        uint32_t scA, mA, scB, mB;
-        scale_min(hdr.y, hdr.z, hdr.w, 2 * p, scA, mA);
-        scale_min(hdr.y, hdr.z, hdr.w, 2 * p + 1, scB, mB);
-        const int64_t eA = sb * 256 + 64 * p + 8 * c, eB = eA + 32;
+        const uint32_t a = byte_of(r.hdr.y, g), b = byte_of(r.hdr.z, g), cc = byte_of(r.hdr.w, g);
+        const uint32_t sc1 = a & 63u, m1 = b & 63u;                                   // sub-block g
+        const uint32_t sc2 = (cc & 0xfu) | ((a >> 2) & 0x30u), m2 = (cc >> 4) | ((b >> 2) & 0x30u);  // 4 + g
+        const uint32_t e1 = sb * 256 + 8 * j, e2 = e1 + 128;
         if constexpr (MID == WF_F16) {
-            const h2 dd = as_h2(hdr.x);                         // (d, dmin)
-            h2 smA, smB;
-            smA[0] = (_Float16)scA; smA[1] = (_Float16)mA;
-            smB[0] = (_Float16)scB; smB[1] = (_Float16)mB;
-            const h2 pA = dd * smA, pB = dd * smB;              // (d * sc, dmin * m), each rounded to f16
-            const h2 dsA = lo2(pA), dmA = hi2(pA), dsB = lo2(pB), dmB = hi2(pB);
-            const h2 bias = h2s(-1024.0f);
-            h2 va[4], vb[4];
+            const h2 dd = as_h2(r.hdr.x);                       // (d, dmin)
+            const h2 off = h2s(-1024.0f);
+            // (sc, m) as float16 pairs through the exponent trick, then (d * sc, dmin * m) rounded to f16
+            const h2 p1 = dd * (as_h2(sc1 | (m1 << 16) | 0x64006400u) + off);
+            const h2 p2 = dd * (as_h2(sc2 | (m2 << 16) | 0x64006400u) + off);
+            const h2 ds1 = lo2(p1), dm1 = hi2(p1), ds2 = lo2(p2), dm2 = hi2(p2);
+            h2 v1[4], v2[4];
 #pragma unroll
             for (int w = 0; w < 2; w++) {
-                va[2 * w] = dsA * (biased_lo(lo[w]) + bias) - dmA;
-                va[2 * w + 1] = dsA * (biased_hi(lo[w]) + bias) - dmA;
-                vb[2 * w] = dsB * (biased_lo(hi[w]) + bias) - dmB;
-                vb[2 * w + 1] = dsB * (biased_hi(hi[w]) + bias) - dmB;
+                v1[2 * w] = ds1 * (biased_lo(n1[w]) + off) - dm1;
+                v1[2 * w + 1] = ds1 * (biased_hi(n1[w]) + off) - dm1;
+                v2[2 * w] = ds2 * (biased_lo(n2[w]) + off) - dm2;
+                v2[2 * w + 1] = ds2 * (biased_hi(n2[w]) + off) - dm2;
             }
-            store8h<OUT>(out, eA, va);
-            store8h<OUT>(out, eB, vb);
+            store8h<OUT>(out, e1, v1);
+            store8h<OUT>(out, e2, v2);
         } else {
-            const float d = round_to<MID>(f16_bits_to_f32(hdr.x & 0xffffu));
-            const float dmin = round_to<MID>(f16_bits_to_f32(hdr.x >> 16));
-            const float dsA = round_to<MID>(d * (float)scA), dmA = round_to<MID>(dmin * (float)mA);
-            const float dsB = round_to<MID>(d * (float)scB), dmB = round_to<MID>(dmin * (float)mB);
-            float va[8], vb[8];
+            const float d = round_to<MID>(f16_bits_to_f32(r.hdr.x & 0xffffu));
+            const float dmin = round_to<MID>(f16_bits_to_f32(r.hdr.x >> 16));
+            const float ds1 = round_to<MID>(d * (float)sc1), dm1 = round_to<MID>(dmin * (float)m1);
+            const float ds2 = round_to<MID>(d * (float)sc2), dm2 = round_to<MID>(dmin * (float)m2);
+            float v1[8], v2[8];
 #pragma unroll
             for (int w = 0; w < 2; w++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    va[4 * w + i] = round_to<MID>(round_to<MID>(dsA * (float)byte_of(lo[w], i)) - dmA);
-                    vb[4 * w + i] = round_to<MID>(round_to<MID>(dsB * (float)byte_of(hi[w], i)) - dmB);
+                    v1[4 * w + i] = round_to<MID>(round_to<MID>(ds1 * (float)byte_of(n1[w], i)) - dm1);
+                    v2[4 * w + i] = round_to<MID>(round_to<MID>(ds2 * (float)byte_of(n2[w], i)) - dm2);
                 }
-            store8<OUT>(out, eA, va);
-            store8<OUT>(out, eB, vb);
+            store8<OUT>(out, e1, v1);
+            store8<OUT>(out, e2, v2);
         }
     }
-}
+};
 
 // ------------------------------------------------------------------------------------------------- Q6_K
-// 210 B: ql[128] @0, qh[64] @128, int8 scales[16] @192, d @208. Lane j (16 per super-block): half h = j / 8,
-// chunk c = j % 8 -> ql bytes [64h + 8c, +8): low nibbles are values 128h + 8c + i, high nibbles 128h + 64 + 8c + i;
-// their 2 high bits come from qh[32h + 8(c % 4) + i] at shift 2(c / 4) and 2(2 + c / 4); scales 8h + c / 2 and
-// 8h + 4 + c / 2. x = MID(MID(MID(d) * sc) * q), q = (lo | hi << 4) - 32, :213-224.
-__device__ __forceinline__ uint2 load8_a2(const uint8_t* base, int64_t o) {
+// 210 B: ql[128] @0, qh[64] @128, int8 scales[16] @192, d @208. Lane-item j (16 per super-block): half h = j / 8,
+// chunk c = j % 8 -> ql bytes [64h + 8c, +8): low nibbles are values 128h + 8c + i, high nibbles
+// 128h + 64 + 8c + i; their 2 high bits come from qh[32h + 8(c % 4) + i] at shift 2(c / 4) and 2(2 + c / 4);
+// scales 8h + c / 2 and 8h + 4 + c / 2. x = MID(MID(MID(d) * sc) * q), q = (lo | hi << 4) - 32, :213-224.
+__device__ __forceinline__ uint2 load8_a2(const uint8_t* base, uint32_t o) {
     // 8 bytes at byte offset o (o even): reads [o, o + 8) plus, when o is 2 (mod 4), the 2 bytes before o (the
     // end of the previous block, or of this block's earlier field; never before the buffer, since block 0 starts
     // dword-aligned)
-    const int64_t a = o & ~(int64_t)3;
-    const uint32_t sh = (uint32_t)(o & 3) * 8u;
+    const uint32_t a = o & ~3u;
+    const uint32_t sh = (o & 3) * 8u;
     const uint32_t* wp = reinterpret_cast<const uint32_t*>(base + a);
     const uint32_t w0 = wp[0], w1 = wp[1];
     const uint32_t w2 = *reinterpret_cast<const uint16_t*>(base + a + (sh ? 8 : 6));
@@ -211,30 +272,36 @@ __device__ __forceinline__ uint2 load8_a2(const uint8_t* base, int64_t o) {
 }
 
 template <int MID, int OUT>
-__global__ __launch_bounds__(256) void deq_q6_k(const uint8_t* __restrict__ src, void* __restrict__ out,
-                                                int64_t nlanes) {
-    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < nlanes;
-         t += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t sb = t >> 4;
+struct Q6_K {
+    static constexpr int LANES_PER_BLOCK = 16, TS = 210, PER = 256, OUT_BYTES = OUT == WF_F32 ? 4 : 2;
+    struct Raw { uint2 ql, qh; uint32_t sl, sh, d; };
+    static __device__ __forceinline__ Raw load(const uint8_t* src, uint32_t t) {
+        const uint32_t sb = t >> 4;
         const int j = (int)(t & 15), h = j >> 3, c = j & 7;
-        const int64_t b0 = sb * 210;
-        const uint2 ql = load8_a2(src, b0 + 64 * h + 8 * c);
-        const uint2 qh = load8_a2(src, b0 + 128 + 32 * h + 8 * (c & 3));
-        const uint32_t sl = src[b0 + 192 + 8 * h + (c >> 1)];
-        const uint32_t shv = src[b0 + 192 + 8 * h + 4 + (c >> 1)];
-        const uint32_t dbits = *reinterpret_cast<const uint16_t*>(src + b0 + 208);
+        const uint32_t b0 = sb * 210;
+        Raw r;
+        r.ql = load8_a2(src, b0 + 64 * h + 8 * c);
+        r.qh = load8_a2(src, b0 + 128 + 32 * h + 8 * (c & 3));
+        r.sl = src[b0 + 192 + 8 * h + (c >> 1)];
+        r.sh = src[b0 + 192 + 8 * h + 4 + (c >> 1)];
+        r.d = *reinterpret_cast<const uint16_t*>(src + b0 + 208);
+        return r;
+    }
+    static __device__ __forceinline__ void emit(void* out, uint32_t t, const Raw& r) {
+        const uint32_t sb = t >> 4;
+        const int j = (int)(t & 15), h = j >> 3, c = j & 7;
         const uint32_t s1 = 2u * (uint32_t)(c >> 2), s2 = s1 + 4u;
         uint32_t lo[2], hi[2];   // 6-bit codes 0..63, one per byte
-        lo[0] = (ql.x & 0x0f0f0f0fu) | (((qh.x >> s1) & 0x03030303u) << 4);
-        hi[0] = ((ql.x >> 4) & 0x0f0f0f0fu) | (((qh.x >> s2) & 0x03030303u) << 4);
-        lo[1] = (ql.y & 0x0f0f0f0fu) | (((qh.y >> s1) & 0x03030303u) << 4);
-        hi[1] = ((ql.y >> 4) & 0x0f0f0f0fu) | (((qh.y >> s2) & 0x03030303u) << 4);
-        const int64_t eA = sb * 256 + 128 * h + 8 * c, eB = eA + 64;
+        lo[0] = (r.ql.x & 0x0f0f0f0fu) | (((r.qh.x >> s1) & 0x03030303u) << 4);
+        hi[0] = ((r.ql.x >> 4) & 0x0f0f0f0fu) | (((r.qh.x >> s2) & 0x03030303u) << 4);
+        lo[1] = (r.ql.y & 0x0f0f0f0fu) | (((r.qh.y >> s1) & 0x03030303u) << 4);
+        hi[1] = ((r.ql.y >> 4) & 0x0f0f0f0fu) | (((r.qh.y >> s2) & 0x03030303u) << 4);
+        const uint32_t eA = sb * 256 + 128 * h + 8 * c, eB = eA + 64;
         if constexpr (MID == WF_F16) {
-            const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)dbits);
+            const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)r.d);
             h2 dsc;
-            dsc[0] = (_Float16)(float)(int8_t)sl;
-            dsc[1] = (_Float16)(float)(int8_t)shv;
+            dsc[0] = (_Float16)(float)(int8_t)r.sl;
+            dsc[1] = (_Float16)(float)(int8_t)r.sh;
             h2 dd; dd[0] = d; dd[1] = d;
             const h2 pd = dd * dsc;                              // (d * sc_lo, d * sc_hi), rounded to f16
             const h2 dA = lo2(pd), dB = hi2(pd);
@@ -250,8 +317,8 @@ __global__ __launch_bounds__(256) void deq_q6_k(const uint8_t* __restrict__ src,
             store8h<OUT>(out, eA, va);
             store8h<OUT>(out, eB, vb);
         } else {
-            const float d = round_to<MID>(f16_bits_to_f32(dbits));
-            const float dA = round_to<MID>(d * (float)(int8_t)sl), dB = round_to<MID>(d * (float)(int8_t)shv);
+            const float d = round_to<MID>(f16_bits_to_f32(r.d));
+            const float dA = round_to<MID>(d * (float)(int8_t)r.sl), dB = round_to<MID>(d * (float)(int8_t)r.sh);
             float va[8], vb[8];
 #pragma unroll
             for (int w = 0; w < 2; w++)
@@ -264,7 +331,7 @@ __global__ __launch_bounds__(256) void deq_q6_k(const uint8_t* __restrict__ src,
             store8<OUT>(out, eB, vb);
         }
     }
-}
+};
 
 // ----------------------------------------------------------------------------- other formats (byte gathers)
 // The legacy formats Q4_0 / Q4_1 / Q5_0 / Q5_1 and the K-quants Q2_K / Q3_K: one lane per 8 values, the
@@ -334,21 +401,30 @@ struct Launch {
     dim3 grid;
 };
 
+// grid of the byte-gather kernels (grid-stride loops: at most 2^20 workgroups)
 static Launch plan(int64_t nlanes) {
-    // one lane-iteration per thread up to 2^20 workgroups; beyond that the kernels loop
     int64_t wgs = (nlanes + 255) / 256;
     if (wgs > (1 << 20)) wgs = 1 << 20;
     if (wgs < 1) wgs = 1;
     return {nlanes, dim3((unsigned)wgs)};
 }
 
+// grid of the tiled kernels: one workgroup per tile of DEQ_ITEMS * 256 lane-items, every tile launched (no loop);
+// wf_dequant bounds the value count so that this fits gridDim.x
+template <typename F>
+static void launch_items(const uint8_t* src, void* out, int64_t nblocks, hipStream_t s) {
+    const int64_t nlanes = nblocks * F::LANES_PER_BLOCK;
+    const int64_t wgs = (nlanes + 256LL * DEQ_ITEMS - 1) / (256LL * DEQ_ITEMS);
+    deq_items<F><<<dim3((unsigned)wgs), 256, 0, s>>>(src, out, nlanes);
+}
+
 template <int MID, int OUT>
 static void launch_fmt(int qtype, const uint8_t* src, void* out, int64_t nblocks, hipStream_t s) {
     switch (qtype) {
-    case 8: { Launch L = plan(nblocks * 4); deq_q8_0<MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
-    case 12: { Launch L = plan(nblocks * 16); deq_q45_k<12, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
-    case 13: { Launch L = plan(nblocks * 16); deq_q45_k<13, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
-    case 14: { Launch L = plan(nblocks * 16); deq_q6_k<MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
+    case 8: launch_items<Q8_0<MID, OUT>>(src, out, nblocks, s); break;
+    case 12: launch_items<Q45_K<12, MID, OUT>>(src, out, nblocks, s); break;
+    case 13: launch_items<Q45_K<13, MID, OUT>>(src, out, nblocks, s); break;
+    case 14: launch_items<Q6_K<MID, OUT>>(src, out, nblocks, s); break;
     case 2: { Launch L = plan(nblocks * 4); deq_gather<2, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
     case 3: { Launch L = plan(nblocks * 4); deq_gather<3, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
     case 6: { Launch L = plan(nblocks * 4); deq_gather<6, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
@@ -406,6 +482,10 @@ extern "C" int wf_dequant(const void* src, int64_t src_bytes, int qtype, int mid
         return WF_EUNSUPPORTED;
     }
     if (n_values == 0) return WF_OK;
+    if (n_values > (int64_t)1 << 40) {   // keeps every tiled launch under 2^31 workgroups
+        set_error("wf_dequant: %lld values is beyond this build's limit of 2^40", (long long)n_values);
+        return WF_EUNSUPPORTED;
+    }
     if (!src || !out) { set_error("wf_dequant: null pointer"); return WF_EINVAL; }
     if (!aligned(src, 16) || !aligned(out, 16)) {
         set_error("wf_dequant: src and out must be 16-byte aligned");
