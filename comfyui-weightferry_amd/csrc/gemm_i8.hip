@@ -1,0 +1,208 @@
+// Int8 W8A8 linear for gfx950: out[m, n] = OUT((float(acc) * xs[m]) * ws[n] (+ bias[n])), acc = sum_k xq[m, k] *
+// wq[n, k] exactly in int32 -- the role of kitchen's cutlass_int8_dequant (enhancers/fused_int8.py:191-206).
+//
+// Tiling: a 256-thread workgroup computes a BM x BN tile with 2 x 2 waves; a wave owns WM x WN 32x32 tiles of
+// v_mfma_i32_32x32x32_i8 (64 lanes x 16 int8 per operand, 16 int32 accumulators per lane). K advances in stages
+// of 128 bytes: each stage of A (xq rows) and B (wq rows, K-major like A) is loaded from global memory into
+// registers one stage ahead and written to a double-buffered LDS tile. Rows are 128 bytes = 8 chunks of 16 bytes;
+// chunk c of row r sits at chunk slot c ^ ((r >> 1) & 7), so the 16 lanes of each quarter-wave hit 16 different
+// 16-byte bank groups both when a stage is written and when 32 rows' fragments are read.
+//
+// Operand layout (both operands the same): lane l of a 32x32x32 fragment holds 16 bytes of row l % 32 at K offset
+// 16 * (l / 32) of the 32-wide K step. Result layout: lane l, register i holds row 8 (i / 4) + 4 (l / 32) + i % 4,
+// column l % 32 of the 32x32 tile.
+//
+// Tile order is XCD-aware: workgroup w runs on XCD w % 8, so consecutive tile indices are dealt to one XCD's
+// workgroups and that XCD's L2 sees neighbouring tiles (they share A rows / B rows); within the order, tiles are
+// grouped GROUP_M tile-rows at a time.
+
+#include "wf_common.h"
+
+namespace wf {
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBK = 128;        // K bytes per stage
+constexpr int kGroupM = 8;      // tile-rows per group of the tile order
+
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+
+__device__ __forceinline__ float to_f32_out(const void* p, int64_t i, int dt) {
+    if (dt == WF_BF16) return __uint_as_float((uint32_t)static_cast<const uint16_t*>(p)[i] << 16);
+    if (dt == WF_F16) return (float)__builtin_bit_cast(_Float16, static_cast<const uint16_t*>(p)[i]);
+    return static_cast<const float*>(p)[i];
+}
+
+// tile index of workgroup w among T tiles (XCD-aware), then grouped row-major order over (tm, tn)
+__device__ __forceinline__ void tile_of(int w, int T, int ntm, int ntn, int& tm, int& tn) {
+    int L = w;
+    if ((T & 7) == 0) L = (w & 7) * (T >> 3) + (w >> 3);
+    const int per_group = kGroupM * ntn;
+    const int group = L / per_group;
+    const int first_m = group * kGroupM;
+    const int gm = min(ntm - first_m, kGroupM);
+    const int in = L - group * per_group;
+    tm = first_m + in % gm;
+    tn = in / gm;
+}
+
+template <int WM, int WN, int OUT, bool BIAS>
+__global__ __launch_bounds__(256) void gemm_i8(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
+                                               const float* __restrict__ xs, const float* __restrict__ ws,
+                                               const void* __restrict__ bias, void* __restrict__ out,
+                                               int M, int N, int K) {
+    constexpr int BM = 2 * WM * 32, BN = 2 * WN * 32;
+    constexpr int ACH = BM * 8 / 256, BCH = BN * 8 / 256;     // 16-byte chunks per thread per stage
+    __shared__ uint4 lds[2][(BM + BN) * 8];
+    const int ntm = (M + BM - 1) / BM, ntn = (N + BN - 1) / BN;
+    int tm, tn;
+    tile_of(blockIdx.x, ntm * ntn, ntm, ntn, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int nk = (K + kBK - 1) / kBK;
+
+    uint4 ra[ACH], rb[BCH];
+    auto gload = [&](int kt) {
+        const int k0 = kt * kBK;
+#pragma unroll
+        for (int i = 0; i < ACH; i++) {
+            const int idx = tid + 256 * i, r = idx >> 3, c = idx & 7;
+            const int gm = m0 + r, gk = k0 + 16 * c;
+            ra[i] = (gm < M && gk < K) ? *reinterpret_cast<const uint4*>(A + (int64_t)gm * K + gk)
+                                       : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < BCH; i++) {
+            const int idx = tid + 256 * i, r = idx >> 3, c = idx & 7;
+            const int gn = n0 + r, gk = k0 + 16 * c;
+            rb[i] = (gn < N && gk < K) ? *reinterpret_cast<const uint4*>(B + (int64_t)gn * K + gk)
+                                       : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto lstore = [&](int buf) {
+        uint4* sa = lds[buf];
+        uint4* sb = lds[buf] + BM * 8;
+#pragma unroll
+        for (int i = 0; i < ACH; i++) {
+            const int idx = tid + 256 * i, r = idx >> 3, c = idx & 7;
+            sa[r * 8 + swz(r, c)] = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < BCH; i++) {
+            const int idx = tid + 256 * i, r = idx >> 3, c = idx & 7;
+            sb[r * 8 + swz(r, c)] = rb[i];
+        }
+    };
+
+    i32x16 acc[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int j = 0; j < WN; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0;
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    const int lr = lane & 31, lk = lane >> 5;
+    for (int kt = 0; kt < nk; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) gload(kt + 1);
+        const uint4* sa = lds[cur];
+        const uint4* sb = lds[cur] + BM * 8;
+#pragma unroll
+        for (int ks = 0; ks < kBK / 32; ks++) {
+            const int ch = 2 * ks + lk;
+            i32x4 af[WM], bf[WN];
+#pragma unroll
+            for (int i = 0; i < WM; i++) {
+                const int r = wm * WM * 32 + i * 32 + lr;
+                af[i] = __builtin_bit_cast(i32x4, sa[r * 8 + swz(r, ch)]);
+            }
+#pragma unroll
+            for (int j = 0; j < WN; j++) {
+                const int r = wn * WN * 32 + j * 32 + lr;
+                bf[j] = __builtin_bit_cast(i32x4, sb[r * 8 + swz(r, ch)]);
+            }
+#pragma unroll
+            for (int i = 0; i < WM; i++)
+#pragma unroll
+                for (int j = 0; j < WN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) lstore(cur ^ 1);
+        __syncthreads();
+    }
+
+    // epilogue: (float(acc) * xs[m]) * ws[n] (+ bias[n]), rounded once to OUT
+#pragma unroll
+    for (int j = 0; j < WN; j++) {
+        const int n = n0 + wn * WN * 32 + j * 32 + lr;
+        if (n >= N) continue;
+        const float wsn = ws[n];
+        const float bn = BIAS ? to_f32_out(bias, n, OUT) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < WM; i++) {
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int m = m0 + wm * WM * 32 + i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
+                if (m >= M) continue;
+                float t = ((float)acc[i][j][e] * xs[m]) * wsn;
+                if (BIAS) t = t + bn;
+                const int64_t o = (int64_t)m * N + n;
+                if constexpr (OUT == WF_BF16) {
+                    static_cast<__bf16*>(out)[o] = (__bf16)t;
+                } else {
+                    static_cast<_Float16*>(out)[o] = (_Float16)t;
+                }
+            }
+        }
+    }
+}
+
+template <int WM, int WN, int OUT>
+static void launch_gemm(const int8_t* A, const int8_t* B, const float* xs, const float* ws, const void* bias,
+                        void* out, int M, int N, int K, hipStream_t s) {
+    constexpr int BM = 2 * WM * 32, BN = 2 * WN * 32;
+    const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    if (bias) gemm_i8<WM, WN, OUT, true><<<dim3(tiles), 256, 0, s>>>(A, B, xs, ws, bias, out, M, N, K);
+    else gemm_i8<WM, WN, OUT, false><<<dim3(tiles), 256, 0, s>>>(A, B, xs, ws, bias, out, M, N, K);
+}
+
+template <int OUT>
+static void dispatch(const int8_t* A, const int8_t* B, const float* xs, const float* ws, const void* bias,
+                     void* out, int M, int N, int K, hipStream_t s) {
+    // large outputs: 256 x 256 tiles (4 x 4 MFMA tiles per wave); small ones keep 128 x 128 to fill the chip
+    const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+    if (big_tiles >= 512) launch_gemm<4, 4, OUT>(A, B, xs, ws, bias, out, M, N, K, s);
+    else launch_gemm<2, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, s);
+}
+
+}  // namespace wf
+
+extern "C" int wf_linear_i8(const int8_t* xq, const int8_t* wq, const float* xs, const float* ws, const void* bias,
+                            void* out, int out_dt, int64_t M, int64_t N, int64_t K, void* stream) {
+    using namespace wf;
+    if (M < 0 || N < 0 || K <= 0) { set_error("wf_linear_i8: M, N, K = %lld, %lld, %lld", (long long)M, (long long)N, (long long)K); return WF_EINVAL; }
+    if (M == 0 || N == 0) return WF_OK;
+    if (!xq || !wq || !xs || !ws || !out) { set_error("wf_linear_i8: null pointer"); return WF_EINVAL; }
+    if (out_dt != WF_BF16 && out_dt != WF_F16) { set_error("wf_linear_i8: output dtype %d", out_dt); return WF_EUNSUPPORTED; }
+    if (K % 16 || !aligned(xq, 16) || !aligned(wq, 16)) {
+        set_error("wf_linear_i8: K %% 16 == 0 and 16-byte aligned operands are required");
+        return WF_EUNSUPPORTED;
+    }
+    if (M >= (1LL << 31) || N >= (1LL << 31) || K >= (1LL << 31) || M * N >= (1LL << 62)) {
+        set_error("wf_linear_i8: sizes beyond this build's 32-bit tile indices");
+        return WF_EUNSUPPORTED;
+    }
+    // int32 accumulation is exact when K * 128 * 128 < 2^31
+    if (K > 131071) { set_error("wf_linear_i8: K = %lld would overflow the int32 accumulator", (long long)K); return WF_EUNSUPPORTED; }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (out_dt == WF_BF16) dispatch<WF_BF16>(xq, wq, xs, ws, bias, out, (int)M, (int)N, (int)K, s);
+    else dispatch<WF_F16>(xq, wq, xs, ws, bias, out, (int)M, (int)N, (int)K, s);
+    WF_LAUNCH_CHECK("wf_linear_i8 launch");
+    return WF_OK;
+}

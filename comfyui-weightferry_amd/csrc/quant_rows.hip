@@ -1,0 +1,249 @@
+// Per-row int8 quantisation of bf16 activations for gfx950: the role of the Triton `_quant_row` with PRE_NONE
+// (enhancers/fused_kernels.py:137-174) and of kitchen's quantize_int8_rowwise_convrot64 (enhancers/fused_int8.py:
+// 178-181).
+//
+// Per row r of K values x (bf16):
+//   mode 1 (ConvRot): each 256-group goes through four radix-4 stages of stride 1, 4, 16, 64 -- (a, b, c, d) ->
+//     (a+b+c-d, a+b-c+d, a-b+c+d, -a+b+c+d), every sum left to right in float32 -- then * 0.0625;
+//   mode 0 (plain per-token): y = x.
+//   amax = min(max |y|, 3.38953139e38); scale = max(amax / 127, 1e-30) (stored as float32);
+//   q = clamp(rint(bf16(bf16(y) / bf16(scale))), -128, 127).
+//
+// One wave per row, the row held in registers. ConvRot: a lane loads 16 consecutive values of a 256-group (the
+// two lowest radix-4 digits), runs stages 1 and 4 on them, exchanges through LDS so that it then holds the 16 values
+// that share its two lowest digits (stride 16), and runs stages 16 and 64. The quotient y / s is computed with a
+// correctly rounded reciprocal of s (one IEEE division per row) and one Markstein correction step -- mul, then two
+// fma -- which is the correctly rounded IEEE quotient for every normal result (subnormal quotients round to 0 in the
+// integer anyway). Built without contraction; the fma calls are explicit.
+
+#include "wf_common.h"
+
+namespace wf {
+
+constexpr float kAmaxClamp = 3.38953139e38f;
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// RN(y / s) for the row's finite scale s, given rs = RN(1 / s). An infinite y (a rotation that overflowed)
+// gives y * rs = +-inf, which is the IEEE quotient; the correction step would turn it into NaN (inf - inf).
+__device__ __forceinline__ float div_rn(float y, float s, float rs) {
+    const float q = y * rs;
+    const float rem = __builtin_fmaf(-q, s, y);
+    const float r = __builtin_fmaf(rem, rs, q);
+    return __builtin_isinf(q) ? q : r;
+}
+
+__device__ __forceinline__ int8_t quant1(float y, float sb, float rsb) {
+    float v = __builtin_rintf(round_bf16(div_rn(round_bf16(y), sb, rsb)));
+    v = fminf(fmaxf(v, -128.0f), 127.0f);
+    return (int8_t)(int)v;
+}
+
+struct RowScale {
+    float scale, sb, rsb;
+};
+
+__device__ __forceinline__ RowScale row_scale(float amax) {
+    RowScale r;
+    amax = fminf(amax, kAmaxClamp);
+    r.scale = fmaxf(amax / 127.0f, 1.0e-30f);
+    r.sb = round_bf16(r.scale);
+    r.rsb = 1.0f / r.sb;
+    return r;
+}
+
+// ------------------------------------------------------------------------------------------------ plain rows
+// CPL chunks of 8 values per lane (chunk c of the row at lane + 64 * i): K <= 512 * CPL, K % 8 == 0.
+template <int CPL>
+__global__ __launch_bounds__(256) void quant_plain(const uint16_t* __restrict__ x, int64_t M, int K,
+                                                   int8_t* __restrict__ xq, float* __restrict__ xs) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;                       // whole waves leave together; no block barrier below
+    const uint4* xr = reinterpret_cast<const uint4*>(x + row * K);
+    const int nchunks = K >> 3;
+    uint4 v[CPL];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPL; i++) {
+        const int c = lane + 64 * i;
+        v[i] = c < nchunks ? xr[c] : make_uint4(0, 0, 0, 0);
+        const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+            amax = fmaxf(amax, fabsf(bf16_bits_to_f32(w[h] & 0xffffu)));
+            amax = fmaxf(amax, fabsf(bf16_bits_to_f32(w[h] >> 16)));
+        }
+    }
+    const RowScale rs = row_scale(wave_max(amax));
+    if (lane == 0) xs[row] = rs.scale;
+    uint2* qr = reinterpret_cast<uint2*>(xq + row * K);
+#pragma unroll
+    for (int i = 0; i < CPL; i++) {
+        const int c = lane + 64 * i;
+        if (c >= nchunks) continue;
+        const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+        uint32_t b[2] = {0, 0};
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+            const uint32_t lo = (uint8_t)quant1(bf16_bits_to_f32(w[h] & 0xffffu), rs.sb, rs.rsb);
+            const uint32_t hi = (uint8_t)quant1(bf16_bits_to_f32(w[h] >> 16), rs.sb, rs.rsb);
+            b[h >> 1] |= (lo | (hi << 8)) << (16 * (h & 1));
+        }
+        qr[c] = make_uint2(b[0], b[1]);
+    }
+}
+
+// --------------------------------------------------------------------------------------------- ConvRot rows
+// radix-4 stage on 4 values (a, b, c, d) in place, sums left to right (enhancers/fused_kernels.py:65-81)
+__device__ __forceinline__ void h4(float& a, float& b, float& c, float& d) {
+    const float y0 = ((a + b) + c) - d;
+    const float y1 = ((a + b) - c) + d;
+    const float y2 = ((a - b) + c) + d;
+    const float y3 = ((-a + b) + c) + d;
+    a = y0; b = y1; c = y2; d = y3;
+}
+
+// LDS slot of element i (0..255) of group g of a wave's 4-group window: 17 floats per 16 elements (conflict-free
+// for both the contiguous and the stride-16 access)
+__device__ __forceinline__ int slot(int g, int i) { return g * 272 + i + (i >> 4); }
+
+// NP passes of 4 groups (1024 values) per wave: K <= 1024 * NP, K % 256 == 0. Lane t of a pass owns group
+// 4p + t / 16, position tl = t % 16.
+template <int NP>
+__global__ __launch_bounds__(256) void quant_convrot(const uint16_t* __restrict__ x, int64_t M, int K,
+                                                     int8_t* __restrict__ xq, float* __restrict__ xs) {
+    __shared__ float stage[4][4 * 272];          // per wave: one 4-group window
+    __shared__ uint32_t qbytes[4][NP * 256];     // per wave: the int8 row, 4 bytes a word
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+    if (row >= M) return;                        // whole waves leave together; only wave barriers below
+    const int G = K >> 8;                        // groups in the row
+    const int gl = lane >> 4, tl = lane & 15;
+    float* st = stage[wave];
+    float y[NP][16];
+    float amax = 0.0f;
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        const int g = 4 * p + gl;
+        const bool live = g < G;
+        // 16 consecutive values [16 tl, 16 tl + 16) of group g: digits k0 (stride 1) and k1 (stride 4)
+        float v[16];
+        if (live) {
+            const uint4* src = reinterpret_cast<const uint4*>(x + row * K + g * 256 + 16 * tl);
+            const uint4 a = src[0], b = src[1];
+            const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int h = 0; h < 8; h++) {
+                v[2 * h] = bf16_bits_to_f32(w[h] & 0xffffu);
+                v[2 * h + 1] = bf16_bits_to_f32(w[h] >> 16);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) v[i] = 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) h4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);   // stride 1
+#pragma unroll
+        for (int q = 0; q < 4; q++) h4(v[q], v[q + 4], v[q + 8], v[q + 12]);                  // stride 4
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int i = 0; i < 16; i++) st[slot(gl, 16 * tl + i)] = v[i];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_s_waitcnt(0);           // LDS writes of this wave done before the reads below
+        __builtin_amdgcn_wave_barrier();
+        // now the 16 values i = tl + 16 m (m = k2 + 4 k3) of group g
+#pragma unroll
+        for (int m = 0; m < 16; m++) v[m] = st[slot(gl, tl + 16 * m)];
+#pragma unroll
+        for (int q = 0; q < 4; q++) h4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);   // stride 16
+#pragma unroll
+        for (int q = 0; q < 4; q++) h4(v[q], v[q + 4], v[q + 8], v[q + 12]);                  // stride 64
+#pragma unroll
+        for (int m = 0; m < 16; m++) {
+            y[p][m] = v[m] * 0.0625f;
+            if (live) amax = fmaxf(amax, fabsf(y[p][m]));
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    const RowScale rs = row_scale(wave_max(amax));
+    if (lane == 0) xs[row] = rs.scale;
+    // quantise, put each byte at its row position in LDS, then write the row with 16-byte stores
+    uint8_t* qb = reinterpret_cast<uint8_t*>(qbytes[wave]);
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        const int g = 4 * p + gl;
+        if (g >= G) continue;
+#pragma unroll
+        for (int m = 0; m < 16; m++) qb[g * 256 + tl + 16 * m] = (uint8_t)quant1(y[p][m], rs.sb, rs.rsb);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    const uint4* qs = reinterpret_cast<const uint4*>(qbytes[wave]);
+    uint4* dst = reinterpret_cast<uint4*>(xq + row * K);
+    for (int c = lane; c < (K >> 4); c += 64) dst[c] = qs[c];
+}
+
+template <int CPL>
+static void launch_plain(const uint16_t* x, int64_t M, int K, int8_t* xq, float* xs, hipStream_t s) {
+    quant_plain<CPL><<<dim3((unsigned)((M + 3) / 4)), 256, 0, s>>>(x, M, K, xq, xs);
+}
+
+template <int NP>
+static void launch_convrot(const uint16_t* x, int64_t M, int K, int8_t* xq, float* xs, hipStream_t s) {
+    quant_convrot<NP><<<dim3((unsigned)((M + 3) / 4)), 256, 0, s>>>(x, M, K, xq, xs);
+}
+
+}  // namespace wf
+
+extern "C" int wf_quant_rows_i8(const void* x_bf16, int64_t M, int64_t K, int mode, int8_t* xq, float* xs,
+                                void* stream) {
+    using namespace wf;
+    if (M < 0 || K <= 0) { set_error("wf_quant_rows_i8: M = %lld, K = %lld", (long long)M, (long long)K); return WF_EINVAL; }
+    if (M == 0) return WF_OK;
+    if (!x_bf16 || !xq || !xs) { set_error("wf_quant_rows_i8: null pointer"); return WF_EINVAL; }
+    if (!aligned(x_bf16, 16) || !aligned(xq, 16) || !aligned(xs, 4)) {
+        set_error("wf_quant_rows_i8: x and xq must be 16-byte aligned");
+        return WF_EUNSUPPORTED;
+    }
+    if (M > ((int64_t)1 << 33)) { set_error("wf_quant_rows_i8: M too large"); return WF_EUNSUPPORTED; }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint16_t* xp = static_cast<const uint16_t*>(x_bf16);
+    const int k = (int)K;
+    if (mode == 0) {
+        if (K % 16 || K > 8192) {
+            set_error("wf_quant_rows_i8: plain mode needs K %% 16 == 0 and K <= 8192 (K = %lld)", (long long)K);
+            return WF_EUNSUPPORTED;
+        }
+        const int cpl = (k + 511) / 512;
+        if (cpl <= 2) launch_plain<2>(xp, M, k, xq, xs, s);
+        else if (cpl <= 4) launch_plain<4>(xp, M, k, xq, xs, s);
+        else if (cpl <= 8) launch_plain<8>(xp, M, k, xq, xs, s);
+        else if (cpl <= 10) launch_plain<10>(xp, M, k, xq, xs, s);
+        else launch_plain<16>(xp, M, k, xq, xs, s);
+    } else if (mode == 1) {
+        if (K % 256 || K > 6144) {
+            set_error("wf_quant_rows_i8: ConvRot mode needs K %% 256 == 0 and K <= 6144 (K = %lld)", (long long)K);
+            return WF_EUNSUPPORTED;
+        }
+        const int np = (k + 1023) / 1024;
+        if (np <= 1) launch_convrot<1>(xp, M, k, xq, xs, s);
+        else if (np <= 2) launch_convrot<2>(xp, M, k, xq, xs, s);
+        else if (np <= 3) launch_convrot<3>(xp, M, k, xq, xs, s);
+        else if (np <= 4) launch_convrot<4>(xp, M, k, xq, xs, s);
+        else if (np <= 5) launch_convrot<5>(xp, M, k, xq, xs, s);
+        else launch_convrot<6>(xp, M, k, xq, xs, s);
+    } else {
+        set_error("wf_quant_rows_i8: mode %d", mode);
+        return WF_EUNSUPPORTED;
+    }
+    WF_LAUNCH_CHECK("wf_quant_rows_i8 launch");
+    return WF_OK;
+}

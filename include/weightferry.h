@@ -47,6 +47,21 @@ const char* wf_last_error(void);
 int wf_dequant(const void* src, int64_t src_bytes, int qtype, int mid_dt, int out_dt, void* out, int64_t n_values,
                void* stream);
 
+/* ---------------------------------------------------------------------------------------------- int8 W8A8 path
+ * Per-row int8 quantisation of bf16 activations: replaces the Triton `_quant_row` with PRE_NONE
+ * (enhancers/fused_kernels.py:137-174, launched at enhancers/fused_int8.py:172-176) and kitchen's
+ * quantize_int8_rowwise_convrot64 (enhancers/fused_int8.py:178-181). mode 0: plain per-token (K % 16 == 0,
+ * K <= 8192); mode 1: ConvRot 256-groups (K % 256 == 0, K <= 6144). x: bf16 [M, K] row-major; xq: int8 [M, K];
+ * xs: float32 [M]. x and xq 16-byte aligned. */
+int wf_quant_rows_i8(const void* x_bf16, int64_t M, int64_t K, int mode, int8_t* xq, float* xs, void* stream);
+
+/* out[m, n] = OUT((float(acc[m, n]) * xs[m]) * ws[n] (+ bias[n])), acc = sum_k xq[m, k] * wq[n, k] exactly in
+ * int32: replaces kitchen's cutlass_int8_dequant (enhancers/fused_int8.py:191-206; the reference returns None and
+ * falls back where this returns WF_EUNSUPPORTED). wq is [N, K] (row = output channel); bias (nullable) has dtype
+ * out_dt; out_dt is WF_BF16 or WF_F16. K % 16 == 0, xq / wq 16-byte aligned. */
+int wf_linear_i8(const int8_t* xq, const int8_t* wq, const float* xs, const float* ws, const void* bias, void* out,
+                 int out_dt, int64_t M, int64_t N, int64_t K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,121 @@
+"""GPU parity of the int8 W8A8 path through the C ABI: wf_quant_rows_i8 (plain and ConvRot) and wf_linear_i8,
+bit for bit against the oracle.
+
+Quantiser: bf16 N(0, 1) rows at several widths (incl. the 14B-DiT width 5120), plus zero rows, a row at bf16's
+largest value and rows built to hit rint ties. GEMM: ragged small shapes (tails in M, N and K) against the C oracle,
+and every workload shape (M in {1024, 4096, 16384}, K = 5120, N in {5120, 13824}) on sampled rows against an exact
+float64 accumulator with the epilogue in torch float32 (the same operations as the oracle's epilogue)."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import sub
+from oracle import lib
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t):
+    return t.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def gpu_quant(native, x_bf16, mode):
+    M, K = x_bf16.shape
+    xq = torch.empty((M, K), dtype=torch.int8, device=x_bf16.device)
+    xs = torch.empty(M, dtype=torch.float32, device=x_bf16.device)
+    rc = native.lib().wf_quant_rows_i8(x_bf16.data_ptr(), M, K, mode, xq.data_ptr(), xs.data_ptr(),
+                                       native.stream_of(x_bf16.device))
+    assert rc == 0, native.last_error()
+    torch.cuda.synchronize()
+    return xq, xs
+
+
+def gpu_linear(native, xq, wq, xs, ws, bias=None, out_dtype=torch.bfloat16):
+    M, K = xq.shape
+    N = wq.shape[0]
+    out = torch.empty((M, N), dtype=out_dtype, device=xq.device)
+    code = 1 if out_dtype == torch.bfloat16 else 0
+    rc = native.lib().wf_linear_i8(xq.data_ptr(), wq.data_ptr(), xs.data_ptr(), ws.data_ptr(),
+                                   bias.data_ptr() if bias is not None else None, out.data_ptr(), code, M, N, K,
+                                   native.stream_of(xq.device))
+    assert rc == 0, native.last_error()
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("mode,K", [(0, 512), (0, 5120), (0, 8192), (0, 48), (1, 256), (1, 1280), (1, 5120),
+                                    (1, 6144)])
+def test_quant_rows_random(native, mode, K):
+    g = torch.Generator().manual_seed(99 + K)
+    x = (torch.randn((257, K), generator=g) * 2).to(torch.bfloat16)
+    xq, xs = gpu_quant(native, x.cuda(), mode)
+    rq, rs = lib.quant_rows(x.view(torch.int16).numpy().view(np.uint16), mode)
+    assert np.array_equal(xs.cpu().numpy().view(np.uint32), rs.view(np.uint32))
+    assert np.array_equal(xq.cpu().numpy(), rq)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_quant_rows_edges(native, mode):
+    K = 512
+    rows = np.zeros((6, K), dtype=np.float32)
+    rows[1, 0] = 3.3895313892515355e38                     # amax clamp
+    rows[1, 1:5] = [-1e38, 1e-38, -7.0, 2.5]
+    rows[2, :8] = [127, 2.5, 3.5, -2.5, -3.5, 0.5, -0.5, 1.5]   # ties in plain mode
+    rows[3] = np.linspace(-1e-20, 1e-20, K)                # tiny values: scale from amax / 127
+    rows[4, ::7] = 1.0
+    rows[5] = -np.arange(K) * 0.01
+    x = torch.from_numpy(rows).to(torch.bfloat16)
+    xq, xs = gpu_quant(native, x.cuda(), mode)
+    rq, rs = lib.quant_rows(x.view(torch.int16).numpy().view(np.uint16), mode)
+    assert np.array_equal(xs.cpu().numpy().view(np.uint32), rs.view(np.uint32))
+    assert np.array_equal(xq.cpu().numpy(), rq)
+
+
+def _rand_i8(g, shape):
+    return torch.randint(-128, 128, shape, generator=g, dtype=torch.int64).to(torch.int8)
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 64, 128), (77, 93, 256), (130, 258, 5120), (300, 1000, 208),
+                                   (512, 640, 1024)])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+def test_linear_small_against_oracle(native, M, N, K, out_dtype):
+    g = torch.Generator().manual_seed(M * 7 + N)
+    xq, wq = _rand_i8(g, (M, K)), _rand_i8(g, (N, K))
+    xs = torch.rand(M, generator=g) * 0.05 + 1e-3
+    ws = torch.rand(N, generator=g) * 0.002 + 1e-5
+    out = gpu_linear(native, xq.cuda(), wq.cuda(), xs.cuda(), ws.cuda(), out_dtype=out_dtype)
+    dt = lib.BF16 if out_dtype == torch.bfloat16 else lib.F16
+    ref = lib.linear_i8(xq.numpy(), wq.numpy(), xs.numpy(), ws.numpy(), out_dt=dt)
+    got = _bits(out)
+    bad = np.argwhere(got != ref)
+    assert bad.size == 0, f"{len(bad)} mismatches, first (m, n): {bad[:6].tolist()}"
+
+
+def test_linear_bias(native):
+    g = torch.Generator().manual_seed(5)
+    M, N, K = 96, 160, 512
+    xq, wq = _rand_i8(g, (M, K)), _rand_i8(g, (N, K))
+    xs, ws = torch.rand(M, generator=g) * 0.05, torch.rand(N, generator=g) * 0.002
+    bias = torch.randn(N, generator=g).to(torch.bfloat16)
+    out = gpu_linear(native, xq.cuda(), wq.cuda(), xs.cuda(), ws.cuda(), bias=bias.cuda())
+    ref = lib.linear_i8(xq.numpy(), wq.numpy(), xs.numpy(), ws.numpy(), out_dt=lib.BF16,
+                        bias=bias.view(torch.int16).numpy().view(np.uint16))
+    assert np.array_equal(_bits(out), ref)
+
+
+@pytest.mark.parametrize("M", [1024, 4096, 16384])
+@pytest.mark.parametrize("N", [5120, 13824])
+def test_linear_workload_shapes_sampled_rows(native, M, N):
+    K = 5120
+    g = torch.Generator().manual_seed(M + N)
+    xq = _rand_i8(g, (M, K))
+    wq = _rand_i8(g, (N, K))
+    xs = torch.rand(M, generator=g) * 0.05 + 1e-3
+    ws = torch.rand(N, generator=g) * 0.002 + 1e-5
+    out = gpu_linear(native, xq.cuda(), wq.cuda(), xs.cuda(), ws.cuda())
+    rows = torch.unique(torch.cat([torch.arange(0, M, max(1, M // 48)), torch.tensor([M - 1, 31, 32, 255, 256])]))
+    rows = rows[rows < M]
+    acc = xq[rows].double() @ wq.double().T                       # exact: |acc| < 2^31
+    ref = ((acc.float() * xs[rows, None]) * ws[None, :]).to(torch.bfloat16)
+    got = out[rows.cuda()].cpu()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
