@@ -27,6 +27,20 @@ EXPORTS = {
     "wf_dequant": (_int, [_p, _i64, _int, _int, _int, _p, _i64, _p]),
     "wf_quant_rows_i8": (_int, [_p, _i64, _i64, _int, _p, _p, _p]),
     "wf_linear_i8": (_int, [_p, _p, _p, _p, _p, _p, _int, _i64, _i64, _i64, _p]),
+    "wf_linear_gguf": (_int, [_p, _i64, _i64, _p, _i64, _int, _i64, _p, _p, _int, _p]),
+    "wf_host_alloc": (_int, [_sz, ctypes.POINTER(ctypes.c_void_p)]),
+    "wf_host_free": (_int, [_p]),
+    "wf_h2d_async": (_int, [_p, _p, _sz, _p]),
+    "wf_stream_create": (_int, [ctypes.POINTER(ctypes.c_void_p)]),
+    "wf_stream_destroy": (_int, [_p]),
+    "wf_stream_synchronize": (_int, [_p]),
+    "wf_event_create": (_int, [ctypes.POINTER(ctypes.c_void_p), _int]),
+    "wf_event_destroy": (_int, [_p]),
+    "wf_event_record": (_int, [_p, _p]),
+    "wf_stream_wait_event": (_int, [_p, _p]),
+    "wf_event_query": (_int, [_p]),
+    "wf_event_synchronize": (_int, [_p]),
+    "wf_event_elapsed_ms": (_int, [_p, _p, ctypes.POINTER(ctypes.c_float)]),
 }
 
 _lib = None
@@ -84,6 +98,66 @@ def check(rc, what):
     if rc == EUNSUPPORTED:
         return False
     raise NativeError(f"{what} failed ({rc}): {last_error()}")
+
+
+def call(fn_name, *args):
+    """lib().<fn_name>(*args), raising NativeError on any non-zero return."""
+    rc = getattr(lib(), fn_name)(*args)
+    if rc != OK:
+        raise NativeError(f"{fn_name} failed ({rc}): {last_error()}")
+    return rc
+
+
+class Stream:
+    """A HIP stream of the library (non-blocking, default priority); .handle is the hipStream_t."""
+
+    def __init__(self):
+        h = ctypes.c_void_p()
+        call("wf_stream_create", ctypes.byref(h))
+        self.handle = h.value
+
+    def synchronize(self):
+        call("wf_stream_synchronize", self.handle)
+
+    def close(self):
+        if self.handle is not None:
+            lib().wf_stream_destroy(self.handle)
+            self.handle = None
+
+
+class Event:
+    """A HIP event of the library; timing=True keeps timestamps for elapsed_ms."""
+
+    def __init__(self, timing=False):
+        h = ctypes.c_void_p()
+        call("wf_event_create", ctypes.byref(h), 1 if timing else 0)
+        self.handle = h.value
+
+    def record(self, stream):
+        call("wf_event_record", self.handle, stream)
+
+    def query(self):
+        rc = lib().wf_event_query(self.handle)
+        if rc < 0:
+            raise NativeError(f"wf_event_query failed ({rc}): {last_error()}")
+        return rc == 0
+
+    def synchronize(self):
+        call("wf_event_synchronize", self.handle)
+
+    def elapsed_ms(self, end):
+        ms = ctypes.c_float()
+        call("wf_event_elapsed_ms", self.handle, end.handle, ctypes.byref(ms))
+        return float(ms.value)
+
+    def close(self):
+        if self.handle is not None:
+            lib().wf_event_destroy(self.handle)
+            self.handle = None
+
+
+def stream_wait(stream, event):
+    call("wf_stream_wait_event", stream, event.handle)
 
 
 def stream_of(device):

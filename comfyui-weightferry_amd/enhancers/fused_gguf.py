@@ -1,0 +1,77 @@
+"""Linear layers whose weight is GGUF K-quant blocks, with the dequantisation inside the GEMM (wf_linear_gguf).
+
+The reference dequantises the weight (enhancers/gguf_dequant.py:296-326, one kernel into a bf16 weight in HBM)
+and ComfyUI-GGUF then runs torch.nn.functional.linear on it. ``linear`` does both in one kernel launch for bf16
+activations and a Q4_K / Q5_K / Q6_K weight, with the same dequantised values (dequant dtype MID, then the layer
+dtype) and float32 accumulation; mode="dequant" keeps the reference's two-step flow (wf_dequant, then F.linear).
+Anything else -- other formats, dtypes, CPU tensors -- returns None from ``fused_linear`` and ``linear`` takes
+the two-step flow."""
+import torch
+
+from .. import _native
+from . import gguf_dequant
+
+_FUSED_TYPES = {12: 144, 13: 176, 14: 210}
+_MID = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+
+def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
+    """y = x @ dequantize(W).T (+ bias) in one kernel, or None when this is not that case."""
+    q = int(qtype) if qtype is not None else None
+    if q not in _FUSED_TYPES or not x.is_cuda or not data.is_cuda or x.dtype != torch.bfloat16:
+        return None
+    n_out, k = int(oshape[0]), int(oshape[1])
+    if x.shape[-1] != k or k % 256 or (bias is not None and (bias.dtype != torch.bfloat16 or bias.numel() != n_out)):
+        return None
+    mid = torch.float16 if mid_dtype is None else mid_dtype
+    if mid not in _MID:
+        return None
+    raw = data.reshape(-1).view(torch.uint8) if data.is_contiguous() else None
+    if raw is None or raw.numel() != n_out * (k // 256) * _FUSED_TYPES[q]:
+        return None
+    x2 = x.reshape(-1, k).contiguous()
+    y = torch.empty((x2.shape[0], n_out), dtype=torch.bfloat16, device=x.device)
+    b = bias.contiguous() if bias is not None else None
+    with torch.cuda.device(x.device):
+        rc = _native.lib().wf_linear_gguf(x2.data_ptr(), x2.shape[0], k, raw.data_ptr(), raw.numel(), q, n_out,
+                                          b.data_ptr() if b is not None else None, y.data_ptr(), _MID[mid],
+                                          _native.stream_of(x.device))
+    if not _native.check(rc, "wf_linear_gguf"):
+        return None
+    return y.reshape(*x.shape[:-1], n_out)
+
+
+def linear(x, data, qtype, oshape, bias=None, mid_dtype=None, mode="fused"):
+    """The layer's forward: the fused kernel when it takes the case (mode "fused"), else the reference's flow --
+    the weight dequantised to x's dtype (wf_dequant), then torch.nn.functional.linear."""
+    if mode == "fused":
+        y = fused_linear(x, data, qtype, oshape, bias, mid_dtype)
+        if y is not None:
+            return y
+    w = gguf_dequant.dequantize(data, qtype, oshape, mid_dtype, x.dtype)
+    if w is None:
+        raise ValueError(f"GGML type {qtype} with shape {tuple(oshape)} is not handled on this path")
+    return torch.nn.functional.linear(x, w, bias)
+
+
+class GGUFLinear(torch.nn.Module):
+    """A linear layer with a GGUF-quantised weight held as raw uint8 blocks (the form ComfyUI-GGUF keeps), so that
+    block streaming moves the quantised bytes."""
+
+    def __init__(self, in_features, out_features, qtype=12, bias=True, mode="fused", mid_dtype=None):
+        super().__init__()
+        q = int(qtype)
+        ts = _FUSED_TYPES.get(q) or gguf_dequant._FORMATS.get(q, (None, None))[1]
+        per = 256 if q in gguf_dequant._KFORMATS else 32
+        if ts is None or in_features % per:
+            raise ValueError(f"GGML type {qtype} with {in_features} inputs")
+        self.in_features, self.out_features, self.qtype = in_features, out_features, q
+        self.mode, self.mid_dtype = mode, mid_dtype
+        self.weight = torch.nn.Parameter(torch.zeros(out_features * in_features // per * ts, dtype=torch.uint8),
+                                         requires_grad=False)
+        self.bias = (torch.nn.Parameter(torch.zeros(out_features, dtype=torch.bfloat16), requires_grad=False)
+                     if bias else None)
+
+    def forward(self, x):
+        return linear(x, self.weight, self.qtype, (self.out_features, self.in_features), self.bias,
+                      self.mid_dtype, self.mode)

@@ -1,0 +1,80 @@
+"""Block streaming of a model's transformer blocks: set-up and the forward wrapper (the roles of
+WeightFerryDiT.apply_streaming and streaming_diffusion_model_wrapper, streaming/dit_node.py:150-455 of the
+reference), for a torch module whose blocks are a ModuleList named blocks / transformer_blocks / layers / block.
+
+The reference attaches these to ComfyUI's ModelPatcher (ON_LOAD callback, diffusion-model wrapper); the host
+application is not part of this path, so here they are plain calls: ``apply_streaming`` captures the blocks and
+installs the hooks, ``StreamedModel.__call__`` runs one forward with streaming active, ``teardown`` undoes it."""
+import torch
+
+from .common import _ACTIVE_ATTR, _STATE_ATTR, _blocks
+from .load_steps import _build_state, _install_block_stream_hooks, _install_first_block_hook
+
+
+class StreamedModel:
+    """A model whose blocks stream from pinned host memory through GPU slots."""
+
+    def __init__(self, dit, state, resident_idx, stream_idx, owner):
+        self.dit = dit
+        self.state = state
+        self.resident_idx = resident_idx
+        self.stream_idx = stream_idx
+        self.owner = owner
+
+    def __call__(self, *args, **kwargs):
+        """One forward with streaming active (streaming_diffusion_model_wrapper, streaming/dit_node.py:414-455):
+        begin_forward, the owner token, and the slot bindings undone afterwards whatever happens."""
+        dit, state = self.dit, self.state
+        setattr(dit, _ACTIVE_ATTR, self.owner)
+        prof = state.profiler
+        try:
+            state.begin_forward()
+            if prof is not None:
+                prof.begin_forward(state.compute_stream())
+            return dit(*args, **kwargs)
+        finally:
+            if prof is not None:
+                prof.end_forward(state.compute_stream())
+            setattr(dit, _ACTIVE_ATTR, None)
+            state.restore_rest_binding()
+
+    def profile_summary(self):
+        return self.state.profile_summary()
+
+    def teardown(self, device=None):
+        """Move the streamed blocks' parameters back to ``device`` (default: the slots' device), release the pinned
+        buffers and slots."""
+        state = self.state
+        dev = torch.device(device) if device is not None else state.device
+        state.close()
+        for blk in state.streaming_blocks:
+            for p in blk.parameters():
+                p.data = p.data.to(dev, copy=True)
+        for h in getattr(state, "holders", []):
+            h.release()
+        state.slot_flats = []
+        state.slot_views = []
+        if getattr(self.dit, _STATE_ATTR, None) is state:
+            delattr(self.dit, _STATE_ATTR)
+
+
+def apply_streaming(dit, device="cuda", resident_blocks=0, prefetch_slots=2, pin_memory=True, profile=None):
+    """Stream all but the first ``resident_blocks`` blocks of ``dit`` (which stay where they are, on ``device``)
+    through ``prefetch_slots`` (>= 2) GPU slots. The reference keeps block 0 resident by default
+    (streaming/dit_node.py:237-267); here resident_blocks = 0 streams every block."""
+    blocks = list(_blocks(dit))
+    if not blocks:
+        raise ValueError("the model has no block list (blocks / transformer_blocks / layers / block)")
+    device = torch.device(device)
+    resident_idx = list(range(min(resident_blocks, len(blocks))))
+    stream_idx = list(range(len(resident_idx), len(blocks)))
+    if not stream_idx:
+        raise ValueError("no block left to stream")
+    for i in resident_idx:
+        blocks[i].to(device)
+    owner = object()
+    state = _build_state(owner, device, [blocks[i] for i in stream_idx], prefetch_slots, pin_memory, profile)
+    _install_first_block_hook(dit, blocks[0], state, owner)
+    _install_block_stream_hooks(dit, state, owner)
+    setattr(dit, _STATE_ATTR, state)
+    return StreamedModel(dit, state, resident_idx, stream_idx, owner)

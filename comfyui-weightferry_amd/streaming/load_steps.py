@@ -1,0 +1,140 @@
+"""Load-time steps of block streaming: capture of the streamed blocks into exact-size pinned host flats, the GPU
+slots and the state, and the forward hooks -- the reference's streaming/load_steps.py on the direct path
+(_capture_streamed_blocks :1152-1274, _build_state :719-766, _install_first_block_hook :315-337,
+_install_block_stream_hooks :451-522)."""
+import time
+
+import torch
+
+from ..core import env as _env
+from ..core.tiers.pinned import PinnedHost
+from .common import _ACTIVE_ATTR, _flat_layout, _specs, _views
+from .profiler import _StreamProfiler
+from .state import _StreamState
+
+
+def _check_block_layouts(blocks):
+    """Every streamed block must have the same parameter layout (one slot layout serves them all)."""
+    specs = _specs(blocks[0])
+    for i, blk in enumerate(blocks[1:], 1):
+        if _specs(blk) != specs:
+            raise ValueError(f"block {i} has a different parameter layout than block 0")
+    return specs
+
+
+def _capture_streamed_blocks(blocks, specs, offsets, flat_bytes, pin_memory=True):
+    """Copy each streamed block's parameters into its own flat host buffer (pinned when pin_memory); returns
+    (holders, host_flats, host_views)."""
+    holders, host_flats, host_views = [], [], []
+    for blk in blocks:
+        if pin_memory:
+            holder = PinnedHost(flat_bytes)
+            holders.append(holder)
+            flat = holder.tensor
+        else:
+            flat = torch.empty(flat_bytes, dtype=torch.uint8)
+        flat.zero_()
+        views = _views(flat, specs, offsets)
+        for p, v in zip(blk.parameters(), views):
+            v.copy_(p.data)
+        host_flats.append(flat)
+        host_views.append(views)
+    return holders, host_flats, host_views
+
+
+def _num_slots(prefetch_slots):
+    n = max(2, int(prefetch_slots))
+    if _env.get("WEIGHTFERRY_SLOTS"):
+        n = max(2, int(_env.get("WEIGHTFERRY_SLOTS")))
+    return n
+
+
+def _build_state(owner, device, blocks, prefetch_slots=2, pin_memory=True, profile=None):
+    """Capture + slots + state for the given streamed blocks; the blocks' parameters end up bound to their host
+    views (their "rest" tensors) until a forward binds them to a slot."""
+    specs = _check_block_layouts(blocks)
+    offsets, flat_bytes = _flat_layout(specs)
+    holders, host_flats, host_views = _capture_streamed_blocks(blocks, specs, offsets, flat_bytes, pin_memory)
+    num_slots = _num_slots(prefetch_slots)
+    slot_flats = [torch.empty(flat_bytes, dtype=torch.uint8, device=device) for _ in range(num_slots)]
+    slot_views = [_views(f, specs, offsets) for f in slot_flats]
+    for blk, views in zip(blocks, host_views):
+        for p, v in zip(blk.parameters(), views):
+            p.data = v
+    state = _StreamState(owner, device, list(blocks), host_flats, host_views, host_views, slot_flats, slot_views,
+                         is_double=True)
+    state.holders = holders
+    state.flat_bytes = flat_bytes
+    if profile is None:
+        profile = _env.get("WEIGHTFERRY_PROFILE") == "1"
+    if profile:
+        state.profiler = _StreamProfiler(len(blocks), flat_bytes, True, True)
+    return state
+
+
+def _install_first_block_hook(dit, first_block, state, owner):
+    """Pre-hook of the model's first block: the prefetch of the first slots, only when block 0 really runs."""
+    def first_block_pre_hook(module, args):
+        if getattr(dit, _ACTIVE_ATTR, None) is owner:
+            t0 = time.perf_counter()
+            state.prefetch_first_slots()
+            if state.profiler is not None:
+                state.profiler.add_cpu(time.perf_counter() - t0)
+    state.handles.append(first_block.register_forward_pre_hook(first_block_pre_hook))
+
+
+def _install_block_stream_hooks(dit, state, owner):
+    """Per streamed block a pre-hook (wait for its copy, bind the slot) and a post-hook (free the slot, issue the
+    copy of the block that takes it next)."""
+    def make_pre_hook(cur_s):
+        def stream_pre_hook(module, args):
+            if getattr(dit, _ACTIVE_ATTR, None) is not owner:
+                return
+            t0 = time.perf_counter()
+            prof = state.profiler
+            if prof is not None:
+                prof.mark(cur_s, "cpu_pre_hook")
+            compute = state.compute_stream()
+            slot_idx = state.slot_of(cur_s)
+            if state.is_double:
+                if not state.issued[cur_s]:
+                    state.issue_prefetch(cur_s)      # the prefetch chain was broken (a block was skipped)
+                if prof is not None:
+                    prof.record(cur_s, "wait0", compute)
+                from .. import _native
+                _native.stream_wait(compute, state.transferred_events[cur_s])
+            else:
+                if prof is not None:
+                    prof.record(cur_s, "wait0", compute)
+                state.materialize(cur_s, 0, compute)
+            if prof is not None:
+                prof.record(cur_s, "start", compute)
+            for p, sv in zip(module.parameters(), state.slot_views[slot_idx]):
+                p.data = sv
+            if prof is not None:
+                prof.add_cpu(time.perf_counter() - t0)
+        return stream_pre_hook
+
+    def make_post_hook(cur_s):
+        def stream_post_hook(module, args, output):
+            if getattr(dit, _ACTIVE_ATTR, None) is not owner:
+                return
+            prof = state.profiler
+            compute = state.compute_stream()
+            if prof is not None:
+                prof.record(cur_s, "end", compute)
+            if not state.is_double:
+                return
+            t0 = time.perf_counter()
+            slot_idx = state.slot_of(cur_s)
+            state.computed_events[slot_idx].record(compute)
+            next_s = cur_s + state.num_slots
+            if next_s < state.num_stream and not state.issued[next_s]:
+                state.issue_prefetch(next_s)
+            if prof is not None:
+                prof.add_cpu(time.perf_counter() - t0)
+        return stream_post_hook
+
+    for s_idx, blk in enumerate(state.streaming_blocks):
+        state.handles.append(blk.register_forward_pre_hook(make_pre_hook(s_idx)))
+        state.handles.append(blk.register_forward_hook(make_post_hook(s_idx)))

@@ -1,0 +1,108 @@
+"""Block streaming state: GPU slots, the copy stream and its event fences -- the drop-in for the reference's
+_StreamState (streaming/state.py:21-323), reduced to the direct path (host flats hold the block's compute bytes;
+one host -> GPU copy per block into its slot; no staging conversion, SSD tier or scaled-fp8 swaps).
+
+Protocol (streaming/state.py:133-161,239-256,294-299 and the hooks of streaming/load_steps.py:451-522):
+  issue_prefetch(s): on the copy stream, wait for computed_events[slot] (the slot's previous reader finished),
+      copy block s's host flat into slot s % num_slots, record transferred_events[s], query it (forces submission).
+  pre-hook of block s: issue the copy if the chain broke, the compute stream waits for transferred_events[s], the
+      block's parameters are bound to the slot's views.
+  post-hook of block s: record computed_events[slot] on the compute stream, issue the copy of block s + num_slots.
+Copies run on the library's stream with hipMemcpyAsync; the compute stream is torch's current stream."""
+import torch
+
+from .. import _native
+
+
+class _StreamState:
+    """Per-model streaming state, owned by one owner token."""
+
+    def __init__(self, owner, device, streaming_blocks, host_flats, host_views, rest, slot_flats, slot_views,
+                 is_double=True):
+        self.owner = owner
+        self.device = torch.device(device)
+        self.streaming_blocks = streaming_blocks
+        self.host_flats = host_flats      # per block: one flat (pinned) uint8 buffer = copy source
+        self.host_views = host_views      # per block: parameter views into host_flats
+        self.rest = rest                  # per block: tensors the parameters are bound to between forwards
+        self.slot_flats = slot_flats      # per slot: one flat GPU uint8 buffer
+        self.slot_views = slot_views      # per slot: parameter views into slot_flats
+        self.is_double = is_double
+        self.num_stream = len(streaming_blocks)
+        self.num_slots = len(slot_flats)
+        self.handles = []
+        self.profiler = None
+        self.prefetch_stream = _native.Stream()
+        self.transferred_events = [_native.Event() for _ in range(self.num_stream)]
+        self.computed_events = [_native.Event() for _ in range(self.num_slots)]
+        # the slots were allocated on the compute stream: the first copy into each waits for the work queued so far
+        compute = self.compute_stream()
+        for ev in self.computed_events:
+            ev.record(compute)
+        self.issued = [False] * self.num_stream
+        self.slot_ptrs = {v.data_ptr() for views in slot_views for v in views}
+        self.copies = 0
+
+    def compute_stream(self):
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def slot_of(self, s_idx):
+        return s_idx % self.num_slots
+
+    def materialize(self, s_idx, slot_idx, stream):
+        """Copy block s_idx's host flat into slot slot_idx on ``stream`` (streaming/state.py:133-149)."""
+        prof = self.profiler
+        src = self.host_flats[s_idx]
+        dst = self.slot_flats[slot_idx]
+        n = min(src.numel(), dst.numel())
+        if prof is not None:
+            prof.record(s_idx, "dma0", stream)
+        _native.call("wf_h2d_async", dst.data_ptr(), src.data_ptr(), n, stream)
+        self.copies += 1
+        if prof is not None:
+            prof.record(s_idx, "dma1", stream)
+            prof.record(s_idx, "ready", stream)
+
+    def issue_prefetch(self, s_idx):
+        """Async copy of block s_idx into its slot, after that slot's last reader finished."""
+        if self.profiler is not None:
+            self.profiler.mark(s_idx, "cpu_issue")
+        slot_idx = self.slot_of(s_idx)
+        stream = self.prefetch_stream.handle
+        _native.stream_wait(stream, self.computed_events[slot_idx])
+        self.materialize(s_idx, slot_idx, stream)
+        self.transferred_events[s_idx].record(stream)
+        self.transferred_events[s_idx].query()        # forces submission without blocking the CPU
+        self.issued[s_idx] = True
+
+    def begin_forward(self):
+        self.issued = [False] * self.num_stream
+
+    def prefetch_first_slots(self):
+        """Called when block 0 runs: the first num_slots copies."""
+        if self.is_double:
+            for s_idx in range(min(self.num_slots, self.num_stream)):
+                if not self.issued[s_idx]:
+                    self.issue_prefetch(s_idx)
+
+    def restore_rest_binding(self):
+        """Rebind every parameter that still points at a GPU slot to its rest tensor."""
+        for blk, rest in zip(self.streaming_blocks, self.rest):
+            for p, r in zip(blk.parameters(), rest):
+                if p.data.data_ptr() in self.slot_ptrs:
+                    p.data = r
+
+    def profile_summary(self):
+        return None if self.profiler is None else self.profiler.summary()
+
+    def close(self):
+        """Wait for the copies, remove the hooks, drop the events and the stream."""
+        self.prefetch_stream.synchronize()
+        for h in self.handles:
+            h.remove()
+        self.handles = []
+        for e in self.transferred_events + self.computed_events:
+            e.close()
+        self.prefetch_stream.close()
+        if self.profiler is not None:
+            self.profiler.close()

@@ -62,6 +62,40 @@ int wf_quant_rows_i8(const void* x_bf16, int64_t M, int64_t K, int mode, int8_t*
 int wf_linear_i8(const int8_t* xq, const int8_t* wq, const float* xs, const float* ws, const void* bias, void* out,
                  int out_dt, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* ------------------------------------------------------------------------------- fused dequant + bf16 GEMM
+ * y[m, n] = bf16(sum_k x[m, k] * W[n, k] (+ bias[n])) with W given as GGUF K-quant blocks (qtype 12 Q4_K, 13 Q5_K,
+ * 14 Q6_K; [N, K] row-major in 256-value super-blocks, wq_bytes = N * K / 256 * block bytes) and dequantised inside
+ * the kernel exactly as wf_dequant does with dequant dtype mid_dt and output bf16; float32 accumulation. No
+ * reference function does this in one step: it replaces `dequantize` (enhancers/gguf_dequant.py:296-326) followed
+ * by ComfyUI-GGUF's torch.nn.functional.linear on the bf16 weight. x: bf16 [M, K], 16-byte aligned; bias: bf16 [N]
+ * or NULL; out: bf16 [M, N]. K % 256 == 0. */
+int wf_linear_gguf(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes, int qtype, int64_t N,
+                   const void* bias_bf16, void* out_bf16, int mid_dt, void* stream);
+
+/* ---------------------------------------------------------------------------------------- block streaming
+ * Exact-size page-locked host memory: replaces PinnedHost's cudaHostRegister / cudaHostUnregister
+ * (core/tiers/pinned.py:84-129); allocated page-locked (hipHostMalloc) instead of registered after the fact. */
+int wf_host_alloc(size_t nbytes, void** ptr);
+int wf_host_free(void* ptr);
+
+/* Asynchronous host -> device copy on `stream`: replaces slot_flats[slot].copy_(host_flat, non_blocking=True)
+ * (streaming/state.py:142-143). */
+int wf_h2d_async(void* dst, const void* src, size_t nbytes, void* stream);
+
+/* The side stream and the event fences of _StreamState (streaming/state.py:47-55,239-256;
+ * streaming/activation.py:506-513). Streams are non-blocking at the default priority. wf_event_query returns 0
+ * when the event's work is complete, 1 when not yet (the reference's event.query(), streaming/state.py:255). */
+int wf_stream_create(void** stream);
+int wf_stream_destroy(void* stream);
+int wf_stream_synchronize(void* stream);
+int wf_event_create(void** event, int timing);
+int wf_event_destroy(void* event);
+int wf_event_record(void* event, void* stream);
+int wf_stream_wait_event(void* stream, void* event);
+int wf_event_query(void* event);
+int wf_event_synchronize(void* event);
+int wf_event_elapsed_ms(void* start, void* end, float* ms);
+
 #ifdef __cplusplus
 }
 #endif
