@@ -6,9 +6,16 @@ bfloat16 output. One step = both matrices (two launches of the same kernel). Inp
 the timed region; each step works on the next of four copies of inputs and outputs (1.45 GB in all), so the
 256 MB last-level cache cannot serve one step's bytes to the next.
 
-Other rows of the workload list are reported under "also": Q8_0 dequantisation of a 5120 x 5120 weight.
+Other rows of the workload list are reported under "also":
+  * Q8_0 dequantisation of a 5120 x 5120 weight (MID float16 and float32);
+  * the int8 W8A8 linear at M in {1024, 4096, 16384}, K = 5120, N in {5120, 13824} (per-token int8 activations,
+    per-channel int8 weights, int32 accumulation, bf16 out), and the row quantiser;
+  * fused Q5_K / Q6_K dequant + bf16 GEMM over the linears of one Wan-2.1-14B block at 4096 tokens, next to the
+    two-step flow (wf_dequant, then torch's bf16 GEMM);
+  * 40 streamed Wan-14B blocks of Q4_K from pinned host memory through 2 GPU slots, 4096 tokens (ms/step, H2D
+    GB/s, share of the copy time hidden behind compute).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--only-headline]
 """
 import argparse
 import importlib
@@ -29,7 +36,129 @@ def _args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true", help="leave out the CPU baseline leg")
+    ap.add_argument("--only-headline", action="store_true", help="the Q4_K dequant leg only")
     return ap.parse_args()
+
+
+def _timed(torch, fn, n, warm):
+    """Mean ms of fn() over n back-to-back calls on torch's current stream (events at both ends)."""
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(n):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / n
+
+
+def int8_leg(torch, native):
+    """W8A8 linear rows: TOPS of wf_linear_i8 and GB/s of wf_quant_rows_i8 (plain per-token)."""
+    lib = native.lib()
+    dev = torch.device("cuda:0")
+    st = native.stream_of(dev)
+    K = 5120
+    out = {}
+    g = torch.Generator(device=dev).manual_seed(1234)
+    for M in (1024, 4096, 16384):
+        x = torch.randn((M, K), device=dev, generator=g).to(torch.bfloat16)
+        xq = torch.empty((M, K), dtype=torch.int8, device=dev)
+        xs = torch.empty(M, dtype=torch.float32, device=dev)
+        msq = _timed(torch, lambda: lib.wf_quant_rows_i8(x.data_ptr(), M, K, 0, xq.data_ptr(), xs.data_ptr(), st),
+                     20, 3)
+        out[f"quant_rows_plain_M{M}"] = {"us": round(msq * 1e3, 2),
+                                         "GB/s": round((3 * M * K + 4 * M) / msq / 1e6, 1)}
+        for N in (5120, 13824):
+            w = torch.randn((N, K), device=dev, generator=g) * 0.02
+            ws = (w.abs().amax(dim=1) / 127).float()
+            wq = torch.clamp(torch.round(w / ws[:, None]), -127, 127).to(torch.int8)
+            del w
+            y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            ms = _timed(torch, lambda: lib.wf_linear_i8(xq.data_ptr(), wq.data_ptr(), xs.data_ptr(), ws.data_ptr(),
+                                                        None, y.data_ptr(), 1, M, N, K, st), 10, 2)
+            tops = 2 * M * N * K / ms / 1e9
+            out[f"gemm_M{M}_N{N}"] = {"us": round(ms * 1e3, 1), "TOPS": round(tops, 1),
+                                      "frac_of_5000": round(tops / 5000, 3)}
+            del wq, y
+        del x, xq
+    torch.cuda.empty_cache()
+    return out
+
+
+WAN_LINEARS = [("q", 5120, 5120), ("k", 5120, 5120), ("v", 5120, 5120), ("o", 5120, 5120),
+               ("ffn_up", 13824, 5120), ("ffn_down", 5120, 13824)]
+
+
+def fused_leg(torch, native):
+    """One Wan-14B block's linears at 4096 tokens with Q5_K / Q6_K weights: the fused kernel and the two-step
+    flow (wf_dequant to bf16, then torch's bf16 GEMM)."""
+    sys.path.insert(0, ROOT)
+    from oracle import encode
+    lib = native.lib()
+    dev = torch.device("cuda:0")
+    st = native.stream_of(dev)
+    M = 4096
+    res = {}
+    for qt, name in ((13, "q5_k"), (14, "q6_k")):
+        tf = tu = 0.0
+        flops = wbytes = 0
+        for lname, N, K in WAN_LINEARS:
+            raw = torch.from_numpy(encode.encode(encode.weights((N, K), seed=N + K), qt)).to(dev)
+            x = torch.randn((M, K), device=dev).to(torch.bfloat16)
+            y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            w = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+
+            def fused():
+                lib.wf_linear_gguf(x.data_ptr(), M, K, raw.data_ptr(), raw.numel(), qt, N, None, y.data_ptr(), 0, st)
+
+            def two_step():
+                lib.wf_dequant(raw.data_ptr(), raw.numel(), qt, 0, 1, w.data_ptr(), N * K, st)
+                torch.matmul(x, w.t(), out=y)
+            tf += _timed(torch, fused, 5, 1)
+            tu += _timed(torch, two_step, 5, 1)
+            flops += 2 * M * N * K
+            wbytes += raw.numel()
+            del raw, x, y, w
+        res[name] = {"fused_ms": round(tf, 3), "fused_TFLOPS": round(flops / tf / 1e9, 1),
+                     "fused_frac_of_2500": round(flops / tf / 1e9 / 2500, 3),
+                     "two_step_ms": round(tu, 3), "two_step_TFLOPS": round(flops / tu / 1e9, 1),
+                     "flop": flops, "weight_bytes": wbytes}
+    torch.cuda.empty_cache()
+    return res
+
+
+def streaming_leg(torch, native, n_blocks=40, steps=10):
+    """40 Wan-14B blocks with Q4_K weights streamed from pinned host memory through 2 GPU slots (4096 tokens)."""
+    syn = importlib.import_module(PKG + ".streaming.synthetic")
+    dn = importlib.import_module(PKG + ".streaming.dit_node")
+    prof_mod = importlib.import_module(PKG + ".streaming.profiler")
+    dev = torch.device("cuda:0")
+    t = time.perf_counter()
+    model = syn.WanLikeStack(n_blocks=n_blocks, qtype=12, mode="dequant")
+    model.fill_random(1234)
+    sm = dn.apply_streaming(model, device=dev, prefetch_slots=2, profile=False)
+    _log(f"streaming: {n_blocks} blocks captured into pinned memory in {time.perf_counter() - t:.1f} s")
+    g = torch.Generator().manual_seed(99)
+    x = torch.randn((1, 4096, 5120), generator=g).to(torch.bfloat16).to(dev)
+    ctx = torch.randn((1, 512, 5120), generator=g).to(torch.bfloat16).to(dev)
+    with torch.no_grad():
+        ms = _timed(torch, lambda: sm(x, ctx), steps, 1)
+        sm.state.profiler = prof_mod._StreamProfiler(n_blocks, sm.state.flat_bytes, True)
+        for _ in range(3):
+            sm(x, ctx)
+    torch.cuda.synchronize()
+    prof = sm.profile_summary()["mean_excluding_first_forward"]
+    flat = sm.state.flat_bytes
+    sm.teardown(device="cpu")
+    del model, sm
+    torch.cuda.empty_cache()
+    return {"ms_per_step": round(ms, 2), "blocks": n_blocks, "slots": 2, "bytes_per_block": flat,
+            "h2d_GBps_effective": round(flat * n_blocks / (ms / 1e3) / 1e9, 2),
+            "profiled": {"forward_ms": prof["forward_ms"], "dma_ms": prof["dma_ms"], "stall_ms": prof["stall_ms"],
+                         "hidden_fraction": prof["overlap_ratio"], "dma_gbps": prof["dma_gbps"]},
+            "linears": "wf_dequant + torch bf16 GEMM"}
 
 
 def _log(msg):
@@ -99,6 +228,19 @@ def cpu_baseline_dequant(torch, raw, qtype, rows, cols, budget_s=12.0):
                       f"first {rows} rows of the 13824x5120 weight, median of {len(times)} runs"}
 
 
+def _traffic():
+    """HBM bytes per launch of the headline kernel from the committed rocprofv3 counter summary (FETCH_SIZE +
+    WRITE_SIZE scaled by the plain-copy calibration), or None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "dequant_q4_k_ffn_pmc.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def main():
     args = _args()
     if args.gpus != 1:
@@ -127,6 +269,20 @@ def main():
     _log(f"Q4_K pair: {ms_step * 1e3:.1f} us/step, kernel {kern_ms * 1e3:.1f} us, {value:.0f} GB/s")
 
     also = {}
+    # calibration: a plain copy of 512 MiB (two rotating pairs: 2 GiB in all) -- the achievable HBM rate, and the
+    # known-size kernel the counter runs are scaled by
+    cp = [(torch.empty(1 << 29, dtype=torch.uint8, device="cuda"), torch.empty(1 << 29, dtype=torch.uint8,
+                                                                               device="cuda")) for _ in range(2)]
+    turn = [0]
+
+    def copy_once():
+        src, dst = cp[turn[0] % 2]
+        turn[0] += 1
+        dst.copy_(src)
+    ms_cp = _timed(torch, copy_once, 10, 2)
+    also["plain_copy_512MiB"] = {"GB/s": round(2 * (1 << 29) / ms_cp / 1e6, 1), "us": round(ms_cp * 1e3, 1)}
+    del cp
+    torch.cuda.empty_cache()
     # MID float32 on the same pair
     ms32, k32, _ = dequant_leg(torch, native, raws, shapes, 12, 2, 1, max(5, args.steps // 2), 3)
     also["q4_k_pair_mid_f32"] = {"GB/s": round(algo / (ms32 / 1e3) / 1e9, 1),
@@ -137,6 +293,13 @@ def main():
         ms8, k8, a8 = dequant_leg(torch, native, q8, [(5120, 5120)], 8, mid, 1, args.steps, args.warmup)
         also[name] = {"GB/s": round(a8 / (k8 / 1e3) / 1e9, 1), "kernel_us": round(k8 * 1e3, 2),
                       "frac": round(a8 / (k8 / 1e3) / 1e9 / HBM_PEAK_GBS, 3), "bytes": a8}
+    if not args.only_headline:
+        also["int8_w8a8"] = int8_leg(torch, native)
+        _log("int8 leg done")
+        also["fused_dequant_gemm_wan_block"] = fused_leg(torch, native)
+        _log("fused leg done")
+        also["streamed_40_blocks_q4_k"] = streaming_leg(torch, native)
+        _log("streaming leg done")
     cpu = None
     if not args.skip_cpu:
         cpu = cpu_baseline_dequant(torch, raws[0], 12, 512, 5120)
@@ -158,7 +321,7 @@ def main():
         "config": {"workload": "Q4_K dequant of a 14B-DiT FFN pair 13824x5120 + 5120x13824 -> bf16 (MID f16)",
                    "bytes_per_step": algo, "rotating_copies": ROTATE},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(),
                      "kernel": "wf::deq_items<wf::Q45_K<12, f16, bf16>>", "kernel_us": round(kern_ms * 1e3, 2),
                      "bytes_per_launch": per_launch},
         "cpu_baseline": cpu,

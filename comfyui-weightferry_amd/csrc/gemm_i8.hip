@@ -47,11 +47,19 @@ __device__ __forceinline__ void tile_of(int w, int T, int ntm, int ntn, int& tm,
     tn = in / gm;
 }
 
-template <int WM, int WN, int OUT, bool BIAS>
+// Epilogue operands of the residual variant: out = OUT(resid + gate[m / rows_per_group] * t), t the plain epilogue
+// value before rounding (the role of kitchen's cutlass_int8_dequant_residual, enhancers/fused_int8.py:212-268).
+struct Residual {
+    const uint16_t* gate;    // bf16 [groups, N]
+    const uint16_t* resid;   // bf16 [M, N]
+    int rows_per_group;
+};
+
+template <int WM, int WN, int OUT, bool BIAS, bool RESID = false>
 __global__ __launch_bounds__(256) void gemm_i8(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
                                                const float* __restrict__ xs, const float* __restrict__ ws,
                                                const void* __restrict__ bias, void* __restrict__ out,
-                                               int M, int N, int K) {
+                                               int M, int N, int K, Residual res = {}) {
     constexpr int BM = 2 * WM * 32, BN = 2 * WN * 32;
     constexpr int ACH = BM * 8 / 256, BCH = BN * 8 / 256;     // 16-byte chunks per thread per stage
     __shared__ uint4 lds[2][(BM + BN) * 8];
@@ -153,6 +161,11 @@ __global__ __launch_bounds__(256) void gemm_i8(const int8_t* __restrict__ A, con
                 float t = ((float)acc[i][j][e] * xs[m]) * wsn;
                 if (BIAS) t = t + bn;
                 const int64_t o = (int64_t)m * N + n;
+                if constexpr (RESID) {
+                    const float g = __uint_as_float((uint32_t)res.gate[(int64_t)(m / res.rows_per_group) * N + n] << 16);
+                    const float r = __uint_as_float((uint32_t)res.resid[o] << 16);
+                    t = r + g * t;
+                }
                 if constexpr (OUT == WF_BF16) {
                     static_cast<__bf16*>(out)[o] = (__bf16)t;
                 } else {
@@ -181,7 +194,37 @@ static void dispatch(const int8_t* A, const int8_t* B, const float* xs, const fl
     else launch_gemm<2, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, s);
 }
 
+template <int WM, int WN>
+static void launch_resid(const int8_t* A, const int8_t* B, const float* xs, const float* ws, void* out, int M, int N,
+                         int K, Residual r, hipStream_t s) {
+    constexpr int BM = 2 * WM * 32, BN = 2 * WN * 32;
+    const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    gemm_i8<WM, WN, WF_BF16, false, true><<<dim3(tiles), 256, 0, s>>>(A, B, xs, ws, nullptr, out, M, N, K, r);
+}
+
 }  // namespace wf
+
+extern "C" int wf_linear_i8_residual(const int8_t* xq, const int8_t* wq, const float* xs, const float* ws,
+                                     const void* gate_bf16, const void* resid_bf16, void* out_bf16, int64_t M,
+                                     int64_t N, int64_t K, int64_t rows_per_group, void* stream) {
+    using namespace wf;
+    if (M < 0 || N < 0 || K <= 0 || rows_per_group <= 0) { set_error("wf_linear_i8_residual: bad sizes"); return WF_EINVAL; }
+    if (M == 0 || N == 0) return WF_OK;
+    if (!xq || !wq || !xs || !ws || !gate_bf16 || !resid_bf16 || !out_bf16) { set_error("wf_linear_i8_residual: null pointer"); return WF_EINVAL; }
+    if (K % 16 || !aligned(xq, 16) || !aligned(wq, 16)) {
+        set_error("wf_linear_i8_residual: K %% 16 == 0 and 16-byte aligned operands are required");
+        return WF_EUNSUPPORTED;
+    }
+    if (M % rows_per_group) { set_error("wf_linear_i8_residual: M is not a whole number of row groups"); return WF_EUNSUPPORTED; }
+    if (M >= (1LL << 31) || N >= (1LL << 31) || K > 131071) { set_error("wf_linear_i8_residual: sizes too large"); return WF_EUNSUPPORTED; }
+    Residual r{static_cast<const uint16_t*>(gate_bf16), static_cast<const uint16_t*>(resid_bf16), (int)rows_per_group};
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+    if (big_tiles >= 512) launch_resid<4, 4>(xq, wq, xs, ws, out_bf16, (int)M, (int)N, (int)K, r, s);
+    else launch_resid<2, 2>(xq, wq, xs, ws, out_bf16, (int)M, (int)N, (int)K, r, s);
+    WF_LAUNCH_CHECK("wf_linear_i8_residual launch");
+    return WF_OK;
+}
 
 extern "C" int wf_linear_i8(const int8_t* xq, const int8_t* wq, const float* xs, const float* ws, const void* bias,
                             void* out, int out_dt, int64_t M, int64_t N, int64_t K, void* stream) {

@@ -62,6 +62,14 @@ int wf_quant_rows_i8(const void* x_bf16, int64_t M, int64_t K, int mode, int8_t*
 int wf_linear_i8(const int8_t* xq, const int8_t* wq, const float* xs, const float* ws, const void* bias, void* out,
                  int out_dt, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* out = bf16(resid + gate[m / rows_per_group] * ((float(acc) * xs[m]) * ws[n])), one product and one sum each
+ * rounded in float32, then the single rounding to bf16: replaces kitchen's cutlass_int8_dequant_residual
+ * (enhancers/fused_int8.py:212-268: x_res + gate * linear(x) per (batch, frame) group of rows). gate: bf16
+ * [M / rows_per_group, N]; resid, out: bf16 [M, N]. */
+int wf_linear_i8_residual(const int8_t* xq, const int8_t* wq, const float* xs, const float* ws, const void* gate_bf16,
+                          const void* resid_bf16, void* out_bf16, int64_t M, int64_t N, int64_t K,
+                          int64_t rows_per_group, void* stream);
+
 /* ------------------------------------------------------------------------------- fused dequant + bf16 GEMM
  * y[m, n] = bf16(sum_k x[m, k] * W[n, k] (+ bias[n])) with W given as GGUF K-quant blocks (qtype 12 Q4_K, 13 Q5_K,
  * 14 Q6_K; [N, K] row-major in 256-value super-blocks, wq_bytes = N * K / 256 * block bytes) and dequantised inside

@@ -119,3 +119,76 @@ def test_linear_workload_shapes_sampled_rows(native, M, N):
     ref = ((acc.float() * xs[rows, None]) * ws[None, :]).to(torch.bfloat16)
     got = out[rows.cuda()].cpu()
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
+# ------------------------------------------------------------------------------------- drop-in entry points
+def test_shared_forward_qkv_share_one_quantisation(native):
+    from fake_quant import FakeQT, Lin
+    fi = sub("enhancers.fused_int8")
+    fs = sub("enhancers.fused_state")
+    fs.stats(reset=True)
+    g = torch.Generator().manual_seed(11)
+    K = 5120
+    x = (torch.randn((2, 300, K), generator=g)).to(torch.bfloat16).cuda()
+    lins, ref = [], []
+    for n in (5120, 5120, 1024):
+        w_q = torch.randint(-127, 128, (n, K), generator=g, dtype=torch.int64).to(torch.int8)
+        ws = torch.rand(n, generator=g) * 0.01
+        lins.append(Lin(FakeQT(w_q.cuda(), ws.cuda())))
+        ref.append((w_q, ws))
+    calls = []
+    orig = fi.quantise_rows
+    fi.quantise_rows = lambda *a: calls.append(1) or orig(*a)
+    try:
+        with fi._Overrides(lins):
+            ys = [lin(x) for lin in lins]
+    finally:
+        fi.quantise_rows = orig
+    torch.cuda.synchronize()
+    assert len(calls) == 1 and fs.stats()["qkv"]["used"] == 3
+    xq, xs = lib.quant_rows(x.reshape(-1, K).cpu().view(torch.int16).numpy().view(np.uint16), 1)
+    for y, (w_q, ws) in zip(ys, ref):
+        assert y.shape == (2, 300, w_q.shape[0])
+        expect = lib.linear_i8(xq, w_q.numpy(), xs, ws.numpy(), out_dt=lib.BF16)
+        assert np.array_equal(_bits(y.reshape(600, -1)), expect)
+
+
+def test_residual_forward_matches_oracle(native):
+    from fake_quant import FakeQT
+    fi = sub("enhancers.fused_int8")
+    g = torch.Generator().manual_seed(12)
+    B, T, H, W, D = 2, 2, 4, 8, 1024
+    x = torch.randn((B, T, H, W, D), generator=g).to(torch.bfloat16).cuda()
+    w_q = torch.randint(-127, 128, (D, D), generator=g, dtype=torch.int64).to(torch.int8)
+    ws = torch.rand(D, generator=g) * 0.01
+    xres = torch.randn((B, T, H, W, D), generator=g).to(torch.bfloat16).cuda()
+    gate = torch.randn((B, T, 1, 1, D), generator=g).to(torch.bfloat16).cuda()
+    fi._tls.res = {"x": xres, "gate": gate, "done": False}
+    try:
+        with fi._Overrides([]):
+            y = fi._residual_forward(x, FakeQT(w_q.cuda(), ws.cuda()), None)
+    finally:
+        fi._tls.res = None
+    torch.cuda.synchronize()
+    xq, xs = lib.quant_rows(x.reshape(-1, D).cpu().view(torch.int16).numpy().view(np.uint16), 1)
+    expect = lib.linear_i8_residual(xq, w_q.numpy(), xs, ws.numpy(),
+                                    gate.reshape(B * T, D).cpu().view(torch.int16).numpy().view(np.uint16),
+                                    xres.reshape(-1, D).cpu().view(torch.int16).numpy().view(np.uint16), H * W)
+    assert y.shape == xres.shape
+    assert np.array_equal(_bits(y.reshape(-1, D)), expect)
+
+
+@pytest.mark.parametrize("M,N", [(1024, 5120), (300, 13824)])
+def test_int8_linear_plain_per_token(native, M, N):
+    fi = sub("enhancers.fused_int8")
+    K = 5120
+    g = torch.Generator().manual_seed(M)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16)
+    w = torch.randn((N, K), generator=g) * 0.02
+    ws = (w.abs().amax(dim=1) / 127).float()
+    w_q = torch.clamp(torch.round(w / ws[:, None]), -127, 127).to(torch.int8)
+    y = fi.int8_linear(x.cuda(), w_q.cuda(), ws.cuda(), convrot=False)
+    torch.cuda.synchronize()
+    xq, xs = lib.quant_rows(x.view(torch.int16).numpy().view(np.uint16), 0)
+    expect = lib.linear_i8(xq, w_q.numpy(), xs, ws.numpy(), out_dt=lib.BF16)
+    assert np.array_equal(_bits(y), expect)
