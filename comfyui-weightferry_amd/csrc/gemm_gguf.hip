@@ -4,13 +4,14 @@
 // The reference does the dequantisation into a bf16 weight in HBM and then ComfyUI-GGUF's F.linear; here the
 // weight never leaves the chip in bf16.
 //
-// Tiling: a 256-thread workgroup computes a 256 x 256 tile with 2 x 2 waves of 128 x 128 (4 x 4 tiles of
-// v_mfma_f32_32x32x16_bf16). K advances in stages of 64 (128 bytes of bf16 per row): the activation stage is
-// loaded from global memory into registers one stage ahead; for the weight stage, thread t takes row n0 + t and
-// dequantises its 64 values (one sub-block pair of the super-block) from the raw blocks, also one stage ahead.
-// Both land in double-buffered LDS with the 16-byte chunk swizzle c ^ ((r >> 1) & 7) (conflict-free writes and
-// fragment reads). Fragment layout: lane l holds 8 bf16 of row l % 32 at K offset 8 * (l / 32) of the 16-wide
-// step; result layout: lane l, register i -> row 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32.
+// Tiling: a 512-thread workgroup computes a 256 x 256 tile with 2 x 4 waves of 128 x 64 (4 x 2 tiles of
+// v_mfma_f32_32x32x16_bf16), two waves per SIMD, so one wave's dequantisation runs while the other's MFMAs do.
+// K advances in stages of 64 (128 bytes of bf16 per row): the activation stage comes in through buffer loads one
+// stage ahead (rows past M read as zeros); for the weight stage, threads 2r and 2r + 1 take the two halves of row
+// n0 + r -- for Q4_K / Q5_K exactly one 32-value sub-block each -- and dequantise them from the raw blocks, loaded
+// one stage ahead. Both land in double-buffered LDS with a 16-byte chunk swizzle that is conflict-free for writes and
+// fragment reads. Fragment layout: lane l holds 8 bf16 of row l % 32 at K offset 8 * (l / 32) of the 16-wide step;
+// result layout: lane l, register i -> row 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32.
 
 #include "kquant.h"
 
@@ -21,7 +22,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kGroupMG = 8;
 
-__device__ __forceinline__ int swz8(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+__device__ __forceinline__ int swz8(int row, int chunk) { return chunk ^ (((row >> 1) ^ ((row & 1) << 2)) & 7); }
 
 __device__ __forceinline__ void tile_order(int w, int T, int ntm, int ntn, int& tm, int& tn) {
     int L = w;
@@ -50,17 +51,18 @@ __device__ __forceinline__ void load_words(const uint8_t* p, uint32_t o, uint32_
     for (int i = 0; i < ND; i++) w[i] = __builtin_amdgcn_alignbit(raw[i + 1], raw[i], sh);
 }
 
-// raw bytes a thread needs for one row's 64 values of a stage
+// Raw bytes a thread needs for its 32 values of a stage: half h (0 / 1) of the stage's 64-value slice `part`
+// (0..3) of one super-block.
 template <int QT>
-struct StageRaw;
-template <> struct StageRaw<12> { uint4 hdr; uint32_t q[8]; };
-template <> struct StageRaw<13> { uint4 hdr; uint32_t q[8]; uint32_t qh[8]; };
-template <> struct StageRaw<14> { uint32_t ql[16]; uint32_t qh[8]; uint32_t sc; uint32_t d; };
+struct HalfRaw;
+template <> struct HalfRaw<12> { uint4 hdr; uint32_t q[8]; };
+template <> struct HalfRaw<13> { uint4 hdr; uint32_t q[8]; uint32_t qh[8]; };
+template <> struct HalfRaw<14> { uint32_t ql[8]; uint32_t qh[8]; uint32_t sc; uint32_t d; };
 
-// Q4_K / Q5_K: pair p = sub-blocks 2p (low nibbles of qs[32p .. 32p + 32)) and 2p + 1 (high nibbles)
 template <int QT>
-__device__ __forceinline__ void raw_load(const uint8_t* sbp, int part, StageRaw<QT>& r) {
+__device__ __forceinline__ void half_load(const uint8_t* sbp, int part, int h, HalfRaw<QT>& r) {
     if constexpr (QT == 12 || QT == 13) {
+        // Q4_K / Q5_K: sub-block 2 part + h = nibble h of qs[32 part .. 32 part + 32); Q5_K bit (2 part + h) of qh
         constexpr int QS = QT == 12 ? 16 : 48;
         r.hdr = *reinterpret_cast<const uint4*>(sbp);
         const uint4 a = *reinterpret_cast<const uint4*>(sbp + QS + 32 * part);
@@ -74,109 +76,87 @@ __device__ __forceinline__ void raw_load(const uint8_t* sbp, int part, StageRaw<
             r.qh[4] = e.x; r.qh[5] = e.y; r.qh[6] = e.z; r.qh[7] = e.w;
         }
     } else {
-        // Q6_K values 64 part .. 64 part + 63: half h = part / 2; ql[64h .. +64), qh[32h .. +32), scales
-        // 4 part .. 4 part + 3, d. The super-block may start 2 (mod 4) bytes into a dword.
-        const int h = part >> 1;
-        load_words<16>(sbp, 64 * h, r.ql);          // bytes [64h - 2, 64h + 68) at most: inside the 210
-        load_words<8>(sbp, 128 + 32 * h, r.qh);     // bytes [126 + 32h, 164 + 32h) at most: inside
-        const uint16_t* sc16 = reinterpret_cast<const uint16_t*>(sbp + 192 + 4 * part);
-        r.sc = (uint32_t)sc16[0] | ((uint32_t)sc16[1] << 16);
+        // Q6_K values 64 part + 32 h + i: ql[64 (part / 2) + 32 h + i] nibble (part & 1); qh[32 (part / 2) + i] at
+        // shift 2 (2 (part & 1) + h); scales 4 part + 2 h + i / 16; d. Reads stay inside the 210-byte block.
+        const int hh = part >> 1;
+        load_words<8>(sbp, 64 * hh + 32 * h, r.ql);       // bytes up to 96 + 36 = 132
+        load_words<8>(sbp, 128 + 32 * hh, r.qh);          // bytes up to 160 + 36 = 196
+        r.sc = *reinterpret_cast<const uint16_t*>(sbp + 192 + 4 * part + 2 * h);
         r.d = *reinterpret_cast<const uint16_t*>(sbp + 208);
     }
 }
 
-// 64 values of the row, as 32 packed bf16 pairs (values 2i, 2i + 1 in o[i])
+// 32 values as 16 packed bf16 pairs (values 2i, 2i + 1 in o[i])
 template <int QT, int MID>
-__device__ __forceinline__ void raw_dequant(const StageRaw<QT>& r, int part, uint32_t (&o)[32]) {
+__device__ __forceinline__ void half_dequant(const HalfRaw<QT>& r, int part, int h, uint32_t (&o)[16]) {
     if constexpr (QT == 12 || QT == 13) {
-        uint32_t lo[8], hi[8];
+        const int sub = 2 * part + h;
+        const uint32_t ns = 4u * (uint32_t)h;
+        uint32_t q[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            lo[i] = r.q[i] & 0x0f0f0f0fu;
-            hi[i] = (r.q[i] >> 4) & 0x0f0f0f0fu;
-            if constexpr (QT == 13) {
-                lo[i] |= ((r.qh[i] >> (2 * part)) & 0x01010101u) << 4;
-                hi[i] |= ((r.qh[i] >> (2 * part + 1)) & 0x01010101u) << 4;
-            }
+            q[i] = (r.q[i] >> ns) & 0x0f0f0f0fu;
+            if constexpr (QT == 13) q[i] |= ((r.qh[i] >> sub) & 0x01010101u) << 4;
         }
-        uint32_t scA, mA, scB, mB;
-        scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * part, scA, mA);
-        scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * part + 1, scB, mB);
+        uint32_t sc, m;
+        scale_min(r.hdr.y, r.hdr.z, r.hdr.w, sub, sc, m);
         if constexpr (MID == WF_F16) {
-            const h2 dd = as_h2(r.hdr.x);
             const h2 off = h2s(-1024.0f);
-            const h2 pA = dd * (as_h2(scA | (mA << 16) | 0x64006400u) + off);
-            const h2 pB = dd * (as_h2(scB | (mB << 16) | 0x64006400u) + off);
-            const h2 dsA = lo2(pA), dmA = hi2(pA), dsB = lo2(pB), dmB = hi2(pB);
+            const h2 pr = as_h2(r.hdr.x) * (as_h2(sc | (m << 16) | 0x64006400u) + off);   // (d * sc, dmin * m)
+            const h2 ds = lo2(pr), dm = hi2(pr);
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                const h2 a0 = dsA * (biased_lo(lo[i]) + off) - dmA, a1 = dsA * (biased_hi(lo[i]) + off) - dmA;
-                const h2 b0 = dsB * (biased_lo(hi[i]) + off) - dmB, b1 = dsB * (biased_hi(hi[i]) + off) - dmB;
-                o[2 * i] = pack_bf16((float)a0[0], (float)a0[1]);
-                o[2 * i + 1] = pack_bf16((float)a1[0], (float)a1[1]);
-                o[16 + 2 * i] = pack_bf16((float)b0[0], (float)b0[1]);
-                o[16 + 2 * i + 1] = pack_bf16((float)b1[0], (float)b1[1]);
+                const h2 v0 = ds * (biased_lo(q[i]) + off) - dm, v1 = ds * (biased_hi(q[i]) + off) - dm;
+                o[2 * i] = pack_bf16((float)v0[0], (float)v0[1]);
+                o[2 * i + 1] = pack_bf16((float)v1[0], (float)v1[1]);
             }
         } else {
             const float d = round_to<MID>(f16_bits_to_f32(r.hdr.x & 0xffffu));
             const float dmin = round_to<MID>(f16_bits_to_f32(r.hdr.x >> 16));
-            const float dsA = round_to<MID>(d * (float)scA), dmA = round_to<MID>(dmin * (float)mA);
-            const float dsB = round_to<MID>(d * (float)scB), dmB = round_to<MID>(dmin * (float)mB);
+            const float ds = round_to<MID>(d * (float)sc), dm = round_to<MID>(dmin * (float)m);
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                float a[4], b[4];
+                float v[4];
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    a[e] = round_to<MID>(round_to<MID>(dsA * (float)byte_of(lo[i], e)) - dmA);
-                    b[e] = round_to<MID>(round_to<MID>(dsB * (float)byte_of(hi[i], e)) - dmB);
-                }
-                o[2 * i] = pack_bf16(a[0], a[1]);
-                o[2 * i + 1] = pack_bf16(a[2], a[3]);
-                o[16 + 2 * i] = pack_bf16(b[0], b[1]);
-                o[16 + 2 * i + 1] = pack_bf16(b[2], b[3]);
+                for (int e = 0; e < 4; e++) v[e] = round_to<MID>(round_to<MID>(ds * (float)byte_of(q[i], e)) - dm);
+                o[2 * i] = pack_bf16(v[0], v[1]);
+                o[2 * i + 1] = pack_bf16(v[2], v[3]);
             }
         }
     } else {
-        // value l (0..63): low bits nibble (part & 1) of ql[l]; high bits of qh[l % 32] at shift 2 (2 (part & 1) +
-        // l / 32); scale byte l / 16 of r.sc
         const uint32_t ns = 4u * (uint32_t)(part & 1);
-        const uint32_t s0 = 2u * (2u * (uint32_t)(part & 1)), s1 = s0 + 2u;
-        uint32_t code[16];
+        const uint32_t hs = 2u * (2u * (uint32_t)(part & 1) + (uint32_t)h);
+        uint32_t code[8];
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const uint32_t hsh = i < 8 ? s0 : s1;
-            code[i] = ((r.ql[i] >> ns) & 0x0f0f0f0fu) | (((r.qh[i & 7] >> hsh) & 0x03030303u) << 4);
-        }
+        for (int i = 0; i < 8; i++)
+            code[i] = ((r.ql[i] >> ns) & 0x0f0f0f0fu) | (((r.qh[i] >> hs) & 0x03030303u) << 4);
         if constexpr (MID == WF_F16) {
             const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)r.d);
             const h2 off = h2s(-1056.0f);
+            h2 dd; dd[0] = d; dd[1] = d;
+            h2 sc2;
+            sc2[0] = (_Float16)(float)(int8_t)byte_of(r.sc, 0);
+            sc2[1] = (_Float16)(float)(int8_t)byte_of(r.sc, 1);
+            const h2 pd = dd * sc2;                       // (d * sc[first 16], d * sc[second 16]), rounded to f16
 #pragma unroll
-            for (int g = 0; g < 4; g++) {                 // scale g covers values 16g .. 16g + 15 = code[4g .. 4g + 3]
-                h2 dsc;
-                dsc[0] = (_Float16)(float)(int8_t)byte_of(r.sc, g);
-                dsc[1] = dsc[0];
-                h2 dd; dd[0] = d; dd[1] = d;
-                const h2 ds = dd * dsc;
-#pragma unroll
-                for (int i = 4 * g; i < 4 * g + 4; i++) {
-                    const h2 v0 = ds * (biased_lo(code[i]) + off), v1 = ds * (biased_hi(code[i]) + off);
-                    o[2 * i] = pack_bf16((float)v0[0], (float)v0[1]);
-                    o[2 * i + 1] = pack_bf16((float)v1[0], (float)v1[1]);
-                }
+            for (int i = 0; i < 8; i++) {
+                const h2 ds = i < 4 ? lo2(pd) : hi2(pd);
+                const h2 v0 = ds * (biased_lo(code[i]) + off), v1 = ds * (biased_hi(code[i]) + off);
+                o[2 * i] = pack_bf16((float)v0[0], (float)v0[1]);
+                o[2 * i + 1] = pack_bf16((float)v1[0], (float)v1[1]);
             }
         } else {
             const float d = round_to<MID>(f16_bits_to_f32(r.d));
+            const float ds0 = round_to<MID>(d * (float)(int8_t)byte_of(r.sc, 0));
+            const float ds1 = round_to<MID>(d * (float)(int8_t)byte_of(r.sc, 1));
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const float ds = round_to<MID>(d * (float)(int8_t)byte_of(r.sc, g));
+            for (int i = 0; i < 8; i++) {
+                const float ds = i < 4 ? ds0 : ds1;
+                float v[4];
 #pragma unroll
-                for (int i = 4 * g; i < 4 * g + 4; i++) {
-                    float v[4];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) v[e] = round_to<MID>(ds * (float)((int)byte_of(code[i], e) - 32));
-                    o[2 * i] = pack_bf16(v[0], v[1]);
-                    o[2 * i + 1] = pack_bf16(v[2], v[3]);
-                }
+                for (int e = 0; e < 4; e++) v[e] = round_to<MID>(ds * (float)((int)byte_of(code[i], e) - 32));
+                o[2 * i] = pack_bf16(v[0], v[1]);
+                o[2 * i + 1] = pack_bf16(v[2], v[3]);
             }
         }
     }
@@ -185,108 +165,128 @@ __device__ __forceinline__ void raw_dequant(const StageRaw<QT>& r, int part, uin
 template <int QT>
 struct GGUFTs { static constexpr int TS = QT == 12 ? 144 : QT == 13 ? 176 : 210; };
 
-template <int QT, int MID, bool BIAS>
-__global__ __launch_bounds__(256) void gemm_gguf(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
-                                                 const uint16_t* __restrict__ bias, uint16_t* __restrict__ Y,
-                                                 int M, int N, int K) {
-    constexpr int BM = 256, BN = 256, WT = 4;          // 4 x 4 MFMA tiles of 32 x 32 per wave
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int64_t bytes) {
+    const int32_t n = bytes > 0x7fffffff ? 0x7fffffff : (int32_t)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, n, 0x00020000);
+}
+
+// VM x VN waves of WM x WN 32x32 tiles; 64 VM VN threads; stage = 64 K values. Thread t dequantises half h = t & 1
+// of weight row t >> 1 of the stage (BN = 32 VN WN = NT / 2 rows).
+template <int VM, int VN, int WM, int WN, int QT, int MID, bool BIAS>
+__global__ __launch_bounds__(64 * VM * VN) void gemm_gguf(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
+                                                          const uint16_t* __restrict__ bias, uint16_t* __restrict__ Y,
+                                                          int M, int N, int K) {
+    constexpr int NT = 64 * VM * VN;
+    constexpr int BM = VM * WM * 32, BN = VN * WN * 32;
+    static_assert(BN * 2 == NT, "two threads per weight row");
     constexpr int TS = GGUFTs<QT>::TS;
-    constexpr int ACH = BM * 8 / 256;                  // 16-byte activation chunks per thread per stage
+    constexpr int ACH = BM * 8 / NT;                   // 16-byte activation chunks per thread per stage
     __shared__ uint4 lds[2][(BM + BN) * 8];
     const int ntm = (M + BM - 1) / BM, ntn = (N + BN - 1) / BN;
     int tm, tn;
     tile_order(blockIdx.x, ntm * ntn, ntm, ntn, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / VN, wn = wave % VN;
     const int nk = K / 64;
     const int sbs_per_row = K / 256;
-    const int wrow = n0 + tid;                         // this thread's weight row
-    const bool wlive = wrow < N;
-    const uint8_t* wrow_p = W + (int64_t)(wlive ? wrow : 0) * sbs_per_row * TS;
+    const int wr = tid >> 1, wh = tid & 1;             // this thread's weight row in the tile, and its half
+    const bool wlive = n0 + wr < N;
+    const uint8_t* wrow_p = W + (int64_t)(wlive ? n0 + wr : 0) * sbs_per_row * TS;
+    const __amdgpu_buffer_rsrc_t xr = rows_rsrc(X + (int64_t)m0 * K, (int64_t)(M - m0) * K * 2);
 
-    uint4 ra[ACH];
-    StageRaw<QT> rw;
-    auto gload = [&](int kt) {
-        const int k0 = kt * 64;
+    uint32_t xoff[ACH];
+    int xslot[ACH];
 #pragma unroll
-        for (int i = 0; i < ACH; i++) {
-            const int idx = tid + 256 * i, r = idx >> 3, c = idx & 7;
-            const int gm = m0 + r;
-            ra[i] = gm < M ? *reinterpret_cast<const uint4*>(X + (int64_t)gm * K + k0 + 8 * c) : make_uint4(0, 0, 0, 0);
-        }
-        if (wlive) raw_load<QT>(wrow_p + (kt >> 2) * TS, kt & 3, rw);
+    for (int i = 0; i < ACH; i++) {
+        const int idx = tid + NT * i, r = idx >> 3, c = idx & 7;
+        xoff[i] = (uint32_t)(r * K + 8 * c) * 2u;
+        xslot[i] = r * 8 + swz8(r, c);
+    }
+    uint4 ra[ACH];
+    HalfRaw<QT> rw;
+    auto gload = [&](int kt) {
+        const uint32_t k0 = (uint32_t)kt * 128u;       // bytes of bf16
+#pragma unroll
+        for (int i = 0; i < ACH; i++)
+            ra[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[i] + k0, 0, 0));
+        if (wlive) half_load<QT>(wrow_p + (kt >> 2) * TS, kt & 3, wh, rw);
     };
     auto lstore = [&](int buf, int kt) {
-        uint4* sa = lds[buf];
-        uint4* sb = lds[buf] + BM * 8;
 #pragma unroll
-        for (int i = 0; i < ACH; i++) {
-            const int idx = tid + 256 * i, r = idx >> 3, c = idx & 7;
-            sa[r * 8 + swz8(r, c)] = ra[i];
-        }
-        uint32_t o[32];
+        for (int i = 0; i < ACH; i++) lds[buf][xslot[i]] = ra[i];
+        uint32_t o[16];
         if (wlive) {
-            raw_dequant<QT, MID>(rw, kt & 3, o);
+            half_dequant<QT, MID>(rw, kt & 3, wh, o);
         } else {
 #pragma unroll
-            for (int i = 0; i < 32; i++) o[i] = 0;
+            for (int i = 0; i < 16; i++) o[i] = 0;
         }
+        uint4* sb = lds[buf] + BM * 8 + wr * 8;
 #pragma unroll
-        for (int c = 0; c < 8; c++) sb[tid * 8 + swz8(tid, c)] = make_uint4(o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]);
+        for (int c = 0; c < 4; c++)
+            sb[swz8(wr, 4 * wh + c)] = make_uint4(o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]);
+    };
+    const int lr = lane & 31, lk = lane >> 5;
+    int arow[WM], brow[WN];
+#pragma unroll
+    for (int i = 0; i < WM; i++) arow[i] = wm * WM * 32 + i * 32 + lr;
+#pragma unroll
+    for (int j = 0; j < WN; j++) brow[j] = wn * WN * 32 + j * 32 + lr;
+    bf16x8 fa[2][WM], fb[2][WN];
+    auto fread = [&](int buf, int ks, int set) {
+        const int ch = 2 * ks + lk;
+        const uint4* sa = lds[buf];
+        const uint4* sb = lds[buf] + BM * 8;
+#pragma unroll
+        for (int i = 0; i < WM; i++) fa[set][i] = __builtin_bit_cast(bf16x8, sa[arow[i] * 8 + swz8(arow[i], ch)]);
+#pragma unroll
+        for (int j = 0; j < WN; j++) fb[set][j] = __builtin_bit_cast(bf16x8, sb[brow[j] * 8 + swz8(brow[j], ch)]);
     };
 
-    f32x16 acc[WT][WT];
+    f32x16 acc[WM][WN];
 #pragma unroll
-    for (int i = 0; i < WT; i++)
+    for (int i = 0; i < WM; i++)
 #pragma unroll
-        for (int j = 0; j < WT; j++)
+        for (int j = 0; j < WN; j++)
 #pragma unroll
             for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
 
     gload(0);
     lstore(0, 0);
     __syncthreads();
-    const int lr = lane & 31, lk = lane >> 5;
+    fread(0, 0, 0);
     for (int kt = 0; kt < nk; kt++) {
         const int cur = kt & 1;
-        if (kt + 1 < nk) gload(kt + 1);
-        const uint4* sa = lds[cur];
-        const uint4* sb = lds[cur] + BM * 8;
+        const bool more = kt + 1 < nk;
+        if (more) gload(kt + 1);
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            const int ch = 2 * ks + lk;
-            bf16x8 af[WT], bf[WT];
+            const int set = ks & 1;
+            if (ks < 3) fread(cur, ks + 1, set ^ 1);
 #pragma unroll
-            for (int i = 0; i < WT; i++) {
-                const int r = wm * WT * 32 + i * 32 + lr;
-                af[i] = __builtin_bit_cast(bf16x8, sa[r * 8 + swz8(r, ch)]);
-            }
+            for (int i = 0; i < WM; i++)
 #pragma unroll
-            for (int j = 0; j < WT; j++) {
-                const int r = wn * WT * 32 + j * 32 + lr;
-                bf[j] = __builtin_bit_cast(bf16x8, sb[r * 8 + swz8(r, ch)]);
-            }
-#pragma unroll
-            for (int i = 0; i < WT; i++)
-#pragma unroll
-                for (int j = 0; j < WT; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < WN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
+            if (ks == 2 && more) lstore(cur ^ 1, kt + 1);  // the other buffer: nobody reads it in this stage
         }
-        if (kt + 1 < nk) lstore(cur ^ 1, kt + 1);
-        __syncthreads();
+        if (more) {
+            __syncthreads();
+            fread(cur ^ 1, 0, 0);
+        }
     }
 
 #pragma unroll
-    for (int j = 0; j < WT; j++) {
-        const int n = n0 + wn * WT * 32 + j * 32 + lr;
+    for (int j = 0; j < WN; j++) {
+        const int n = n0 + wn * WN * 32 + j * 32 + lr;
         if (n >= N) continue;
         const float bn = BIAS ? __uint_as_float((uint32_t)bias[n] << 16) : 0.0f;
 #pragma unroll
-        for (int i = 0; i < WT; i++) {
+        for (int i = 0; i < WM; i++) {
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                const int m = m0 + wm * WT * 32 + i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
+                const int m = m0 + wm * WM * 32 + i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
                 if (m >= M) continue;
                 float t = acc[i][j][e];
                 if (BIAS) t = t + bn;
@@ -299,9 +299,10 @@ __global__ __launch_bounds__(256) void gemm_gguf(const uint16_t* __restrict__ X,
 template <int QT, int MID>
 static void launch(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
                    hipStream_t s) {
+    // 8 waves (2 x 4) of 4 x 2 tiles: a 256 x 256 tile, two waves per SIMD
     const int tiles = ((M + 255) / 256) * ((N + 255) / 256);
-    if (bias) gemm_gguf<QT, MID, true><<<dim3(tiles), 256, 0, s>>>(X, W, bias, Y, M, N, K);
-    else gemm_gguf<QT, MID, false><<<dim3(tiles), 256, 0, s>>>(X, W, bias, Y, M, N, K);
+    if (bias) gemm_gguf<2, 4, 4, 2, QT, MID, true><<<dim3(tiles), 512, 0, s>>>(X, W, bias, Y, M, N, K);
+    else gemm_gguf<2, 4, 4, 2, QT, MID, false><<<dim3(tiles), 512, 0, s>>>(X, W, bias, Y, M, N, K);
 }
 
 template <int QT>
