@@ -4,14 +4,16 @@
 // The reference does the dequantisation into a bf16 weight in HBM and then ComfyUI-GGUF's F.linear; here the
 // weight never leaves the chip in bf16.
 //
-// Tiling: a 512-thread workgroup computes a 256 x 256 tile with 2 x 4 waves of 128 x 64 (4 x 2 tiles of
-// v_mfma_f32_32x32x16_bf16), two waves per SIMD, so one wave's dequantisation runs while the other's MFMAs do.
-// K advances in stages of 64 (128 bytes of bf16 per row): the activation stage comes in through buffer loads one
-// stage ahead (rows past M read as zeros); for the weight stage, threads 2r and 2r + 1 take the two halves of row
-// n0 + r -- for Q4_K / Q5_K exactly one 32-value sub-block each -- and dequantise them from the raw blocks, loaded
-// one stage ahead. Both land in double-buffered LDS with a 16-byte chunk swizzle that is conflict-free for writes and
-// fragment reads. Fragment layout: lane l holds 8 bf16 of row l % 32 at K offset 8 * (l / 32) of the 16-wide step;
-// result layout: lane l, register i -> row 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32.
+// Tiling: a 256-thread workgroup computes a 256 x 128 tile with 2 x 2 waves of 128 x 64 (4 x 2 tiles of
+// v_mfma_f32_32x32x16_bf16), and two workgroups share a CU (48 KB of LDS and at most 256 registers per lane each),
+// so one workgroup's barrier waits, dequantisation and LDS writes run while the other's MFMAs do. K advances in
+// stages of 64 (128 bytes of bf16 per row): the next stage's activations (buffer loads; rows past M read as zeros)
+// and raw weight blocks come into registers while the current stage's MFMAs run; after a barrier the stage is
+// written to the single LDS tile -- threads 2r and 2r + 1 take the two halves of weight row n0 + r (for Q4_K / Q5_K
+// exactly one 32-value sub-block each) and dequantise them on the way -- and a second barrier publishes it. A
+// 16-byte chunk swizzle keeps the LDS writes and fragment reads conflict-free. Fragment layout: lane l holds 8 bf16
+// of row l % 32 at K offset 8 * (l / 32) of the 16-wide step; result layout: lane l, register i -> row
+// 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32.
 
 #include "kquant.h"
 
@@ -171,9 +173,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, in
 }
 
 // VM x VN waves of WM x WN 32x32 tiles; 64 VM VN threads; stage = 64 K values. Thread t dequantises half h = t & 1
-// of weight row t >> 1 of the stage (BN = 32 VN WN = NT / 2 rows).
-template <int VM, int VN, int WM, int WN, int QT, int MID, bool BIAS>
-__global__ __launch_bounds__(64 * VM * VN) void gemm_gguf(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
+// of weight row t >> 1 of the stage (BN = 32 VN WN = NT / 2 rows). WPE workgroups' waves share each SIMD.
+template <int VM, int VN, int WM, int WN, int QT, int MID, bool BIAS, int WPE>
+__global__ __launch_bounds__(64 * VM * VN) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void gemm_gguf(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
                                                           const uint16_t* __restrict__ bias, uint16_t* __restrict__ Y,
                                                           int M, int N, int K) {
     constexpr int NT = 64 * VM * VN;
@@ -181,7 +183,7 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_gguf(const uint16_t* __rest
     static_assert(BN * 2 == NT, "two threads per weight row");
     constexpr int TS = GGUFTs<QT>::TS;
     constexpr int ACH = BM * 8 / NT;                   // 16-byte activation chunks per thread per stage
-    __shared__ uint4 lds[2][(BM + BN) * 8];
+    __shared__ uint4 lds[(BM + BN) * 8];
     const int ntm = (M + BM - 1) / BM, ntn = (N + BN - 1) / BN;
     int tm, tn;
     tile_order(blockIdx.x, ntm * ntn, ntm, ntn, tm, tn);
@@ -212,9 +214,9 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_gguf(const uint16_t* __rest
             ra[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[i] + k0, 0, 0));
         if (wlive) half_load<QT>(wrow_p + (kt >> 2) * TS, kt & 3, wh, rw);
     };
-    auto lstore = [&](int buf, int kt) {
+    auto lstore = [&](int kt) {
 #pragma unroll
-        for (int i = 0; i < ACH; i++) lds[buf][xslot[i]] = ra[i];
+        for (int i = 0; i < ACH; i++) lds[xslot[i]] = ra[i];
         uint32_t o[16];
         if (wlive) {
             half_dequant<QT, MID>(rw, kt & 3, wh, o);
@@ -222,7 +224,7 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_gguf(const uint16_t* __rest
 #pragma unroll
             for (int i = 0; i < 16; i++) o[i] = 0;
         }
-        uint4* sb = lds[buf] + BM * 8 + wr * 8;
+        uint4* sb = lds + BM * 8 + wr * 8;
 #pragma unroll
         for (int c = 0; c < 4; c++)
             sb[swz8(wr, 4 * wh + c)] = make_uint4(o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]);
@@ -234,10 +236,10 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_gguf(const uint16_t* __rest
 #pragma unroll
     for (int j = 0; j < WN; j++) brow[j] = wn * WN * 32 + j * 32 + lr;
     bf16x8 fa[2][WM], fb[2][WN];
-    auto fread = [&](int buf, int ks, int set) {
+    auto fread = [&](int ks, int set) {
         const int ch = 2 * ks + lk;
-        const uint4* sa = lds[buf];
-        const uint4* sb = lds[buf] + BM * 8;
+        const uint4* sa = lds;
+        const uint4* sb = lds + BM * 8;
 #pragma unroll
         for (int i = 0; i < WM; i++) fa[set][i] = __builtin_bit_cast(bf16x8, sa[arow[i] * 8 + swz8(arow[i], ch)]);
 #pragma unroll
@@ -253,27 +255,27 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_gguf(const uint16_t* __rest
             for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
 
     gload(0);
-    lstore(0, 0);
+    lstore(0);
     __syncthreads();
-    fread(0, 0, 0);
+    fread(0, 0);
     for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
         const bool more = kt + 1 < nk;
         if (more) gload(kt + 1);
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             const int set = ks & 1;
-            if (ks < 3) fread(cur, ks + 1, set ^ 1);
+            if (ks < 3) fread(ks + 1, set ^ 1);
 #pragma unroll
             for (int i = 0; i < WM; i++)
 #pragma unroll
                 for (int j = 0; j < WN; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
-            if (ks == 2 && more) lstore(cur ^ 1, kt + 1);  // the other buffer: nobody reads it in this stage
         }
         if (more) {
+            __syncthreads();          // every wave is done reading this stage
+            lstore(kt + 1);
             __syncthreads();
-            fread(cur ^ 1, 0, 0);
+            fread(0, 0);
         }
     }
 
@@ -299,10 +301,10 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_gguf(const uint16_t* __rest
 template <int QT, int MID>
 static void launch(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
                    hipStream_t s) {
-    // 8 waves (2 x 4) of 4 x 2 tiles: a 256 x 256 tile, two waves per SIMD
-    const int tiles = ((M + 255) / 256) * ((N + 255) / 256);
-    if (bias) gemm_gguf<2, 4, 4, 2, QT, MID, true><<<dim3(tiles), 512, 0, s>>>(X, W, bias, Y, M, N, K);
-    else gemm_gguf<2, 4, 4, 2, QT, MID, false><<<dim3(tiles), 512, 0, s>>>(X, W, bias, Y, M, N, K);
+    // 4 waves (2 x 2) of 4 x 2 tiles: a 256 x 128 tile, two workgroups per CU
+    const int tiles = ((M + 255) / 256) * ((N + 127) / 128);
+    if (bias) gemm_gguf<2, 2, 4, 2, QT, MID, true, 2><<<dim3(tiles), 256, 0, s>>>(X, W, bias, Y, M, N, K);
+    else gemm_gguf<2, 2, 4, 2, QT, MID, false, 2><<<dim3(tiles), 256, 0, s>>>(X, W, bias, Y, M, N, K);
 }
 
 template <int QT>
