@@ -12,6 +12,8 @@ Other rows of the workload list are reported under "also":
     per-channel int8 weights, int32 accumulation, bf16 out), and the row quantiser;
   * fused Q5_K / Q6_K dequant + bf16 GEMM over the linears of one Wan-2.1-14B block at 4096 tokens, next to the
     two-step flow (wf_dequant, then torch's bf16 GEMM);
+  * the LoRA add on a Q4_K 13824 x 5120 weight: the first LoRA fused into the dequantisation and a later LoRA
+    onto the bf16 weight (float32 difference of n values each);
   * 40 streamed Wan-14B blocks of Q4_K from pinned host memory through 2 GPU slots, 4096 tokens (ms/step, H2D
     GB/s, share of the copy time hidden behind compute).
 
@@ -165,6 +167,37 @@ def _log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def lora_leg(torch, native, raw, shape, steps=20):
+    """wf_dequant_add on one Q4_K weight (MID float16 -> bf16): the first LoRA inside the dequantisation (blocks +
+    float32 difference in, bf16 out) and a later LoRA onto the weight (bf16 + difference in, bf16 out). Two copies
+    of every buffer alternate (1.2 GB in all), so the last-level cache does not serve a call's bytes to the next."""
+    lib = native.lib()
+    dev = torch.device("cuda:0")
+    stream = native.stream_of(dev)
+    n = shape[0] * shape[1]
+    g = torch.Generator(device=dev).manual_seed(1234)
+    bufs = [(torch.from_numpy(raw).to(dev), torch.randn(n, generator=g, device=dev) * 0.01,
+             torch.empty(n, dtype=torch.bfloat16, device=dev)) for _ in range(2)]
+    res = {}
+    for name, first in (("first_lora_fused_into_dequant", True), ("later_lora_onto_weight", False)):
+        turn = [0]
+
+        def call():
+            rw, df, out = bufs[turn[0] % 2]
+            turn[0] += 1
+            rc = lib.wf_dequant_add(rw.data_ptr() if first else None, rw.numel() if first else 0, 12, 0, 1,
+                                    df.data_ptr(), 0.5, out.data_ptr(), n, stream)
+            if rc != 0:
+                raise RuntimeError(native.last_error())
+        ms = _timed(torch, call, steps, 3)
+        nbytes = (raw.size + 4 * n + 2 * n) if first else (2 * n + 4 * n + 2 * n)
+        res[name] = {"GB/s": round(nbytes / (ms / 1e3) / 1e9, 1), "kernel_us": round(ms * 1e3, 1),
+                     "frac": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 3), "bytes": nbytes}
+    del bufs
+    torch.cuda.empty_cache()
+    return res
+
+
 def dequant_leg(torch, native, raws, shapes, qtype, mid, out_dt, steps, warmup):
     """Time `steps` steps of dequantising every matrix once, launched back to back on torch's current stream with
     events at both ends of the timed region on that stream. Returns (ms per step, mean ms per launch, bytes/step);
@@ -294,6 +327,8 @@ def main():
         also[name] = {"GB/s": round(a8 / (k8 / 1e3) / 1e9, 1), "kernel_us": round(k8 * 1e3, 2),
                       "frac": round(a8 / (k8 / 1e3) / 1e9 / HBM_PEAK_GBS, 3), "bytes": a8}
     if not args.only_headline:
+        also["lora_add_q4_k_13824x5120"] = lora_leg(torch, native, raws[0], shapes[0])
+        _log("lora leg done")
         also["int8_w8a8"] = int8_leg(torch, native)
         _log("int8 leg done")
         also["fused_dequant_gemm_wan_block"] = fused_leg(torch, native)

@@ -25,6 +25,7 @@ EXPORTS = {
     "wf_abi_version": (_int, []),
     "wf_last_error": (ctypes.c_char_p, []),
     "wf_dequant": (_int, [_p, _i64, _int, _int, _int, _p, _i64, _p]),
+    "wf_dequant_add": (_int, [_p, _i64, _int, _int, _int, _p, ctypes.c_float, _p, _i64, _p]),
     "wf_quant_rows_i8": (_int, [_p, _i64, _i64, _int, _p, _p, _p]),
     "wf_linear_i8": (_int, [_p, _p, _p, _p, _p, _p, _int, _i64, _i64, _i64, _p]),
     "wf_linear_i8_residual": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p]),

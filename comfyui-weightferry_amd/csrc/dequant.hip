@@ -79,18 +79,59 @@ __device__ __forceinline__ void store8h(void* out, int64_t e0, const h2 (&v)[4])
     }
 }
 
-// Every fast kernel is a Format with load(src, t) -> Raw (only global loads) and emit(out, t, Raw) (arithmetic and
+// Where a lane-item's 8 values (MID values held in float32, or float16 pairs for MID = f16) go. ToOut: cast to OUT
+// and stored -- the dequantisation. AddDiff: the LoRA add of the reference's _deq_add (enhancers/gguf_dequant.py:
+// 99-133) fused behind it: w = OUT(x), then out = OUT(w + OUT(diff * sa)), each product and sum rounded on its own.
+struct ToOut {
+    void* out;
+    template <int OUT>
+    __device__ __forceinline__ void put(int64_t e0, const float (&v)[8]) const { store8<OUT>(out, e0, v); }
+    template <int OUT>
+    __device__ __forceinline__ void puth(int64_t e0, const h2 (&v)[4]) const { store8h<OUT>(out, e0, v); }
+};
+
+template <int OUT>
+__device__ __forceinline__ void add_scaled(float (&w)[8], const float* diff, float sa) {
+    const float4 d0 = *reinterpret_cast<const float4*>(diff), d1 = *reinterpret_cast<const float4*>(diff + 4);
+    const float d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++) w[i] = round_to<OUT>(w[i] + round_to<OUT>(d[i] * sa));
+}
+
+struct AddDiff {
+    void* out;
+    const float* diff;
+    float sa;
+    template <int OUT>
+    __device__ __forceinline__ void put(int64_t e0, const float (&v)[8]) const {
+        float w[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) w[i] = round_to<OUT>(v[i]);
+        add_scaled<OUT>(w, diff + e0, sa);
+        store8<OUT>(out, e0, w);
+    }
+    template <int OUT>
+    __device__ __forceinline__ void puth(int64_t e0, const h2 (&v)[4]) const {
+        float f[8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) { f[2 * i] = (float)v[i][0]; f[2 * i + 1] = (float)v[i][1]; }
+        put<OUT>(e0, f);
+    }
+};
+
+// Every fast kernel is a Format with load(src, t) -> Raw (only global loads) and emit(sink, t, Raw) (arithmetic and
 // stores) for lane-item t of one workgroup's tile; the driver issues the loads of DEQ_ITEMS items before emitting
 // any of them. A tile is DEQ_ITEMS * 256 lane-items = whole blocks, so the workgroup's block and output bases are
 // scalar and each lane works with 32-bit offsets. The grid covers every lane-item (no loop).
-template <typename F>
+template <typename F, bool ADD>
 __global__ __launch_bounds__(256) void deq_items(const uint8_t* __restrict__ src, void* __restrict__ out,
-                                                 int64_t nlanes) {
+                                                 int64_t nlanes, const float* __restrict__ diff, float sa) {
     constexpr int U = DEQ_ITEMS;
     constexpr int TILE_BLOCKS = U * 256 / F::LANES_PER_BLOCK;
     const int64_t t0 = (int64_t)blockIdx.x * (U * 256);
     const uint8_t* tsrc = src + (int64_t)blockIdx.x * TILE_BLOCKS * F::TS;
-    void* tout = static_cast<char*>(out) + (int64_t)blockIdx.x * TILE_BLOCKS * F::PER * F::OUT_BYTES;
+    const int64_t tval = (int64_t)blockIdx.x * TILE_BLOCKS * F::PER;     // first value of the tile
+    void* tout = static_cast<char*>(out) + tval * F::OUT_BYTES;
     typename F::Raw r[U];
 #pragma unroll
     for (int u = 0; u < U; u++) {
@@ -100,7 +141,10 @@ __global__ __launch_bounds__(256) void deq_items(const uint8_t* __restrict__ src
 #pragma unroll
     for (int u = 0; u < U; u++) {
         const uint32_t t = threadIdx.x + 256u * u;
-        if (t0 + t < nlanes) F::emit(tout, t, r[u]);
+        if (t0 + t < nlanes) {
+            if constexpr (ADD) F::emit(AddDiff{tout, diff + tval, sa}, t, r[u]);
+            else F::emit(ToOut{tout}, t, r[u]);
+        }
     }
 }
 
@@ -125,7 +169,8 @@ struct Q8_0 {
         r.q = funnel8(w0, w1, w2, sh);
         return r;
     }
-    static __device__ __forceinline__ void emit(void* out, uint32_t t, const Raw& r) {
+    template <class S>
+    static __device__ __forceinline__ void emit(const S& o, uint32_t t, const Raw& r) {
         const uint32_t e0 = t * 8;
         if constexpr (MID == WF_F16) {
             const h2 d2 = as_h2(r.d | (r.d << 16));
@@ -136,7 +181,7 @@ struct Q8_0 {
             v[1] = d2 * (biased_hi(u0) + bias);
             v[2] = d2 * (biased_lo(u1) + bias);
             v[3] = d2 * (biased_hi(u1) + bias);
-            store8h<OUT>(out, e0, v);
+            o.template puth<OUT>(e0, v);
         } else {
             const float d = round_to<MID>(f16_bits_to_f32(r.d));
             float v[8];
@@ -145,7 +190,7 @@ struct Q8_0 {
                 v[i] = round_to<MID>(d * (float)(int8_t)byte_of(r.q.x, i));
                 v[4 + i] = round_to<MID>(d * (float)(int8_t)byte_of(r.q.y, i));
             }
-            store8<OUT>(out, e0, v);
+            o.template put<OUT>(e0, v);
         }
     }
 };
@@ -175,7 +220,8 @@ struct Q45_K {
         if constexpr (QT == 13) r.qh = *reinterpret_cast<const uint2*>(base + 16 + 8 * c);
         return r;
     }
-    static __device__ __forceinline__ void emit(void* out, uint32_t t, const Raw& r) {
+    template <class S>
+    static __device__ __forceinline__ void emit(const S& o, uint32_t t, const Raw& r) {
         const uint32_t sb = t >> 4;
         const int j = (int)(t & 15), g = j >> 2;
         const uint32_t ns = 4u * (uint32_t)(g & 1);
@@ -207,8 +253,8 @@ struct Q45_K {
                 v2[2 * w] = ds2 * (biased_lo(n2[w]) + off) - dm2;
                 v2[2 * w + 1] = ds2 * (biased_hi(n2[w]) + off) - dm2;
             }
-            store8h<OUT>(out, e1, v1);
-            store8h<OUT>(out, e2, v2);
+            o.template puth<OUT>(e1, v1);
+            o.template puth<OUT>(e2, v2);
         } else {
             const float d = round_to<MID>(f16_bits_to_f32(r.hdr.x & 0xffffu));
             const float dmin = round_to<MID>(f16_bits_to_f32(r.hdr.x >> 16));
@@ -222,8 +268,8 @@ struct Q45_K {
                     v1[4 * w + i] = round_to<MID>(round_to<MID>(ds1 * (float)byte_of(n1[w], i)) - dm1);
                     v2[4 * w + i] = round_to<MID>(round_to<MID>(ds2 * (float)byte_of(n2[w], i)) - dm2);
                 }
-            store8<OUT>(out, e1, v1);
-            store8<OUT>(out, e2, v2);
+            o.template put<OUT>(e1, v1);
+            o.template put<OUT>(e2, v2);
         }
     }
 };
@@ -261,7 +307,8 @@ struct Q6_K {
         r.d = *reinterpret_cast<const uint16_t*>(src + b0 + 208);
         return r;
     }
-    static __device__ __forceinline__ void emit(void* out, uint32_t t, const Raw& r) {
+    template <class S>
+    static __device__ __forceinline__ void emit(const S& o, uint32_t t, const Raw& r) {
         const uint32_t sb = t >> 4;
         const int j = (int)(t & 15), h = j >> 3, c = j & 7;
         const uint32_t s1 = 2u * (uint32_t)(c >> 2), s2 = s1 + 4u;
@@ -288,8 +335,8 @@ struct Q6_K {
                 vb[2 * w] = dB * (biased_lo(hi[w]) + bias);
                 vb[2 * w + 1] = dB * (biased_hi(hi[w]) + bias);
             }
-            store8h<OUT>(out, eA, va);
-            store8h<OUT>(out, eB, vb);
+            o.template puth<OUT>(eA, va);
+            o.template puth<OUT>(eB, vb);
         } else {
             const float d = round_to<MID>(f16_bits_to_f32(r.d));
             const float dA = round_to<MID>(d * (float)(int8_t)r.sl), dB = round_to<MID>(d * (float)(int8_t)r.sh);
@@ -301,8 +348,8 @@ struct Q6_K {
                     va[4 * w + i] = round_to<MID>(dA * (float)((int)byte_of(lo[w], i) - 32));
                     vb[4 * w + i] = round_to<MID>(dB * (float)((int)byte_of(hi[w], i) - 32));
                 }
-            store8<OUT>(out, eA, va);
-            store8<OUT>(out, eB, vb);
+            o.template put<OUT>(eA, va);
+            o.template put<OUT>(eB, vb);
         }
     }
 };
@@ -353,9 +400,9 @@ __device__ __forceinline__ float deq_value(const uint8_t* b, int v) {
     }
 }
 
-template <int QT, int MID, int OUT>
+template <int QT, int MID, int OUT, bool ADD>
 __global__ __launch_bounds__(256) void deq_gather(const uint8_t* __restrict__ src, void* __restrict__ out,
-                                                  int64_t nlanes) {
+                                                  int64_t nlanes, const float* __restrict__ diff, float sa) {
     constexpr int TS = Fmt<QT>::TS, PER = Fmt<QT>::PER, LPB = PER / 8;
     for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < nlanes;
          t += (int64_t)gridDim.x * blockDim.x) {
@@ -365,7 +412,53 @@ __global__ __launch_bounds__(256) void deq_gather(const uint8_t* __restrict__ sr
         float v[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = deq_value<QT, MID>(b, v0 + i);
-        store8<OUT>(out, t * 8, v);
+        if constexpr (ADD) AddDiff{out, diff, sa}.template put<OUT>(t * 8, v);
+        else store8<OUT>(out, t * 8, v);
+    }
+}
+
+// out = OUT(out + OUT(diff * sa)) on n values already in out: the reference's _deq_add with DEQ off (a K-quant
+// dequantised by its own kernel first, or the second and later LoRAs, enhancers/gguf_dequant.py:387-409). Lane t
+// takes values [8t, 8t + 8); the last lane of a count that is not a multiple of 8 goes value by value.
+template <int OUT>
+__global__ __launch_bounds__(256) void add_diff(void* __restrict__ out, const float* __restrict__ diff, float sa,
+                                                int64_t n) {
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t * 8 < n; t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t e0 = t * 8;
+        if (e0 + 8 <= n) {
+            float w[8];
+            if constexpr (OUT == WF_F32) {
+                const float4 a = *reinterpret_cast<const float4*>(static_cast<float*>(out) + e0);
+                const float4 b = *reinterpret_cast<const float4*>(static_cast<float*>(out) + e0 + 4);
+                w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+            } else {
+                const uint4 a = *reinterpret_cast<const uint4*>(static_cast<uint16_t*>(out) + e0);
+                const uint32_t u[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    if constexpr (OUT == WF_BF16) {
+                        w[2 * i] = __uint_as_float(u[i] << 16);
+                        w[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+                    } else {
+                        w[2 * i] = f16_bits_to_f32(u[i] & 0xffffu);
+                        w[2 * i + 1] = f16_bits_to_f32(u[i] >> 16);
+                    }
+                }
+            }
+            add_scaled<OUT>(w, diff + e0, sa);
+            store8<OUT>(out, e0, w);
+        } else {
+            for (int64_t e = e0; e < n; e++) {
+                float w;
+                if constexpr (OUT == WF_F32) w = static_cast<float*>(out)[e];
+                else if constexpr (OUT == WF_BF16) w = __uint_as_float((uint32_t)static_cast<uint16_t*>(out)[e] << 16);
+                else w = f16_bits_to_f32(static_cast<uint16_t*>(out)[e]);
+                w = round_to<OUT>(w + round_to<OUT>(diff[e] * sa));
+                if constexpr (OUT == WF_F32) static_cast<float*>(out)[e] = w;
+                else if constexpr (OUT == WF_BF16) static_cast<uint16_t*>(out)[e] = __builtin_bit_cast(uint16_t, (__bf16)w);
+                else static_cast<uint16_t*>(out)[e] = __builtin_bit_cast(uint16_t, (_Float16)w);
+            }
+        }
     }
 }
 
@@ -385,35 +478,51 @@ static Launch plan(int64_t nlanes) {
 
 // grid of the tiled kernels: one workgroup per tile of DEQ_ITEMS * 256 lane-items, every tile launched (no loop);
 // wf_dequant bounds the value count so that this fits gridDim.x
-template <typename F>
-static void launch_items(const uint8_t* src, void* out, int64_t nblocks, hipStream_t s) {
+template <typename F, bool ADD>
+static void launch_items(const uint8_t* src, void* out, int64_t nblocks, const float* diff, float sa, hipStream_t s) {
     const int64_t nlanes = nblocks * F::LANES_PER_BLOCK;
     const int64_t wgs = (nlanes + 256LL * DEQ_ITEMS - 1) / (256LL * DEQ_ITEMS);
-    deq_items<F><<<dim3((unsigned)wgs), 256, 0, s>>>(src, out, nlanes);
+    deq_items<F, ADD><<<dim3((unsigned)wgs), 256, 0, s>>>(src, out, nlanes, diff, sa);
 }
 
-template <int MID, int OUT>
-static void launch_fmt(int qtype, const uint8_t* src, void* out, int64_t nblocks, hipStream_t s) {
+template <int QT, int MID, int OUT, bool ADD>
+static void launch_gather(const uint8_t* src, void* out, int64_t nblocks, const float* diff, float sa, hipStream_t s) {
+    const Launch L = plan(nblocks * (Fmt<QT>::PER / 8));
+    deq_gather<QT, MID, OUT, ADD><<<L.grid, 256, 0, s>>>(src, out, L.nlanes, diff, sa);
+}
+
+template <int MID, int OUT, bool ADD>
+static void launch_fmt(int qtype, const uint8_t* src, void* out, int64_t nblocks, const float* diff, float sa,
+                       hipStream_t s) {
     switch (qtype) {
-    case 8: launch_items<Q8_0<MID, OUT>>(src, out, nblocks, s); break;
-    case 12: launch_items<Q45_K<12, MID, OUT>>(src, out, nblocks, s); break;
-    case 13: launch_items<Q45_K<13, MID, OUT>>(src, out, nblocks, s); break;
-    case 14: launch_items<Q6_K<MID, OUT>>(src, out, nblocks, s); break;
-    case 2: { Launch L = plan(nblocks * 4); deq_gather<2, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
-    case 3: { Launch L = plan(nblocks * 4); deq_gather<3, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
-    case 6: { Launch L = plan(nblocks * 4); deq_gather<6, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
-    case 7: { Launch L = plan(nblocks * 4); deq_gather<7, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
-    case 10: { Launch L = plan(nblocks * 32); deq_gather<10, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
-    case 11: { Launch L = plan(nblocks * 32); deq_gather<11, MID, OUT><<<L.grid, 256, 0, s>>>(src, out, L.nlanes); break; }
+    case 8: launch_items<Q8_0<MID, OUT>, ADD>(src, out, nblocks, diff, sa, s); break;
+    case 12: launch_items<Q45_K<12, MID, OUT>, ADD>(src, out, nblocks, diff, sa, s); break;
+    case 13: launch_items<Q45_K<13, MID, OUT>, ADD>(src, out, nblocks, diff, sa, s); break;
+    case 14: launch_items<Q6_K<MID, OUT>, ADD>(src, out, nblocks, diff, sa, s); break;
+    case 2: launch_gather<2, MID, OUT, ADD>(src, out, nblocks, diff, sa, s); break;
+    case 3: launch_gather<3, MID, OUT, ADD>(src, out, nblocks, diff, sa, s); break;
+    case 6: launch_gather<6, MID, OUT, ADD>(src, out, nblocks, diff, sa, s); break;
+    case 7: launch_gather<7, MID, OUT, ADD>(src, out, nblocks, diff, sa, s); break;
+    case 10: launch_gather<10, MID, OUT, ADD>(src, out, nblocks, diff, sa, s); break;
+    case 11: launch_gather<11, MID, OUT, ADD>(src, out, nblocks, diff, sa, s); break;
     default: break;
     }
 }
 
-template <int MID>
-static void launch_mid(int out_dt, int qtype, const uint8_t* src, void* out, int64_t nblocks, hipStream_t s) {
-    if (out_dt == WF_F16) launch_fmt<MID, WF_F16>(qtype, src, out, nblocks, s);
-    else if (out_dt == WF_BF16) launch_fmt<MID, WF_BF16>(qtype, src, out, nblocks, s);
-    else launch_fmt<MID, WF_F32>(qtype, src, out, nblocks, s);
+template <int MID, bool ADD>
+static void launch_mid(int out_dt, int qtype, const uint8_t* src, void* out, int64_t nblocks, const float* diff,
+                       float sa, hipStream_t s) {
+    if (out_dt == WF_F16) launch_fmt<MID, WF_F16, ADD>(qtype, src, out, nblocks, diff, sa, s);
+    else if (out_dt == WF_BF16) launch_fmt<MID, WF_BF16, ADD>(qtype, src, out, nblocks, diff, sa, s);
+    else launch_fmt<MID, WF_F32, ADD>(qtype, src, out, nblocks, diff, sa, s);
+}
+
+template <bool ADD>
+static void launch_all(int mid_dt, int out_dt, int qtype, const uint8_t* src, void* out, int64_t nblocks,
+                       const float* diff, float sa, hipStream_t s) {
+    if (mid_dt == WF_F16) launch_mid<WF_F16, ADD>(out_dt, qtype, src, out, nblocks, diff, sa, s);
+    else if (mid_dt == WF_BF16) launch_mid<WF_BF16, ADD>(out_dt, qtype, src, out, nblocks, diff, sa, s);
+    else launch_mid<WF_F32, ADD>(out_dt, qtype, src, out, nblocks, diff, sa, s);
 }
 
 // bytes per block and values per block of a supported GGML type (0 when unsupported)
@@ -435,41 +544,78 @@ int block_bytes(int qtype, int* per) {
 
 }  // namespace wf
 
-extern "C" int wf_dequant(const void* src, int64_t src_bytes, int qtype, int mid_dt, int out_dt, void* out,
-                          int64_t n_values, void* stream) {
-    using namespace wf;
+namespace wf {
+// the checks wf_dequant and wf_dequant_add share; returns WF_OK and the block count, or the error code
+static int check_blocks(const char* who, const void* src, int64_t src_bytes, int qtype, int mid_dt, int out_dt,
+                        const void* out, int64_t n_values, int64_t* nblocks) {
     int per = 0;
     const int ts = block_bytes(qtype, &per);
-    if (!ts) { set_error("wf_dequant: GGML type %d is not handled", qtype); return WF_EUNSUPPORTED; }
+    if (!ts) { set_error("%s: GGML type %d is not handled", who, qtype); return WF_EUNSUPPORTED; }
     if (mid_dt < 0 || mid_dt > 2 || out_dt < 0 || out_dt > 2) {
-        set_error("wf_dequant: dtype codes %d / %d", mid_dt, out_dt);
+        set_error("%s: dtype codes %d / %d", who, mid_dt, out_dt);
         return WF_EUNSUPPORTED;
     }
     if (src_bytes < 0 || n_values < 0 || src_bytes % ts) {
-        set_error("wf_dequant: %lld bytes is not a whole number of %d-byte blocks", (long long)src_bytes, ts);
+        set_error("%s: %lld bytes is not a whole number of %d-byte blocks", who, (long long)src_bytes, ts);
         return WF_EUNSUPPORTED;
     }
-    const int64_t nblocks = src_bytes / ts;
-    if (nblocks * per != n_values) {
-        set_error("wf_dequant: %lld blocks hold %lld values, not %lld", (long long)nblocks,
-                  (long long)(nblocks * per), (long long)n_values);
+    *nblocks = src_bytes / ts;
+    if (*nblocks * per != n_values) {
+        set_error("%s: %lld blocks hold %lld values, not %lld", who, (long long)*nblocks,
+                  (long long)(*nblocks * per), (long long)n_values);
         return WF_EUNSUPPORTED;
     }
-    if (n_values == 0) return WF_OK;
     if (n_values > (int64_t)1 << 40) {   // keeps every tiled launch under 2^31 workgroups
-        set_error("wf_dequant: %lld values is beyond this build's limit of 2^40", (long long)n_values);
+        set_error("%s: %lld values is beyond this build's limit of 2^40", who, (long long)n_values);
         return WF_EUNSUPPORTED;
     }
-    if (!src || !out) { set_error("wf_dequant: null pointer"); return WF_EINVAL; }
+    if (n_values && (!src || !out)) { set_error("%s: null pointer", who); return WF_EINVAL; }
     if (!aligned(src, 16) || !aligned(out, 16)) {
-        set_error("wf_dequant: src and out must be 16-byte aligned");
+        set_error("%s: src and out must be 16-byte aligned", who);
         return WF_EUNSUPPORTED;
     }
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const uint8_t* p = static_cast<const uint8_t*>(src);
-    if (mid_dt == WF_F16) launch_mid<WF_F16>(out_dt, qtype, p, out, nblocks, s);
-    else if (mid_dt == WF_BF16) launch_mid<WF_BF16>(out_dt, qtype, p, out, nblocks, s);
-    else launch_mid<WF_F32>(out_dt, qtype, p, out, nblocks, s);
+    return WF_OK;
+}
+}  // namespace wf
+
+extern "C" int wf_dequant(const void* src, int64_t src_bytes, int qtype, int mid_dt, int out_dt, void* out,
+                          int64_t n_values, void* stream) {
+    using namespace wf;
+    int64_t nblocks = 0;
+    const int rc = check_blocks("wf_dequant", src, src_bytes, qtype, mid_dt, out_dt, out, n_values, &nblocks);
+    if (rc != WF_OK || n_values == 0) return rc;
+    launch_all<false>(mid_dt, out_dt, qtype, static_cast<const uint8_t*>(src), out, nblocks, nullptr, 0.0f,
+                      static_cast<hipStream_t>(stream));
     WF_LAUNCH_CHECK("wf_dequant launch");
+    return WF_OK;
+}
+
+extern "C" int wf_dequant_add(const void* src, int64_t src_bytes, int qtype, int mid_dt, int out_dt,
+                              const float* diff, float scale, void* out, int64_t n_values, void* stream) {
+    using namespace wf;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!src) {
+        if (out_dt < 0 || out_dt > 2) { set_error("wf_dequant_add: dtype code %d", out_dt); return WF_EUNSUPPORTED; }
+        if (n_values < 0) { set_error("wf_dequant_add: %lld values", (long long)n_values); return WF_EINVAL; }
+        if (n_values == 0) return WF_OK;
+        if (!out || !diff) { set_error("wf_dequant_add: null pointer"); return WF_EINVAL; }
+        if (!aligned(out, 16) || !aligned(diff, 16)) {
+            set_error("wf_dequant_add: out and diff must be 16-byte aligned");
+            return WF_EUNSUPPORTED;
+        }
+        const Launch L = plan((n_values + 7) / 8);
+        if (out_dt == WF_F16) add_diff<WF_F16><<<L.grid, 256, 0, s>>>(out, diff, scale, n_values);
+        else if (out_dt == WF_BF16) add_diff<WF_BF16><<<L.grid, 256, 0, s>>>(out, diff, scale, n_values);
+        else add_diff<WF_F32><<<L.grid, 256, 0, s>>>(out, diff, scale, n_values);
+        WF_LAUNCH_CHECK("wf_dequant_add launch");
+        return WF_OK;
+    }
+    int64_t nblocks = 0;
+    const int rc = check_blocks("wf_dequant_add", src, src_bytes, qtype, mid_dt, out_dt, out, n_values, &nblocks);
+    if (rc != WF_OK || n_values == 0) return rc;
+    if (!diff) { set_error("wf_dequant_add: null pointer"); return WF_EINVAL; }
+    if (!aligned(diff, 16)) { set_error("wf_dequant_add: diff must be 16-byte aligned"); return WF_EUNSUPPORTED; }
+    launch_all<true>(mid_dt, out_dt, qtype, static_cast<const uint8_t*>(src), out, nblocks, diff, scale, s);
+    WF_LAUNCH_CHECK("wf_dequant_add launch");
     return WF_OK;
 }

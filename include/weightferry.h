@@ -47,6 +47,16 @@ const char* wf_last_error(void);
 int wf_dequant(const void* src, int64_t src_bytes, int qtype, int mid_dt, int out_dt, void* out, int64_t n_values,
                void* stream);
 
+/* LoRA add on a GGUF weight: replaces the Triton kernel `_deq_add` (enhancers/gguf_dequant.py:99-133) as
+ * `_add_loras` launches it once per LoRA (:387-409). out[i] = OUT(w + OUT(diff[i] * scale)) for i < n_values, the
+ * product, the sum and each rounding on their own; w is the dequantisation of `src` exactly as wf_dequant gives it
+ * (the first LoRA, DEQ on) when src is not NULL, else the value already in out (a later LoRA; qtype, src_bytes
+ * and mid_dt are then ignored). diff: float32 [n_values], comfy's up @ down of one LoRA; scale = strength *
+ * alpha / rank. The reference dequantises a K-quant by its own kernel and adds every LoRA afterwards; here the
+ * first add is fused into the K-quant dequantisation too (the same values). out and diff 16-byte aligned. */
+int wf_dequant_add(const void* src, int64_t src_bytes, int qtype, int mid_dt, int out_dt, const float* diff,
+                   float scale, void* out, int64_t n_values, void* stream);
+
 /* ---------------------------------------------------------------------------------------------- int8 W8A8 path
  * Per-row int8 quantisation of bf16 activations: replaces the Triton `_quant_row` with PRE_NONE
  * (enhancers/fused_kernels.py:137-174, launched at enhancers/fused_int8.py:172-176) and kitchen's

@@ -41,6 +41,8 @@ def load():
         lib.wfo_scale_min.restype = None
         lib.wfo_dequant.argtypes = [p, i64, c_int, c_int, c_int, p, i64]
         lib.wfo_dequant.restype = c_int
+        lib.wfo_dequant_add.argtypes = [p, i64, c_int, c_int, c_int, p, ctypes.c_float, p, i64]
+        lib.wfo_dequant_add.restype = c_int
         lib.wfo_quant_rows.argtypes = [p, i64, i64, c_int, p, p, p]
         lib.wfo_quant_rows.restype = c_int
         lib.wfo_linear_i8.argtypes = [p, p, p, p, p, p, c_int, i64, i64, i64, p]
@@ -69,6 +71,25 @@ def dequant(raw, qtype, mid, out, n):
     rc = load().wfo_dequant(_ptr(raw), raw.size, qtype, mid, out, _ptr(dst), n)
     if rc != 0:
         raise ValueError(f"oracle dequant rejected the input (rc={rc})")
+    return dst
+
+
+def dequant_add(raw, qtype, mid, out, diff, sa, base=None):
+    """wfo_dequant_add: the LoRA add of one difference ``diff`` (float32, n values) scaled by ``sa``, onto the
+    dequantisation of ``raw`` when it is given (the first LoRA), else onto ``base`` (values of dtype ``out``: uint16
+    bits for f16/bf16, float32 for f32)."""
+    diff = np.ascontiguousarray(diff, dtype=np.float32).ravel()
+    n = diff.size
+    if raw is None:
+        dst = np.array(base, dtype=NP_OUT[out]).ravel().copy()
+        assert dst.size == n
+        rc = load().wfo_dequant_add(None, 0, 0, 0, out, _ptr(diff), float(sa), _ptr(dst), n)
+    else:
+        raw = np.ascontiguousarray(raw, dtype=np.uint8)
+        dst = np.empty(n, dtype=NP_OUT[out])
+        rc = load().wfo_dequant_add(_ptr(raw), raw.size, qtype, mid, out, _ptr(diff), float(sa), _ptr(dst), n)
+    if rc != 0:
+        raise ValueError(f"oracle dequant_add rejected the input (rc={rc})")
     return dst
 
 

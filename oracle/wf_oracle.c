@@ -8,6 +8,7 @@
  *   - rounding helpers            enhancers/gguf_dequant.py:72-96
  *   - legacy 32-value blocks      enhancers/gguf_dequant.py:52-54,136-167
  *   - K-quant 256-value blocks    enhancers/gguf_dequant.py:56,170-256
+ *   - LoRA add (_deq_add)         enhancers/gguf_dequant.py:99-133,387-409
  *   - int8 row quantiser          enhancers/fused_kernels.py:44-49,65-81,137-174
  *   - int8 linear epilogue        enhancers/fused_int8.py:191-206 (order of the epilogue fixed by this build)
  *
@@ -200,6 +201,31 @@ int wfo_dequant(const uint8_t* src, int64_t nbytes, int qtype, int MID, int OUT,
     for (int64_t blk = 0; blk < n / 256; blk++)
         for (int v = 0; v < 256; v++)
             store_dt(dst, blk * 256 + v, deq_k(src + blk * ts, qtype, v, MID, OUT), OUT);
+    return 0;
+}
+
+/* ---------------------------------------------------------------------------------------------- LoRA add */
+
+/* value i of dtype D at dst, widened exactly to float32 */
+static inline float load_dt(const void* dst, int64_t i, int D) {
+    if (D == 0) return wfo_f16_bits_to_f32(((const uint16_t*)dst)[i]);
+    if (D == 1) return u2f((uint32_t)((const uint16_t*)dst)[i] << 16);
+    return ((const float*)dst)[i];
+}
+
+/* _deq_add of enhancers/gguf_dequant.py:99-133 on a flat weight of n values, as _add_loras launches it (:387-409):
+ * w = the dequantised value (the chain of wfo_dequant, rounded to OUT) when src is not NULL (DEQ), else the OUT
+ * value already in dst; then dst = R_OUT(w + R_OUT(diff * sa)) -- the product, its rounding, the sum and its
+ * rounding each on their own (:127). Returns 0, or -1 when the blocks do not hold n values. */
+int wfo_dequant_add(const uint8_t* src, int64_t nbytes, int qtype, int MID, int OUT, const float* diff, float sa,
+                    void* dst, int64_t n) {
+    if (OUT < 0 || OUT > 2) return -1;
+    if (src && wfo_dequant(src, nbytes, qtype, MID, OUT, dst, n)) return -1;
+    for (int64_t i = 0; i < n; i++) {
+        const float w = load_dt(dst, i, OUT);
+        const float p = diff[i] * sa;
+        store_dt(dst, i, wfo_round(w + wfo_round(p, OUT), OUT), OUT);
+    }
     return 0;
 }
 

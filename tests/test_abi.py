@@ -51,6 +51,25 @@ def test_argument_checks_without_gpu():
     assert lib.wf_dequant(p16, 0, 12, 0, 1, p16, 0, None) == native.OK
 
 
+def test_dequant_add_argument_checks_without_gpu():
+    native = sub("_native")
+    lib = native.lib()
+    buf = ctypes.create_string_buffer(8192)
+    p16 = (ctypes.addressof(buf) + 15) // 16 * 16
+    # the same block checks as wf_dequant when the weight is dequantised first
+    assert lib.wf_dequant_add(p16, 144, 99, 0, 1, p16, 0.5, p16, 256, None) == native.EUNSUPPORTED
+    assert lib.wf_dequant_add(p16, 144, 12, 0, 1, p16, 0.5, p16, 255, None) == native.EUNSUPPORTED
+    assert lib.wf_dequant_add(p16, 144, 12, 0, 1, None, 0.5, p16, 256, None) == native.EINVAL
+    assert lib.wf_dequant_add(p16, 144, 12, 0, 1, p16 + 4, 0.5, p16, 256, None) == native.EUNSUPPORTED
+    assert "aligned" in native.last_error()
+    # a later LoRA (no blocks): only the output dtype, the pointers and their alignment matter
+    assert lib.wf_dequant_add(None, 0, 0, 0, 3, p16, 0.5, p16, 8, None) == native.EUNSUPPORTED
+    assert lib.wf_dequant_add(None, 0, 0, 0, 1, None, 0.5, p16, 8, None) == native.EINVAL
+    assert lib.wf_dequant_add(None, 0, 0, 0, 1, p16, 0.5, p16 + 2, 8, None) == native.EUNSUPPORTED
+    assert lib.wf_dequant_add(None, 0, 0, 0, 1, p16, 0.5, p16, -1, None) == native.EINVAL
+    assert lib.wf_dequant_add(None, 0, 0, 0, 1, None, 0.5, None, 0, None) == native.OK
+
+
 def test_check_maps_codes():
     native = sub("_native")
     assert native.check(native.OK, "x") is True
