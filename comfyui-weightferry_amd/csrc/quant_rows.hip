@@ -15,6 +15,15 @@
 // correctly rounded reciprocal of s (one IEEE division per row) and one Markstein correction step -- mul, then two
 // fma -- which is the correctly rounded IEEE quotient for every normal result (subnormal quotients round to 0 in the
 // integer anyway). Built without contraction; the fma calls are explicit.
+//
+// ConvRot rows may first go through the operation the reference's quantiser applies before its rotation (PRE,
+// enhancers/fused_kernels.py:14-18,143-163): GELU by table lookup (torch's GELU of every bf16 value), the
+// scale-and-shift bf16(bf16(x * s1) + shift) of the row's group, or LayerNorm without affine, rounded to bf16, and
+// then the scale-and-shift. The LayerNorm statistics follow the reference's Welford order (:97-136): 128 virtual
+// threads, thread t updating (mean, sigma2, count) over the 4-value vectors t, t + 128, ... of the row, then
+// shuffle-down merges within 32-thread warps (16, 8, 4, 2, 1) and across warps (2, 3 into 0, 1; 1 into 0). Lane l
+// of the wave plays virtual threads l and l + 64. rstd = 1 / sqrt(var + eps) correctly rounded (the reference's
+// rsqrt.approx.f32 is an NVIDIA approximation).
 
 #include "wf_common.h"
 
@@ -56,6 +65,62 @@ __device__ __forceinline__ RowScale row_scale(float amax) {
     r.sb = round_bf16(r.scale);
     r.rsb = 1.0f / r.sb;
     return r;
+}
+
+// ----------------------------------------------------------------------------------------- operations (PRE)
+struct PreArgs {
+    const uint16_t* s;        // GELU: bf16 table [65536]; MOD / LNMOD: bf16 s1 = 1 + scale, [groups, K]
+    const uint16_t* h;        // MOD / LNMOD: bf16 shift, [groups, K]
+    int64_t rows_per_group;
+    float eps;                // LNMOD
+};
+
+// PyTorch's cuWelfordCombine(dataB = own, dataA = other) as the reference restates it, with the contractions it
+// makes explicit (enhancers/fused_kernels.py:84-94)
+__device__ __forceinline__ void wcombine(float& m, float& s, float& c, float mo, float so, float co) {
+    const float delta = m - mo;
+    const float count = co + c;
+    const float coef = 1.0f / count;
+    const float na = co * coef, nb = c * coef;
+    const float mean = __builtin_fmaf(na, mo, nb * m);
+    const float sig = __builtin_fmaf((delta * delta) * co, nb, so + s);
+    m = mean; s = sig; c = count;
+}
+
+// mean and sigma2 / K of one row (K % 512 == 0), every lane gets the result
+__device__ __forceinline__ void ln_stats(const uint16_t* xr, int K, int lane, float& mu, float& var) {
+    float m[2] = {0.0f, 0.0f}, sg[2] = {0.0f, 0.0f}, c[2] = {0.0f, 0.0f};
+    for (int j = 0; j < (K >> 9); j++) {
+#pragma unroll
+        for (int vt = 0; vt < 2; vt++) {
+            const int t = lane + 64 * vt;
+            const uint2 w = *reinterpret_cast<const uint2*>(xr + 4 * (t + 128 * j));
+            const float v4[4] = {bf16_bits_to_f32(w.x & 0xffffu), bf16_bits_to_f32(w.x >> 16),
+                                 bf16_bits_to_f32(w.y & 0xffffu), bf16_bits_to_f32(w.y >> 16)};
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) {
+                const float delta = v4[ii] - m[vt];
+                c[vt] = c[vt] + 1.0f;
+                m[vt] = __builtin_fmaf(delta, 1.0f / c[vt], m[vt]);
+                sg[vt] = __builtin_fmaf(delta, v4[ii] - m[vt], sg[vt]);
+            }
+        }
+    }
+    // within each 32-thread virtual warp: lane i < o merges lane i + o
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) {
+#pragma unroll
+        for (int vt = 0; vt < 2; vt++) {
+            const float mo = __shfl_down(m[vt], o, 32), so = __shfl_down(sg[vt], o, 32), co = __shfl_down(c[vt], o, 32);
+            if ((lane & 31) < o) wcombine(m[vt], sg[vt], c[vt], mo, so, co);
+        }
+    }
+    // warps 2, 3 (lanes 0, 32 of the second virtual thread) into warps 0, 1; then warp 1 (lane 32) into warp 0
+    wcombine(m[0], sg[0], c[0], m[1], sg[1], c[1]);
+    const float mo = __shfl(m[0], 32, 64), so = __shfl(sg[0], 32, 64), co = __shfl(c[0], 32, 64);
+    wcombine(m[0], sg[0], c[0], mo, so, co);
+    mu = __shfl(m[0], 0, 64);
+    var = __shfl(sg[0], 0, 64) / (float)K;
 }
 
 // ------------------------------------------------------------------------------------------------ plain rows
@@ -116,9 +181,9 @@ __device__ __forceinline__ int slot(int g, int i) { return g * 272 + i + (i >> 4
 
 // NP passes of 4 groups (1024 values) per wave: K <= 1024 * NP, K % 256 == 0. Lane t of a pass owns group
 // 4p + t / 16, position tl = t % 16.
-template <int NP>
+template <int NP, int PRE>
 __global__ __launch_bounds__(256) void quant_convrot(const uint16_t* __restrict__ x, int64_t M, int K,
-                                                     int8_t* __restrict__ xq, float* __restrict__ xs) {
+                                                     int8_t* __restrict__ xq, float* __restrict__ xs, PreArgs pa) {
     __shared__ float stage[4][4 * 272];          // per wave: one 4-group window
     __shared__ uint32_t qbytes[4][NP * 256];     // per wave: the int8 row, 4 bytes a word
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -129,6 +194,13 @@ __global__ __launch_bounds__(256) void quant_convrot(const uint16_t* __restrict_
     float* st = stage[wave];
     float y[NP][16];
     float amax = 0.0f;
+    float mu = 0.0f, rstd = 0.0f;
+    const int64_t grp = PRE >= 2 ? row / pa.rows_per_group : 0;
+    if constexpr (PRE == 3) {
+        float var;
+        ln_stats(x + row * K, K, lane, mu, var);
+        rstd = (float)(1.0 / __builtin_sqrt((double)(var + pa.eps)));
+    }
 #pragma unroll
     for (int p = 0; p < NP; p++) {
         const int g = 4 * p + gl;
@@ -143,6 +215,28 @@ __global__ __launch_bounds__(256) void quant_convrot(const uint16_t* __restrict_
             for (int h = 0; h < 8; h++) {
                 v[2 * h] = bf16_bits_to_f32(w[h] & 0xffffu);
                 v[2 * h + 1] = bf16_bits_to_f32(w[h] >> 16);
+            }
+            if constexpr (PRE == 1) {
+#pragma unroll
+                for (int h = 0; h < 8; h++) {
+                    v[2 * h] = bf16_bits_to_f32(pa.s[w[h] & 0xffffu]);
+                    v[2 * h + 1] = bf16_bits_to_f32(pa.s[w[h] >> 16]);
+                }
+            } else if constexpr (PRE >= 2) {
+                const int64_t o = grp * K + g * 256 + 16 * tl;
+                const uint4* sp = reinterpret_cast<const uint4*>(pa.s + o);
+                const uint4* hp = reinterpret_cast<const uint4*>(pa.h + o);
+                const uint4 s0 = sp[0], s1 = sp[1], h0 = hp[0], h1 = hp[1];
+                const uint32_t sw[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+                const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float sc = bf16_bits_to_f32(i & 1 ? sw[i >> 1] >> 16 : sw[i >> 1] & 0xffffu);
+                    const float sh = bf16_bits_to_f32(i & 1 ? hw[i >> 1] >> 16 : hw[i >> 1] & 0xffffu);
+                    float t = v[i];
+                    if constexpr (PRE == 3) t = round_bf16((t - mu) * rstd);
+                    v[i] = round_bf16(round_bf16(t * sc) + sh);
+                }
             }
         } else {
 #pragma unroll
@@ -196,9 +290,35 @@ static void launch_plain(const uint16_t* x, int64_t M, int K, int8_t* xq, float*
     quant_plain<CPL><<<dim3((unsigned)((M + 3) / 4)), 256, 0, s>>>(x, M, K, xq, xs);
 }
 
-template <int NP>
-static void launch_convrot(const uint16_t* x, int64_t M, int K, int8_t* xq, float* xs, hipStream_t s) {
-    quant_convrot<NP><<<dim3((unsigned)((M + 3) / 4)), 256, 0, s>>>(x, M, K, xq, xs);
+template <int NP, int PRE>
+static void launch_convrot_pre(const uint16_t* x, int64_t M, int K, int8_t* xq, float* xs, const PreArgs& pa,
+                               hipStream_t s) {
+    quant_convrot<NP, PRE><<<dim3((unsigned)((M + 3) / 4)), 256, 0, s>>>(x, M, K, xq, xs, pa);
+}
+
+template <int PRE>
+static void launch_convrot(const uint16_t* x, int64_t M, int K, int8_t* xq, float* xs, const PreArgs& pa,
+                           hipStream_t s) {
+    const int np = (K + 1023) / 1024;
+    if (np <= 1) launch_convrot_pre<1, PRE>(x, M, K, xq, xs, pa, s);
+    else if (np <= 2) launch_convrot_pre<2, PRE>(x, M, K, xq, xs, pa, s);
+    else if (np <= 3) launch_convrot_pre<3, PRE>(x, M, K, xq, xs, pa, s);
+    else if (np <= 4) launch_convrot_pre<4, PRE>(x, M, K, xq, xs, pa, s);
+    else if (np <= 5) launch_convrot_pre<5, PRE>(x, M, K, xq, xs, pa, s);
+    else launch_convrot_pre<6, PRE>(x, M, K, xq, xs, pa, s);
+}
+
+// the checks both entry points share
+static int check_rows(const char* who, const void* x, int64_t M, int64_t K, const int8_t* xq, const float* xs) {
+    if (M < 0 || K <= 0) { set_error("%s: M = %lld, K = %lld", who, (long long)M, (long long)K); return WF_EINVAL; }
+    if (M == 0) return WF_OK;
+    if (!x || !xq || !xs) { set_error("%s: null pointer", who); return WF_EINVAL; }
+    if (!aligned(x, 16) || !aligned(xq, 16) || !aligned(xs, 4)) {
+        set_error("%s: x and xq must be 16-byte aligned", who);
+        return WF_EUNSUPPORTED;
+    }
+    if (M > ((int64_t)1 << 33)) { set_error("%s: M too large", who); return WF_EUNSUPPORTED; }
+    return WF_OK;
 }
 
 }  // namespace wf
@@ -206,14 +326,8 @@ static void launch_convrot(const uint16_t* x, int64_t M, int K, int8_t* xq, floa
 extern "C" int wf_quant_rows_i8(const void* x_bf16, int64_t M, int64_t K, int mode, int8_t* xq, float* xs,
                                 void* stream) {
     using namespace wf;
-    if (M < 0 || K <= 0) { set_error("wf_quant_rows_i8: M = %lld, K = %lld", (long long)M, (long long)K); return WF_EINVAL; }
-    if (M == 0) return WF_OK;
-    if (!x_bf16 || !xq || !xs) { set_error("wf_quant_rows_i8: null pointer"); return WF_EINVAL; }
-    if (!aligned(x_bf16, 16) || !aligned(xq, 16) || !aligned(xs, 4)) {
-        set_error("wf_quant_rows_i8: x and xq must be 16-byte aligned");
-        return WF_EUNSUPPORTED;
-    }
-    if (M > ((int64_t)1 << 33)) { set_error("wf_quant_rows_i8: M too large"); return WF_EUNSUPPORTED; }
+    const int rc = check_rows("wf_quant_rows_i8", x_bf16, M, K, xq, xs);
+    if (rc != WF_OK || M == 0) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const uint16_t* xp = static_cast<const uint16_t*>(x_bf16);
     const int k = (int)K;
@@ -233,17 +347,49 @@ extern "C" int wf_quant_rows_i8(const void* x_bf16, int64_t M, int64_t K, int mo
             set_error("wf_quant_rows_i8: ConvRot mode needs K %% 256 == 0 and K <= 6144 (K = %lld)", (long long)K);
             return WF_EUNSUPPORTED;
         }
-        const int np = (k + 1023) / 1024;
-        if (np <= 1) launch_convrot<1>(xp, M, k, xq, xs, s);
-        else if (np <= 2) launch_convrot<2>(xp, M, k, xq, xs, s);
-        else if (np <= 3) launch_convrot<3>(xp, M, k, xq, xs, s);
-        else if (np <= 4) launch_convrot<4>(xp, M, k, xq, xs, s);
-        else if (np <= 5) launch_convrot<5>(xp, M, k, xq, xs, s);
-        else launch_convrot<6>(xp, M, k, xq, xs, s);
+        launch_convrot<0>(xp, M, k, xq, xs, PreArgs{nullptr, nullptr, 1, 0.0f}, s);
     } else {
         set_error("wf_quant_rows_i8: mode %d", mode);
         return WF_EUNSUPPORTED;
     }
     WF_LAUNCH_CHECK("wf_quant_rows_i8 launch");
+    return WF_OK;
+}
+
+extern "C" int wf_quant_rows_i8_pre(const void* x_bf16, int64_t M, int64_t K, int pre, const void* s_bf16,
+                                    const void* shift_bf16, int64_t rows_per_group, float eps, int8_t* xq, float* xs,
+                                    void* stream) {
+    using namespace wf;
+    const int rc = check_rows("wf_quant_rows_i8_pre", x_bf16, M, K, xq, xs);
+    if (rc != WF_OK || M == 0) return rc;
+    if (pre < 0 || pre > 3) { set_error("wf_quant_rows_i8_pre: operation %d", pre); return WF_EUNSUPPORTED; }
+    if (K % 256 || K > 6144 || (pre == 3 && K % 512)) {
+        set_error("wf_quant_rows_i8_pre: K = %lld (K %% 256 == 0, K <= 6144; LayerNorm K %% 512 == 0)", (long long)K);
+        return WF_EUNSUPPORTED;
+    }
+    if (pre >= 1 && !s_bf16) { set_error("wf_quant_rows_i8_pre: null pointer"); return WF_EINVAL; }
+    if (pre >= 2) {
+        if (!shift_bf16) { set_error("wf_quant_rows_i8_pre: null pointer"); return WF_EINVAL; }
+        if (rows_per_group <= 0 || M % rows_per_group) {
+            set_error("wf_quant_rows_i8_pre: M = %lld is not a whole number of %lld-row groups", (long long)M,
+                      (long long)rows_per_group);
+            return WF_EUNSUPPORTED;
+        }
+        if (!aligned(s_bf16, 16) || !aligned(shift_bf16, 16)) {
+            set_error("wf_quant_rows_i8_pre: scale and shift must be 16-byte aligned");
+            return WF_EUNSUPPORTED;
+        }
+    }
+    if (pre == 1 && !aligned(s_bf16, 2)) { set_error("wf_quant_rows_i8_pre: table alignment"); return WF_EUNSUPPORTED; }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint16_t* xp = static_cast<const uint16_t*>(x_bf16);
+    const PreArgs pa{static_cast<const uint16_t*>(s_bf16), static_cast<const uint16_t*>(shift_bf16),
+                     rows_per_group > 0 ? rows_per_group : 1, eps};
+    const int k = (int)K;
+    if (pre == 0) launch_convrot<0>(xp, M, k, xq, xs, pa, s);
+    else if (pre == 1) launch_convrot<1>(xp, M, k, xq, xs, pa, s);
+    else if (pre == 2) launch_convrot<2>(xp, M, k, xq, xs, pa, s);
+    else launch_convrot<3>(xp, M, k, xq, xs, pa, s);
+    WF_LAUNCH_CHECK("wf_quant_rows_i8_pre launch");
     return WF_OK;
 }

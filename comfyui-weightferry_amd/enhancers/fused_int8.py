@@ -14,7 +14,7 @@ no counterpart here. ``int8_linear`` is the direct entry (plain per-token or Con
 import torch
 
 from .. import _native
-from .fused_kernels import QUANT_MODES
+from .fused_kernels import PRE_GELU, PRE_LNMOD, PRE_MOD, QUANT_MODES
 from .fused_state import _count, _state, _tls
 
 _QUANT_MAX_K = {0: 8192, 1: 6144}
@@ -26,10 +26,16 @@ def _key2d(t):
 
 
 def _set_pre(marker, kind, scale=None, shift=None, norm=None):
-    """Register a pending input: the layer that receives ``marker`` uses kind(marker) (modq / gelu / lnmod)
-    (enhancers/fused_int8.py:28-39)."""
+    """Register a pending input: the layer that receives ``marker`` quantises kind(marker) itself (modq / gelu;
+    lnmod: marker is the block input, norm its LayerNorm) (enhancers/fused_int8.py:28-39)."""
     pre = {"key": _key2d(marker), "kind": kind, "src": marker, "used": False, "mat": None, "norm": norm,
            "scale5": scale, "shift5": shift}
+    if kind in ("mod", "lnmod"):
+        D = marker.shape[-1]
+        groups = scale.numel() // D
+        pre["s1"] = (1 + scale).contiguous().view(groups, D)
+        pre["shift"] = shift.contiguous().view(groups, D)
+        pre["rows_per_group"] = marker.numel() // D // groups
     _tls.pre = pre
     return pre
 
@@ -59,6 +65,54 @@ def _pending_for(input):
     is_pre = (pre is not None and torch.is_tensor(input) and input.dim() >= 2
               and pre["key"] == _key2d(input.reshape(-1, input.shape[-1])))
     return pre, is_pre
+
+
+_PRE_CODE = {"gelu": PRE_GELU, "mod": PRE_MOD, "lnmod": PRE_LNMOD}
+_gelu_tables = {}
+
+
+def _gelu_table(device):
+    """torch's GELU (erf) of every bfloat16 value, indexed by its 16 bits (enhancers/fused_int8.py:94-105): the
+    quantiser's GELU looks its results up here, so they are torch's own on this device."""
+    key = str(device)
+    tab = _gelu_tables.get(key)
+    if tab is None:
+        xs = torch.arange(65536, dtype=torch.int32, device=device).to(torch.int16).view(torch.bfloat16)
+        tab = torch.nn.functional.gelu(xs).contiguous()
+        _gelu_tables[key] = tab
+    return tab
+
+
+def _pre_fusable(pre, k):
+    """Whether the pending operation can run inside the quantiser at width k (LNMOD: a LayerNorm without affine
+    weights, k % 512 == 0)."""
+    if pre["kind"] == "lnmod":
+        norm = pre["norm"]
+        return (k % 512 == 0 and getattr(norm, "weight", None) is None and getattr(norm, "bias", None) is None
+                and isinstance(getattr(norm, "eps", None), float))
+    return pre["kind"] in _PRE_CODE
+
+
+def quantise_pre(pre, x_2d):
+    """(x_q, x_s) of kind(x_2d) for the pending input ``pre`` with its operation inside the ConvRot quantiser
+    (wf_quant_rows_i8_pre; the reference's _quantise_pre, enhancers/fused_int8.py:60-75), or None when declined."""
+    m, k = x_2d.shape
+    dev = x_2d.device
+    x_q = torch.empty((m, k), dtype=torch.int8, device=dev)
+    x_s = torch.empty((m, 1), dtype=torch.float32, device=dev)
+    code = _PRE_CODE[pre["kind"]]
+    if code == PRE_GELU:
+        s, h, rows, eps = _gelu_table(dev), None, 1, 0.0
+    else:
+        s, h, rows = pre["s1"], pre["shift"], pre["rows_per_group"]
+        eps = float(pre["norm"].eps) if code == PRE_LNMOD else 0.0
+    with torch.cuda.device(dev):
+        rc = _native.lib().wf_quant_rows_i8_pre(x_2d.data_ptr(), m, k, code, s.data_ptr(),
+                                                h.data_ptr() if h is not None else None, rows, eps,
+                                                x_q.data_ptr(), x_s.data_ptr(), _native.stream_of(dev))
+    if not _native.check(rc, "wf_quant_rows_i8_pre"):
+        return None
+    return x_q, x_s
 
 
 # ------------------------------------------------------------------------------------------------- the weight
@@ -161,17 +215,22 @@ def _int8_quantised(x, weight, bias):
             or not 256 <= k <= _QUANT_MAX_K[1] or w_q.shape[1] != k):
         return None
     pre, is_pre = _pending_for(x_2d)
-    if is_pre:
-        # no operation is fused into the quantiser here: the real input is quantised (q / k / v still share it)
-        _count({"gelu": "gelu", "lnmod": "ln"}.get(pre["kind"], "modq"), False, "pending input materialised")
+    part = {"gelu": "gelu", "lnmod": "ln"}.get(pre["kind"], "modq") if is_pre else None
+    if is_pre and not _pre_fusable(pre, k):
+        # quantise the real input instead, as ComfyUI does (q / k / v still share it)
+        _count(part, False, f"{pre['kind']} at width {k} is not fused")
         x_2d = _materialise(pre).reshape(-1, k).contiguous()
-    key = (x_2d.data_ptr(), tuple(x_2d.shape), tuple(x_2d.stride()), gs, False)
+        is_pre = False
+    key = (x_2d.data_ptr(), tuple(x_2d.shape), tuple(x_2d.stride()), gs, is_pre)
     if cache.get("key") == key:
         x_q, x_s = cache["q"]
     else:
-        q = quantise_rows(x_2d, QUANT_MODES["convrot"])
+        # the pending operation inside the quantiser: the same bits as quantising its real value
+        q = quantise_pre(pre, x_2d) if is_pre else quantise_rows(x_2d, QUANT_MODES["convrot"])
         if q is None:
             return None
+        if is_pre:
+            _count(part, True)
         x_q, x_s = q
         cache["key"], cache["q"] = key, (x_q, x_s)
     ws = _weight_scale(w_scale, n, x.device)
@@ -299,5 +358,5 @@ class _Overrides:
         return False
 
 
-__all__ = ["_int8_quantised", "_int8_linear_shared", "_int8_linear_residual", "_shared_forward",
+__all__ = ["quantise_pre", "_gelu_table", "_int8_quantised", "_int8_linear_shared", "_int8_linear_residual", "_shared_forward",
            "_residual_forward", "_Overrides", "int8_linear", "quantise_rows", "gemm", "_state"]

@@ -65,6 +65,17 @@ int wf_dequant_add(const void* src, int64_t src_bytes, int qtype, int mid_dt, in
  * xs: float32 [M]. x and xq 16-byte aligned. */
 int wf_quant_rows_i8(const void* x_bf16, int64_t M, int64_t K, int mode, int8_t* xq, float* xs, void* stream);
 
+/* The ConvRot quantisation (mode 1 above) with an operation applied to each value first: replaces the Triton
+ * `_quant_row` with PRE 1..3 (enhancers/fused_kernels.py:137-163) as `_quantise_pre` launches it for a pending input
+ * (enhancers/fused_int8.py:60-75). pre 0: none; 1 GELU: y = table[bits(x)], s_bf16 = torch's GELU of all 65536 bf16
+ * values (:94-105); 2 MOD: y = bf16(bf16(x * s1) + shift) with s_bf16 = s1 = 1 + scale and shift_bf16 = shift, both
+ * bf16 [M / rows_per_group, K], row r using group r / rows_per_group (:28-39); 3 LNMOD: LayerNorm without affine
+ * first -- mean and variance by the reference's Welford order (:84-136), rstd = 1 / sqrt(var + eps) correctly rounded
+ * where the reference uses the NVIDIA approximation rsqrt.approx.f32 -- rounded to bf16, then MOD. K % 256 == 0,
+ * K <= 6144 (LNMOD: K % 512 == 0); s / shift 16-byte aligned for MOD / LNMOD. */
+int wf_quant_rows_i8_pre(const void* x_bf16, int64_t M, int64_t K, int pre, const void* s_bf16, const void* shift_bf16,
+                         int64_t rows_per_group, float eps, int8_t* xq, float* xs, void* stream);
+
 /* out[m, n] = OUT((float(acc[m, n]) * xs[m]) * ws[n] (+ bias[n])), acc = sum_k xq[m, k] * wq[n, k] exactly in
  * int32: replaces kitchen's cutlass_int8_dequant (enhancers/fused_int8.py:191-206; the reference returns None and
  * falls back where this returns WF_EUNSUPPORTED). wq is [N, K] (row = output channel); bias (nullable) has dtype

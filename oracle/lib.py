@@ -44,6 +44,9 @@ def load():
         lib.wfo_dequant_add.argtypes = [p, i64, c_int, c_int, c_int, p, ctypes.c_float, p, i64]
         lib.wfo_dequant_add.restype = c_int
         lib.wfo_quant_rows.argtypes = [p, i64, i64, c_int, p, p, p]
+        lib.wfo_ln_stats.argtypes = [p, i64, p, p]
+        lib.wfo_quant_rows_pre.argtypes = [p, i64, i64, c_int, p, p, i64, ctypes.c_float, p, p, p, p]
+        lib.wfo_quant_rows_pre.restype = c_int
         lib.wfo_quant_rows.restype = c_int
         lib.wfo_linear_i8.argtypes = [p, p, p, p, p, p, c_int, i64, i64, i64, p]
         lib.wfo_linear_i8.restype = c_int
@@ -103,6 +106,32 @@ def quant_rows(x_bf16_bits, mode):
     rc = load().wfo_quant_rows(_ptr(x), M, K, mode, _ptr(xq), _ptr(xs), _ptr(work))
     if rc != 0:
         raise ValueError(f"oracle quant_rows rejected the input (rc={rc})")
+    return xq, xs
+
+
+def ln_stats(row_bf16_bits):
+    """(mean, sigma2 / K) of one bf16 row by the reference's Welford order (wfo_ln_stats)."""
+    r = np.ascontiguousarray(row_bf16_bits, dtype=np.uint16)
+    mu, var = np.zeros(1, np.float32), np.zeros(1, np.float32)
+    load().wfo_ln_stats(_ptr(r), r.size, _ptr(mu), _ptr(var))
+    return mu[0], var[0]
+
+
+def quant_rows_pre(x_bf16_bits, pre, s=None, h=None, rows_per_group=1, eps=0.0):
+    """ConvRot row quantisation with the operation ``pre`` first (wfo_quant_rows_pre): GELU with ``s`` the bf16 bits
+    of the 65536-entry table; MOD / LNMOD with ``s`` = bf16 bits of 1 + scale and ``h`` of the shift, [groups, K]."""
+    x = np.ascontiguousarray(x_bf16_bits, dtype=np.uint16)
+    M, K = x.shape
+    xq = np.empty((M, K), dtype=np.int8)
+    xs = np.empty(M, dtype=np.float32)
+    work = np.empty(K, dtype=np.float32)
+    rowbuf = np.empty(K, dtype=np.uint16)
+    s_ = np.ascontiguousarray(s, dtype=np.uint16) if s is not None else None
+    h_ = np.ascontiguousarray(h, dtype=np.uint16) if h is not None else None
+    rc = load().wfo_quant_rows_pre(_ptr(x), M, K, pre, _ptr(s_), _ptr(h_), rows_per_group, float(eps), _ptr(xq),
+                                   _ptr(xs), _ptr(work), _ptr(rowbuf))
+    if rc != 0:
+        raise ValueError(f"oracle quant_rows_pre rejected the input (rc={rc})")
     return xq, xs
 
 

@@ -10,6 +10,7 @@
  *   - K-quant 256-value blocks    enhancers/gguf_dequant.py:56,170-256
  *   - LoRA add (_deq_add)         enhancers/gguf_dequant.py:99-133,387-409
  *   - int8 row quantiser          enhancers/fused_kernels.py:44-49,65-81,137-174
+ *   - quantiser operations (PRE)  enhancers/fused_kernels.py:14-18,84-136,143-163; enhancers/fused_int8.py:28-39,94-105
  *   - int8 linear epilogue        enhancers/fused_int8.py:191-206 (order of the epilogue fixed by this build)
  *
  * Build: gcc -O2 -fPIC -shared -ffp-contract=off -fno-fast-math (see oracle/Makefile). No FMA contraction: every
@@ -323,6 +324,82 @@ int wfo_linear_i8_residual(const int8_t* xq, const int8_t* wq, const float* xs, 
 /* ------------------------------------------------------------------------------------------- array helpers */
 
 /* n float32 values -> their binary16 bits (textbook RNE above), for exhaustive checks over bit patterns */
+/* ----------------------------------------------------------------------------------- quantiser operations */
+
+/* cuWelfordCombine(dataB = own, dataA = other) as the reference restates it, contractions explicit
+ * (enhancers/fused_kernels.py:84-94) */
+static void wcombine(float* m, float* s, float* c, float mo, float so, float co) {
+    const float delta = *m - mo;
+    const float count = co + *c;
+    const float coef = 1.0f / count;
+    const float na = co * coef, nb = *c * coef;
+    const float mean = fmaf(na, mo, nb * *m);
+    const float sig = fmaf((delta * delta) * co, nb, so + *s);
+    *m = mean; *s = sig; *c = count;
+}
+
+/* _ln_stats of enhancers/fused_kernels.py:108-136 on one bf16 row of K values (K % 512 == 0): 128 threads, thread t
+ * updating (mean, sigma2, count) over values (t + 128 j) * 4 + ii, j-major; then the shuffle-down merges of [4, 32]
+ * (N = 32 .. 2) and of the 4 warps (2, 3 into 0, 1; 1 into 0). Returns mean and sigma2 / K. */
+void wfo_ln_stats(const uint16_t* xr, int64_t K, float* mu, float* var) {
+    float m[128], sg[128], c[128];
+    for (int t = 0; t < 128; t++) {
+        m[t] = 0.0f; sg[t] = 0.0f; c[t] = 0.0f;
+        for (int64_t j = 0; j < K / 512; j++)
+            for (int ii = 0; ii < 4; ii++) {
+                const float v = u2f((uint32_t)xr[(t + j * 128) * 4 + ii] << 16);
+                const float delta = v - m[t];
+                c[t] = c[t] + 1.0f;
+                m[t] = fmaf(delta, 1.0f / c[t], m[t]);
+                sg[t] = fmaf(delta, v - m[t], sg[t]);
+            }
+    }
+    for (int N = 32; N >= 2; N /= 2)
+        for (int w = 0; w < 4; w++)
+            for (int t = 0; t < N / 2; t++) {
+                const int a = 32 * w + t, b = 32 * w + t + N / 2;
+                wcombine(&m[a], &sg[a], &c[a], m[b], sg[b], c[b]);
+            }
+    wcombine(&m[0], &sg[0], &c[0], m[64], sg[64], c[64]);      /* warp 2 into warp 0 */
+    wcombine(&m[32], &sg[32], &c[32], m[96], sg[96], c[96]);   /* warp 3 into warp 1 */
+    wcombine(&m[0], &sg[0], &c[0], m[32], sg[32], c[32]);      /* warp 1 into warp 0 */
+    *mu = m[0];
+    *var = sg[0] / (float)K;
+}
+
+/* _quant_row with an operation before the rotation (enhancers/fused_kernels.py:137-174), ConvRot mode:
+ * pre 0 none; 1 GELU: y = table[bits(x)] (table: bf16 bits [65536]); 2 MOD: y = R16(R16(x * s1[g]) + h[g]);
+ * 3 LNMOD: y = R16((x - mu) * rstd), then MOD; g = row / rows_per_group, s1 and h bf16 [groups, K].
+ * rstd = RN(1 / sqrt(var + eps)) (the reference's rsqrt.approx.f32 is an NVIDIA approximation). */
+int wfo_quant_rows_pre(const uint16_t* x, int64_t M, int64_t K, int pre, const uint16_t* s, const uint16_t* h,
+                       int64_t rows_per_group, float eps, int8_t* xq, float* xs, float* work, uint16_t* rowbuf) {
+    if (K % 256 || pre < 0 || pre > 3 || (pre == 3 && K % 512)) return -1;
+    if (pre >= 2 && (rows_per_group <= 0 || M % rows_per_group)) return -1;
+    for (int64_t r = 0; r < M; r++) {
+        const uint16_t* xr = x + r * K;
+        float mu = 0.0f, rstd = 0.0f;
+        if (pre == 3) {
+            float var;
+            wfo_ln_stats(xr, K, &mu, &var);
+            rstd = (float)(1.0 / sqrt((double)(var + eps)));
+        }
+        const int64_t g = pre >= 2 ? r / rows_per_group : 0;
+        for (int64_t k = 0; k < K; k++) {
+            float v = u2f((uint32_t)xr[k] << 16);
+            if (pre == 1) {
+                v = u2f((uint32_t)s[xr[k]] << 16);
+            } else if (pre >= 2) {
+                if (pre == 3) v = wfo_round((v - mu) * rstd, 1);
+                const float sc = u2f((uint32_t)s[g * K + k] << 16), sh = u2f((uint32_t)h[g * K + k] << 16);
+                v = wfo_round(wfo_round(v * sc, 1) + sh, 1);
+            }
+            rowbuf[k] = (uint16_t)(f2u(v) >> 16);      /* every value here is a bf16 value */
+        }
+        if (wfo_quant_rows(rowbuf, 1, K, 1, xq + r * K, xs + r, work)) return -1;
+    }
+    return 0;
+}
+
 void wfo_f32_to_f16_array(const float* x, uint16_t* h, int64_t n) {
     for (int64_t i = 0; i < n; i++) h[i] = wfo_f32_to_f16_bits(x[i]);
 }

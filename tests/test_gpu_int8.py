@@ -192,3 +192,82 @@ def test_int8_linear_plain_per_token(native, M, N):
     xq, xs = lib.quant_rows(x.view(torch.int16).numpy().view(np.uint16), 0)
     expect = lib.linear_i8(xq, w_q.numpy(), xs, ws.numpy(), out_dt=lib.BF16)
     assert np.array_equal(_bits(y), expect)
+
+
+# ------------------------------------------------------------------------------ quantiser operations (PRE)
+def _gelu_table_bits():
+    table = torch.nn.functional.gelu(torch.arange(65536, dtype=torch.int32, device="cuda").to(torch.int16)
+                                     .view(torch.bfloat16))
+    return table, _bits(table)
+
+
+def gpu_quant_pre(native, x, pre, s=None, h=None, rows=1, eps=0.0):
+    M, K = x.shape
+    xq = torch.empty((M, K), dtype=torch.int8, device="cuda")
+    xs = torch.empty(M, dtype=torch.float32, device="cuda")
+    rc = native.lib().wf_quant_rows_i8_pre(x.data_ptr(), M, K, pre, s.data_ptr() if s is not None else None,
+                                           h.data_ptr() if h is not None else None, rows, eps, xq.data_ptr(),
+                                           xs.data_ptr(), native.stream_of(x.device))
+    assert rc == 0, native.last_error()
+    torch.cuda.synchronize()
+    return xq, xs
+
+
+@pytest.mark.parametrize("pre", [0, 1, 2, 3])
+@pytest.mark.parametrize("K,groups,rows", [(1024, 3, 5), (5120, 2, 64), (6144, 1, 7)])
+def test_quant_rows_pre_against_oracle(native, pre, K, groups, rows):
+    g = torch.Generator().manual_seed(pre * 100 + K)
+    x = (torch.randn((groups * rows, K), generator=g) * 1.5).to(torch.bfloat16)
+    x[0] = 0.75                                         # a constant row (LayerNorm variance 0)
+    scale = (torch.randn((groups, K), generator=g) * 0.3).to(torch.bfloat16)
+    shift = (torch.randn((groups, K), generator=g) * 0.5).to(torch.bfloat16)
+    s1 = 1 + scale
+    print(f"case pre={pre} K={K} groups={groups} rows={rows}", flush=True)
+    if pre == 1:
+        table, tbits = _gelu_table_bits()
+        xq, xs = gpu_quant_pre(native, x.cuda(), 1, table)
+        rq, rs = lib.quant_rows_pre(_bits(x), 1, tbits)
+    elif pre >= 2:
+        xq, xs = gpu_quant_pre(native, x.cuda(), pre, s1.cuda(), shift.cuda(), rows, 1e-6)
+        rq, rs = lib.quant_rows_pre(_bits(x), pre, _bits(s1), _bits(shift), rows, 1e-6)
+    else:
+        xq, xs = gpu_quant_pre(native, x.cuda(), 0)
+        rq, rs = lib.quant_rows_pre(_bits(x), 0)
+    assert np.array_equal(xs.cpu().numpy().view(np.uint32), rs.view(np.uint32))
+    bad = np.argwhere(xq.cpu().numpy() != rq)
+    assert bad.size == 0, bad[:8].tolist()
+
+
+@pytest.mark.parametrize("kind", ["mod", "gelu", "lnmod"])
+def test_pending_input_quantised_with_its_operation(native, kind):
+    from fake_quant import FakeQT, Lin
+    fi = sub("enhancers.fused_int8")
+    fs = sub("enhancers.fused_state")
+    fs.stats(reset=True)
+    g = torch.Generator().manual_seed(21)
+    B, N, K = 2, 160, 5120
+    src = (torch.randn((B, N, K), generator=g)).to(torch.bfloat16).cuda()
+    scale = (torch.randn((B, 1, K), generator=g) * 0.2).to(torch.bfloat16).cuda()
+    shift = (torch.randn((B, 1, K), generator=g) * 0.2).to(torch.bfloat16).cuda()
+    norm = torch.nn.LayerNorm(K, elementwise_affine=False, eps=1e-6)
+    w_q = torch.randint(-127, 128, (640, K), generator=g, dtype=torch.int64).to(torch.int8)
+    ws = torch.rand(640, generator=g) * 0.01
+    lin = Lin(FakeQT(w_q.cuda(), ws.cuda()))
+    with fi._Overrides([lin]):
+        if kind == "gelu":
+            fi._set_pre(src, "gelu")
+        else:
+            fi._set_pre(src, kind, scale, shift, norm=norm if kind == "lnmod" else None)
+        y = lin(src)
+        fi._clear_pre()
+    torch.cuda.synchronize()
+    part = {"gelu": "gelu", "lnmod": "ln"}.get(kind, "modq")
+    assert fs.stats()[part]["used"] == 1, fs.stats()
+    xb = _bits(src.reshape(-1, K))
+    if kind == "gelu":
+        rq, rs = lib.quant_rows_pre(xb, 1, _gelu_table_bits()[1])
+    else:
+        rq, rs = lib.quant_rows_pre(xb, 2 if kind == "mod" else 3, _bits((1 + scale).reshape(B, K)),
+                                    _bits(shift.reshape(B, K)), N, 1e-6)
+    expect = lib.linear_i8(rq, w_q.numpy(), rs, ws.numpy(), out_dt=lib.BF16)
+    assert np.array_equal(_bits(y.reshape(-1, 640)), expect)
