@@ -17,7 +17,9 @@ Other rows of the workload list are reported under "also":
   * 40 streamed Wan-14B blocks of Q4_K from pinned host memory through 2 GPU slots, 4096 tokens (ms/step, H2D
     GB/s, share of the copy time hidden behind compute).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--only-headline]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--only-headline] [--legs LEGS]
+--legs (comma list of headline, lora, int8, fused, streaming; default all) runs only those legs, for profiling one
+kernel family; without the headline leg the printed line holds the legs' figures only.
 """
 import argparse
 import importlib
@@ -39,7 +41,11 @@ def _args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true", help="leave out the CPU baseline leg")
     ap.add_argument("--only-headline", action="store_true", help="the Q4_K dequant leg only")
-    return ap.parse_args()
+    ap.add_argument("--legs", default="all", help="comma list: headline, lora, int8, fused, streaming")
+    a = ap.parse_args()
+    a.legs = {"headline"} if a.only_headline else (
+        {"headline", "lora", "int8", "fused", "streaming"} if a.legs == "all" else set(a.legs.split(",")))
+    return a
 
 
 def _timed(torch, fn, n, warm):
@@ -97,7 +103,7 @@ def fused_leg(torch, native):
     """One Wan-14B block's linears at 4096 tokens with Q5_K / Q6_K weights: the fused kernel and the two-step
     flow (wf_dequant to bf16, then torch's bf16 GEMM)."""
     sys.path.insert(0, ROOT)
-    from oracle import encode
+    encode = importlib.import_module(PKG + ".gguf_encode")
     lib = native.lib()
     dev = torch.device("cuda:0")
     st = native.stream_of(dev)
@@ -284,16 +290,30 @@ def main():
     import numpy as np  # noqa: F401
     import torch
 
-    from oracle import encode
+    encode = importlib.import_module(PKG + ".gguf_encode")
 
     native = importlib.import_module(PKG + "._native")
     native.lib()
     _log(f"library {native.LIB_PATH}")
 
     shapes = [(13824, 5120), (5120, 13824)]
-    t = time.perf_counter()
-    raws = [encode.encode_q4_k(encode.weights(s, seed=1234 + i)) for i, s in enumerate(shapes)]
-    _log(f"encoded Q4_K pair in {time.perf_counter() - t:.1f} s")
+    also = {}
+    raws = None
+    if args.legs & {"headline", "lora"}:
+        t = time.perf_counter()
+        raws = [encode.encode_q4_k(encode.weights(s, seed=1234 + i)) for i, s in enumerate(shapes)]
+        _log(f"encoded Q4_K pair in {time.perf_counter() - t:.1f} s")
+    if "headline" not in args.legs:
+        if "lora" in args.legs:
+            also["lora_add_q4_k_13824x5120"] = lora_leg(torch, native, raws[0], shapes[0])
+        if "int8" in args.legs:
+            also["int8_w8a8"] = int8_leg(torch, native)
+        if "fused" in args.legs:
+            also["fused_dequant_gemm_wan_block"] = fused_leg(torch, native)
+        if "streaming" in args.legs:
+            also["streamed_40_blocks_q4_k"] = streaming_leg(torch, native)
+        print(json.dumps({"legs": sorted(args.legs), "also": also}), flush=True)
+        return
 
     ms_step, kern_ms, algo = dequant_leg(torch, native, raws, shapes, 12, 0, 1, args.steps, args.warmup)
     value = algo / (ms_step / 1e3) / 1e9
@@ -301,7 +321,6 @@ def main():
     achieved = per_launch / (kern_ms / 1e3) / 1e9
     _log(f"Q4_K pair: {ms_step * 1e3:.1f} us/step, kernel {kern_ms * 1e3:.1f} us, {value:.0f} GB/s")
 
-    also = {}
     # calibration: a plain copy of 512 MiB (two rotating pairs: 2 GiB in all) -- the achievable HBM rate, and the
     # known-size kernel the counter runs are scaled by
     cp = [(torch.empty(1 << 29, dtype=torch.uint8, device="cuda"), torch.empty(1 << 29, dtype=torch.uint8,
@@ -326,13 +345,16 @@ def main():
         ms8, k8, a8 = dequant_leg(torch, native, q8, [(5120, 5120)], 8, mid, 1, args.steps, args.warmup)
         also[name] = {"GB/s": round(a8 / (k8 / 1e3) / 1e9, 1), "kernel_us": round(k8 * 1e3, 2),
                       "frac": round(a8 / (k8 / 1e3) / 1e9 / HBM_PEAK_GBS, 3), "bytes": a8}
-    if not args.only_headline:
+    if "lora" in args.legs:
         also["lora_add_q4_k_13824x5120"] = lora_leg(torch, native, raws[0], shapes[0])
         _log("lora leg done")
+    if "int8" in args.legs:
         also["int8_w8a8"] = int8_leg(torch, native)
         _log("int8 leg done")
+    if "fused" in args.legs:
         also["fused_dequant_gemm_wan_block"] = fused_leg(torch, native)
         _log("fused leg done")
+    if "streaming" in args.legs:
         also["streamed_40_blocks_q4_k"] = streaming_leg(torch, native)
         _log("streaming leg done")
     cpu = None

@@ -1,4 +1,5 @@
-"""ORACLE (test infrastructure only): synthetic GGUF block encoders and random-block generators.
+"""Synthetic GGUF inputs: block encoders and random-block generators for the benchmarks, the smoke check and the
+tests (no part of the hot path: ComfyUI-GGUF hands the kernels blocks from .gguf files).
 
 The encoders turn float32 weights into valid blocks of the GGML layouts the reference decodes
 (enhancers/gguf_dequant.py:52-56,195-249): Q8_0 (d = f16(absmax / 127), q = rint(x / d)), and simple deterministic

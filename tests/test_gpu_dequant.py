@@ -8,7 +8,9 @@ import pytest
 import torch
 
 from conftest import sub
-from oracle import encode, lib, np_oracle
+from oracle import lib, np_oracle
+
+encode = sub("gguf_encode")
 
 pytestmark = pytest.mark.gpu
 

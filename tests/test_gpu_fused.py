@@ -8,7 +8,11 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import encode, lib
+from conftest import sub
+
+from oracle import lib
+
+encode = sub("gguf_encode")
 
 pytestmark = pytest.mark.gpu
 TS = {12: 144, 13: 176, 14: 210}

@@ -13,7 +13,10 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import encode, lib, np_oracle, torch_chain
+from conftest import sub
+from oracle import lib, np_oracle, torch_chain
+
+encode = sub("gguf_encode")
 
 F16, BF16, F32 = 0, 1, 2
 TD = {F16: torch.float16, BF16: torch.bfloat16, F32: torch.float32}

@@ -12,7 +12,11 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import encode, lib
+from conftest import sub
+
+from oracle import lib
+
+encode = sub("gguf_encode")
 
 F16, BF16, F32 = 0, 1, 2
 ALL_TYPES = [2, 3, 6, 7, 8, 10, 11, 12, 13, 14]
