@@ -1,16 +1,17 @@
 // Int8 W8A8 linear for gfx950: out[m, n] = OUT((float(acc) * xs[m]) * ws[n] (+ bias[n])), acc = sum_k xq[m, k] *
 // wq[n, k] exactly in int32 -- the role of kitchen's cutlass_int8_dequant (enhancers/fused_int8.py:191-206).
 //
-// Tiling: a 256-thread workgroup computes a BM x BN tile with 2 x 2 waves; a wave owns WM x WN 32x32 tiles of
-// v_mfma_i32_32x32x32_i8 (64 lanes x 16 int8 per operand, 16 int32 accumulators per lane). K advances in stages
-// of 128 bytes: each stage of A (xq rows) and B (wq rows, K-major like A) is loaded from global memory into
-// registers one stage ahead and written to a double-buffered LDS tile. Rows are 128 bytes = 8 chunks of 16 bytes;
-// chunk c of row r sits at chunk slot c ^ ((r >> 1) & 7), so the 16 lanes of each quarter-wave hit 16 different
-// 16-byte bank groups both when a stage is written and when 32 rows' fragments are read.
+// Operand layout (both operands K-major): lane l of a v_mfma_i32_32x32x32_i8 fragment holds 16 bytes of row l % 32
+// at K offset 16 * (l / 32) of the 32-wide K step. Result layout: lane l, register i holds row 8 (i / 4) +
+// 4 (l / 32) + i % 4, column l % 32 of the 32x32 tile.
 //
-// Operand layout (both operands the same): lane l of a 32x32x32 fragment holds 16 bytes of row l % 32 at K offset
-// 16 * (l / 32) of the 32-wide K step. Result layout: lane l, register i holds row 8 (i / 4) + 4 (l / 32) + i % 4,
-// column l % 32 of the 32x32 tile.
+// Two kernels:
+//  * gemm_i8_dl (K % 64 == 0, the workload): 256 x 256 tiles of 8 waves (4 x 2 MFMA tiles each), operands streamed
+//    global -> LDS by the load unit (no register staging) through a 4-stage ring of 64-byte K stages, and an
+//    epilogue that stages the rounded tile in LDS and stores whole 16-byte runs of output rows.
+//  * gemm_i8 (K % 16 == 0 otherwise): 2 x 2 waves, predicated loads staged through registers into a
+//    double-buffered LDS tile of 128-byte K stages. Rows are 8 chunks of 16 bytes; chunk c of row r sits at slot
+//    c ^ (((r >> 1) ^ ((r & 1) << 2)) & 7), conflict-free for stage writes and fragment reads.
 //
 // Tile order is XCD-aware: workgroup w runs on XCD w % 8, so consecutive tile indices are dealt to one XCD's
 // workgroups and that XCD's L2 sees neighbouring tiles (they share A rows / B rows); within the order, tiles are
@@ -23,19 +24,10 @@ namespace wf {
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBK = 128;        // K bytes per stage
+constexpr int kBK = 128;        // K bytes per stage of gemm_i8
 constexpr int kGroupM = 8;      // tile-rows per group of the tile order
 
-#ifndef GEMM_SWZ_NEW
-#define GEMM_SWZ_NEW 1
-#endif
-__device__ __forceinline__ int swz(int row, int chunk) {
-#if GEMM_SWZ_NEW
-    return chunk ^ (((row >> 1) ^ ((row & 1) << 2)) & 7);
-#else
-    return chunk ^ ((row >> 1) & 7);
-#endif
-}
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ (((row >> 1) ^ ((row & 1) << 2)) & 7); }
 
 __device__ __forceinline__ float to_f32_out(const void* p, int64_t i, int dt) {
     if (dt == WF_BF16) return __uint_as_float((uint32_t)static_cast<const uint16_t*>(p)[i] << 16);
@@ -185,86 +177,101 @@ __global__ __launch_bounds__(256) void gemm_i8(const int8_t* __restrict__ A, con
     }
 }
 
-// ---------------------------------------------------------------------------------------- K % 128 == 0 path
-// The same tiling with the main loop arranged for the MFMA pipe: A / B stages come in through buffer loads whose
-// resource starts at the tile's first row and ends at the last valid row (rows past M or N read as zeros, with no
-// branch), fragments are double-buffered in registers (the reads of K step ks + 1 are issued before the MFMAs of
-// step ks), and the next stage's LDS writes follow the current stage's last fragment reads.
+// buffer resource over [base, base + bytes): loads past the end read as zeros, with no branch
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const int8_t* base, int64_t bytes) {
     const int32_t n = bytes > 0x7fffffff ? 0x7fffffff : (int32_t)bytes;
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(base), 0, n, 0x00020000);
 }
 
-#ifndef GEMM_I8_LSTORE_LATE
-#define GEMM_I8_LSTORE_LATE 0
-#endif
+// ------------------------------------------------------------------------- K % 64 == 0: direct-to-LDS ring
+// The same tiling with the operands streamed through a 4-stage LDS ring of 64-byte K stages. The loads go from
+// global memory straight into LDS (buffer_load_dwordx4 ... lds: lane l of an instruction writes the 16 bytes at LDS
+// slot l of a 1 KiB run, so the swizzle is applied on the global side -- lane l loads the chunk that belongs in slot
+// l), with no register staging and no LDS write instructions; rows past M or N read as zeros. Stage kt + 3 is issued
+// while stage kt is computed. The barrier at the top of stage kt certifies that stage kt + 1 has landed (every wave
+// waited for its own loads) and that stage kt - 1 is no longer read, so the wave can prefetch stage kt + 1's first
+// fragments during stage kt and never waits on LDS right after a barrier. Rows are 64 bytes = 4 chunks; chunk c
+// of row r sits at slot c ^ ((r >> 2) & 3), conflict-free for the 16 lanes that read 16 rows' same chunk.
+constexpr int kDlBK = 64;
+constexpr int kDlStages = 4;
 
-// VM x VN waves, each owning WM x WN 32x32 tiles: BM = 32 VM WM, BN = 32 VN WN, 64 VM VN threads.
+__device__ __forceinline__ int swz4(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
+
+// 16 bytes per lane from buffer r at voffset + soffset into LDS slot `lane` of the 1 KiB run at lds (wave-uniform).
+// The address-space cast is device code only; the host pass of this file never sees it.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset, int soffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, soffset,
+                                             0, 0);
+#endif
+}
+
+__device__ __forceinline__ void wave_barrier_sync() {
+    // s_barrier without the workgroup fence __syncthreads adds (that fence waits for every outstanding load,
+    // which would drain the ring); the memory clobber keeps the compiler from moving LDS accesses across it
+    asm volatile("s_barrier" ::: "memory");
+}
+
 template <int VM, int VN, int WM, int WN, int OUT, bool BIAS, bool RESID>
-__global__ __launch_bounds__(64 * VM * VN) void gemm_i8_k128(const int8_t* __restrict__ A,
-                                                             const int8_t* __restrict__ B,
-                                                             const float* __restrict__ xs,
-                                                             const float* __restrict__ ws,
-                                                             const void* __restrict__ bias, void* __restrict__ out,
-                                                             int M, int N, int K, Residual res) {
-    constexpr int NT = 64 * VM * VN;
+__global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
+                                                           const float* __restrict__ xs,
+                                                           const float* __restrict__ ws,
+                                                           const void* __restrict__ bias, void* __restrict__ out,
+                                                           int M, int N, int K, Residual res) {
+    constexpr int NT = 64 * VM * VN, NW = NT / 64;
     constexpr int BM = VM * WM * 32, BN = VN * WN * 32;
-    constexpr int ACH = BM * 8 / NT, BCH = BN * 8 / NT;
-    constexpr int KS = kBK / 32;
-    __shared__ uint4 lds[2][(BM + BN) * 8];
+    constexpr int AI = BM / 16, BI = BN / 16;             // 1 KiB load instructions per stage (16 rows each)
+    constexpr int IPW = (AI + BI) / NW;                   // per wave
+    static_assert((AI + BI) % NW == 0, "whole load instructions per wave");
+    constexpr int SLOTS = (BM + BN) * 4;                  // 16-byte slots per stage
+    __shared__ i32x4 st0[SLOTS], st1[SLOTS], st2[SLOTS], st3[SLOTS];
     const int ntm = (M + BM - 1) / BM, ntn = (N + BN - 1) / BN;
     int tm, tn;
     tile_of(blockIdx.x, ntm * ntn, ntm, ntn, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);     // wave-uniform: scalar load bases
     const int wm = wave / VN, wn = wave % VN;
-    const int nk = K / kBK;
-    const __amdgpu_buffer_rsrc_t ra_rsrc = tile_rsrc(A + (int64_t)m0 * K, (int64_t)(M - m0) * K);
-    const __amdgpu_buffer_rsrc_t rb_rsrc = tile_rsrc(B + (int64_t)n0 * K, (int64_t)(N - n0) * K);
-
-    uint32_t aoff[ACH], boff[BCH];
-    int aslot[ACH], bslot[BCH];
+    const int nk = K / kDlBK;
+    const __amdgpu_buffer_rsrc_t ra = tile_rsrc(A + (int64_t)m0 * K, (int64_t)(M - m0) * K);
+    const __amdgpu_buffer_rsrc_t rb = tile_rsrc(B + (int64_t)n0 * K, (int64_t)(N - n0) * K);
+    // this wave's load instructions: global chunk run gi = wave * IPW + q (A rows for gi < AI, then B rows)
+    uint32_t voff[IPW];
 #pragma unroll
-    for (int i = 0; i < ACH; i++) {
-        const int idx = tid + NT * i, r = idx >> 3, c = idx & 7;
-        aoff[i] = (uint32_t)(r * K + 16 * c);
-        aslot[i] = r * 8 + swz(r, c);
+    for (int q = 0; q < IPW; q++) {
+        const int gi = wave * IPW + q;
+        const int r = (gi < AI ? gi : gi - AI) * 16 + (lane >> 2);
+        voff[q] = (uint32_t)(r * K + 16 * swz4(r, lane & 3));
     }
+    auto issue = [&](i32x4* st, int kt) {
+        const int k0 = kt * kDlBK;
 #pragma unroll
-    for (int i = 0; i < BCH; i++) {
-        const int idx = tid + NT * i, r = idx >> 3, c = idx & 7;
-        boff[i] = (uint32_t)(r * K + 16 * c);
-        bslot[i] = BM * 8 + r * 8 + swz(r, c);
-    }
-    i32x4 ra[ACH], rb[BCH];
-    auto gload = [&](int kt) {
-        const uint32_t k0 = (uint32_t)kt * kBK;
-#pragma unroll
-        for (int i = 0; i < ACH; i++) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(ra_rsrc, aoff[i] + k0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < BCH; i++) rb[i] = __builtin_amdgcn_raw_buffer_load_b128(rb_rsrc, boff[i] + k0, 0, 0);
-    };
-    auto lstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < ACH; i++) lds[buf][aslot[i]] = __builtin_bit_cast(uint4, ra[i]);
-#pragma unroll
-        for (int i = 0; i < BCH; i++) lds[buf][bslot[i]] = __builtin_bit_cast(uint4, rb[i]);
+        for (int q = 0; q < IPW; q++) {
+            const int gi = wave * IPW + q;
+            lds_dma16(gi < AI ? ra : rb, st + 64 * gi, voff[q] + (uint32_t)k0, 0);   // k0 inside the range check
+        }
     };
     const int lr = lane & 31, lk = lane >> 5;
-    int arow[WM], brow[WN];
+    int aslot[WM][2], bslot[WN][2];
 #pragma unroll
-    for (int i = 0; i < WM; i++) arow[i] = wm * WM * 32 + i * 32 + lr;
+    for (int i = 0; i < WM; i++) {
+        const int row = wm * WM * 32 + i * 32 + lr;
 #pragma unroll
-    for (int j = 0; j < WN; j++) brow[j] = BM + wn * WN * 32 + j * 32 + lr;
+        for (int ks = 0; ks < 2; ks++) aslot[i][ks] = row * 4 + swz4(row, 2 * ks + lk);
+    }
+#pragma unroll
+    for (int j = 0; j < WN; j++) {
+        const int row = wn * WN * 32 + j * 32 + lr;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) bslot[j][ks] = BM * 4 + row * 4 + swz4(row, 2 * ks + lk);
+    }
     i32x4 fa[2][WM], fb[2][WN];
-    auto fread = [&](int buf, int ks, int set) {
-        const int ch = 2 * ks + lk;
+    auto fread = [&](const i32x4* st, int ks, int set) {
 #pragma unroll
-        for (int i = 0; i < WM; i++) fa[set][i] = __builtin_bit_cast(i32x4, lds[buf][arow[i] * 8 + swz(arow[i], ch)]);
+        for (int i = 0; i < WM; i++) fa[set][i] = st[aslot[i][ks]];
 #pragma unroll
-        for (int j = 0; j < WN; j++) fb[set][j] = __builtin_bit_cast(i32x4, lds[buf][brow[j] * 8 + swz(brow[j], ch)]);
+        for (int j = 0; j < WN; j++) fb[set][j] = st[bslot[j][ks]];
     };
-
     i32x16 acc[WM][WN];
 #pragma unroll
     for (int i = 0; i < WM; i++)
@@ -272,34 +279,110 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_k128(const int8_t* __res
         for (int j = 0; j < WN; j++)
 #pragma unroll
             for (int e = 0; e < 16; e++) acc[i][j][e] = 0;
+    auto mfmas = [&](int set) {
+#pragma unroll
+        for (int i = 0; i < WM; i++)
+#pragma unroll
+            for (int j = 0; j < WN; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
+    };
+    // vmcnt waits (lgkmcnt and expcnt left at their maxima)
+    constexpr int kWaitIPW = (IPW & 15) | ((IPW >> 4) << 14) | (7 << 4) | (15 << 8);
 
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    fread(0, 0, 0);
-    for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < nk;
-        if (more) gload(kt + 1);
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-            const int set = ks & 1;
-            if (ks + 1 < KS) fread(cur, ks + 1, set ^ 1);
-#pragma unroll
-            for (int i = 0; i < WM; i++)
-#pragma unroll
-                for (int j = 0; j < WN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
-            if (!GEMM_I8_LSTORE_LATE && ks == KS - 2 && more) lstore(cur ^ 1);
-        }
-        if (more) {
-            if (GEMM_I8_LSTORE_LATE) lstore(cur ^ 1);     // the other buffer: nobody reads it in this stage
-            __syncthreads();
-            fread(cur ^ 1, 0, 0);
-        }
+    constexpr int kWait2IPW = ((2 * IPW) & 15) | (((2 * IPW) >> 4) << 14) | (7 << 4) | (15 << 8);
+    // The ring always issues: stages at or past K read past the row's end -- inside the buffer range (other rows'
+    // bytes) or past it (zeros) -- into a buffer no later stage reads. Branch-free issue keeps the compiler's
+    // per-buffer tracking of the outstanding loads exact, so it adds no waits of its own before LDS reads.
+    issue(st0, 0);
+    issue(st1, 1);
+    issue(st2, 2);
+    __builtin_amdgcn_s_waitcnt(kWait2IPW);                       // stage 0 landed; 1 and 2 may be in flight
+    wave_barrier_sync();
+    fread(st0, 0, 0);
+    // one ring step: stage kt in buffer CUR; NXT holds kt + 1, FREE (kt - 1) receives kt + 3
+    auto step = [&](int kt, i32x4* cur, i32x4* nxt, i32x4* free_) {
+        __builtin_amdgcn_s_waitcnt(kWaitIPW);                    // stage kt + 1 landed (kt + 2 may be in flight)
+        wave_barrier_sync();
+        issue(free_, kt + 3);
+        fread(cur, 1, 1);
+        mfmas(0);
+        fread(nxt, 0, 0);
+        mfmas(1);
+    };
+    int kt = 0;
+    for (; kt + 4 <= nk; kt += 4) {
+        step(kt, st0, st1, st3);
+        step(kt + 1, st1, st2, st0);
+        step(kt + 2, st2, st3, st1);
+        step(kt + 3, st3, st0, st2);
     }
+    if (kt < nk) step(kt, st0, st1, st3);
+    if (kt + 1 < nk) step(kt + 1, st1, st2, st0);
+    if (kt + 2 < nk) step(kt + 2, st2, st3, st1);
 
     // epilogue: (float(acc) * xs[m]) * ws[n] (+ bias[n]), rounded once to OUT
+    if constexpr (!RESID) {
+        // Through LDS: each wave writes its WM*32 x WN*32 tile, rounded, into its own LDS region (row-major,
+        // WN*32 values a row), then stores whole 16-byte runs of output rows. The ring is idle by now: every
+        // wave's last loads have landed (s_waitcnt) and every wave is past its last fragment reads (barrier).
+        constexpr int TR = WM * 32, TC = WN * 32;          // this wave's rows and columns
+        static_assert(TR * TC * 2 <= SLOTS * 16 * 4 / NW, "the output tile fits in the ring");
+        __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
+        wave_barrier_sync();
+        constexpr int PER_BUF = SLOTS * 16 / (TR * TC * 2); // wave regions per ring buffer
+        i32x4* buf = wave / PER_BUF == 0 ? st0 : wave / PER_BUF == 1 ? st1 : wave / PER_BUF == 2 ? st2 : st3;
+        uint16_t* ot = reinterpret_cast<uint16_t*>(buf) + (wave % PER_BUF) * TR * TC;
+        const int mw = m0 + wm * TR, nw = n0 + wn * TC;
+#pragma unroll
+        for (int j = 0; j < WN; j++) {
+            const int n = nw + j * 32 + lr;
+            const float wsn = n < N ? ws[n] : 0.0f;
+            const float bn = BIAS && n < N ? to_f32_out(bias, n, OUT) : 0.0f;
+#pragma unroll
+            for (int i = 0; i < WM; i++) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int r0 = i * 32 + 8 * q + 4 * lk;    // rows r0 .. r0 + 3 of this wave's tile
+                    float xm[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) xm[e] = mw + r0 + e < M ? xs[mw + r0 + e] : 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        float t = ((float)acc[i][j][4 * q + e] * xm[e]) * wsn;
+                        if (BIAS) t = t + bn;
+                        ot[(r0 + e) * TC + j * 32 + lr] = OUT == WF_BF16 ? __builtin_bit_cast(uint16_t, (__bf16)t)
+                                                                         : __builtin_bit_cast(uint16_t, (_Float16)t);
+                    }
+                }
+            }
+        }
+        // the wave reads back only its own region: its LDS writes and reads execute in order
+        const uint4* ov = reinterpret_cast<const uint4*>(ot);
+        constexpr int RUNS = TC / 8;                       // 16-byte runs per row
+        uint16_t* Y = static_cast<uint16_t*>(out);
+        if ((N & 7) == 0) {
+#pragma unroll
+            for (int it = 0; it < TR * RUNS / 64; it++) {
+                const int q = it * 64 + lane, r = q / RUNS, c = q % RUNS;
+                const int m = mw + r, n = nw + 8 * c;
+                const uint4 v = ov[q];
+                if (m < M && n < N) *reinterpret_cast<uint4*>(Y + (int64_t)m * N + n) = v;   // N % 8: whole runs
+            }
+        } else {
+            for (int it = 0; it < TR * RUNS / 64; it++) {
+                const int q = it * 64 + lane, r = q / RUNS, c = q % RUNS;
+                const int m = mw + r;
+                if (m >= M) continue;
+                const uint16_t* row = ot + r * TC + 8 * c;
+                for (int e = 0; e < 8; e++) {
+                    const int n = nw + 8 * c + e;
+                    if (n < N) Y[(int64_t)m * N + n] = row[e];
+                }
+            }
+        }
+        return;
+    }
+    // the residual form keeps float32 until its single rounding: element stores
 #pragma unroll
     for (int j = 0; j < WN; j++) {
         const int n = n0 + wn * WN * 32 + j * 32 + lr;
@@ -330,62 +413,61 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_k128(const int8_t* __res
     }
 }
 
-#ifndef GEMM_I8_SHAPE
-#define GEMM_I8_SHAPE 2
-#endif
-
-// K % 128 == 0: the tile shape by output size. Shape 1: 4 waves of 4 x 4 tiles (256 x 256, one wave per SIMD);
-// shape 2: 8 waves of 4 x 2 tiles (256 x 256, two waves per SIMD); small outputs: 4 waves of 2 x 2 (128 x 128).
+// K % 64 == 0: the direct-to-LDS kernel. 256 x 256 tiles (8 waves of 4 x 2 MFMA tiles) for all but the smallest
+// outputs; below 128 such tiles, 256 x 128 tiles (4 waves, one per SIMD) put more workgroups on the chip.
 template <int VM, int VN, int WM, int WN, int OUT>
-static void launch_k128_shape(const int8_t* A, const int8_t* B, const float* xs, const float* ws, const void* bias,
-                              void* out, int M, int N, int K, Residual r, bool resid, hipStream_t s) {
+static void launch_dl_shape(const int8_t* A, const int8_t* B, const float* xs, const float* ws, const void* bias,
+                            void* out, int M, int N, int K, Residual r, bool resid, hipStream_t s) {
     constexpr int BM = VM * WM * 32, BN = VN * WN * 32, NT = 64 * VM * VN;
     const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    if (resid) gemm_i8_k128<VM, VN, WM, WN, OUT, false, true><<<dim3(tiles), NT, 0, s>>>(A, B, xs, ws, nullptr, out, M, N, K, r);
-    else if (bias) gemm_i8_k128<VM, VN, WM, WN, OUT, true, false><<<dim3(tiles), NT, 0, s>>>(A, B, xs, ws, bias, out, M, N, K, r);
-    else gemm_i8_k128<VM, VN, WM, WN, OUT, false, false><<<dim3(tiles), NT, 0, s>>>(A, B, xs, ws, bias, out, M, N, K, r);
+    if (resid) gemm_i8_dl<VM, VN, WM, WN, OUT, false, true><<<dim3(tiles), NT, 0, s>>>(A, B, xs, ws, nullptr, out, M, N, K, r);
+    else if (bias) gemm_i8_dl<VM, VN, WM, WN, OUT, true, false><<<dim3(tiles), NT, 0, s>>>(A, B, xs, ws, bias, out, M, N, K, r);
+    else gemm_i8_dl<VM, VN, WM, WN, OUT, false, false><<<dim3(tiles), NT, 0, s>>>(A, B, xs, ws, bias, out, M, N, K, r);
 }
 
 template <int OUT>
-static void launch_k128(const int8_t* A, const int8_t* B, const float* xs, const float* ws, const void* bias,
-                        void* out, int M, int N, int K, Residual r, bool resid, hipStream_t s) {
+static void launch_dl(const int8_t* A, const int8_t* B, const float* xs, const float* ws, const void* bias,
+                      void* out, int M, int N, int K, Residual r, bool resid, hipStream_t s) {
     const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
-    if (big_tiles < 512) launch_k128_shape<2, 2, 2, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
-    else if (GEMM_I8_SHAPE == 1) launch_k128_shape<2, 2, 4, 4, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
-    else launch_k128_shape<2, 4, 4, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
+    if (big_tiles < 128) launch_dl_shape<2, 2, 4, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
+    else launch_dl_shape<2, 4, 4, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
 }
 
-template <int WM, int WN, int OUT>
-static void launch_gemm(const int8_t* A, const int8_t* B, const float* xs, const float* ws, const void* bias,
-                        void* out, int M, int N, int K, hipStream_t s) {
-    constexpr int BM = 2 * WM * 32, BN = 2 * WN * 32;
-    const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    if (K % kBK == 0) {
-        launch_k128<OUT>(A, B, xs, ws, bias, out, M, N, K, {}, false, s);
-        return;
-    }
-    if (bias) gemm_i8<WM, WN, OUT, true><<<dim3(tiles), 256, 0, s>>>(A, B, xs, ws, bias, out, M, N, K);
-    else gemm_i8<WM, WN, OUT, false><<<dim3(tiles), 256, 0, s>>>(A, B, xs, ws, bias, out, M, N, K);
-}
-
+// K % 16 == 0 otherwise: the predicated register-staged kernel
 template <int OUT>
 static void dispatch(const int8_t* A, const int8_t* B, const float* xs, const float* ws, const void* bias,
                      void* out, int M, int N, int K, hipStream_t s) {
+    if (K % kDlBK == 0) {
+        launch_dl<OUT>(A, B, xs, ws, bias, out, M, N, K, {}, false, s);
+        return;
+    }
     // large outputs: 256 x 256 tiles (4 x 4 MFMA tiles per wave); small ones keep 128 x 128 to fill the chip
     const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
-    if (big_tiles >= 512) launch_gemm<4, 4, OUT>(A, B, xs, ws, bias, out, M, N, K, s);
-    else launch_gemm<2, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, s);
+    if (big_tiles >= 512) {
+        const int tiles = ((M + 255) / 256) * ((N + 255) / 256);
+        if (bias) gemm_i8<4, 4, OUT, true><<<dim3(tiles), 256, 0, s>>>(A, B, xs, ws, bias, out, M, N, K);
+        else gemm_i8<4, 4, OUT, false><<<dim3(tiles), 256, 0, s>>>(A, B, xs, ws, bias, out, M, N, K);
+    } else {
+        const int tiles = ((M + 127) / 128) * ((N + 127) / 128);
+        if (bias) gemm_i8<2, 2, OUT, true><<<dim3(tiles), 256, 0, s>>>(A, B, xs, ws, bias, out, M, N, K);
+        else gemm_i8<2, 2, OUT, false><<<dim3(tiles), 256, 0, s>>>(A, B, xs, ws, bias, out, M, N, K);
+    }
 }
 
-template <int WM, int WN>
-static void launch_resid(const int8_t* A, const int8_t* B, const float* xs, const float* ws, void* out, int M, int N,
-                         int K, Residual r, hipStream_t s) {
-    constexpr int BM = 2 * WM * 32, BN = 2 * WN * 32;
-    const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    if (K % kBK == 0)
-        launch_k128<WF_BF16>(A, B, xs, ws, nullptr, out, M, N, K, r, true, s);
-    else
-        gemm_i8<WM, WN, WF_BF16, false, true><<<dim3(tiles), 256, 0, s>>>(A, B, xs, ws, nullptr, out, M, N, K, r);
+static void dispatch_resid(const int8_t* A, const int8_t* B, const float* xs, const float* ws, void* out, int M, int N,
+                           int K, Residual r, hipStream_t s) {
+    if (K % kDlBK == 0) {
+        launch_dl<WF_BF16>(A, B, xs, ws, nullptr, out, M, N, K, r, true, s);
+        return;
+    }
+    const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+    if (big_tiles >= 512) {
+        const int tiles = ((M + 255) / 256) * ((N + 255) / 256);
+        gemm_i8<4, 4, WF_BF16, false, true><<<dim3(tiles), 256, 0, s>>>(A, B, xs, ws, nullptr, out, M, N, K, r);
+    } else {
+        const int tiles = ((M + 127) / 128) * ((N + 127) / 128);
+        gemm_i8<2, 2, WF_BF16, false, true><<<dim3(tiles), 256, 0, s>>>(A, B, xs, ws, nullptr, out, M, N, K, r);
+    }
 }
 
 }  // namespace wf
@@ -405,9 +487,7 @@ extern "C" int wf_linear_i8_residual(const int8_t* xq, const int8_t* wq, const f
     if (M >= (1LL << 31) || N >= (1LL << 31) || K > 131071) { set_error("wf_linear_i8_residual: sizes too large"); return WF_EUNSUPPORTED; }
     Residual r{static_cast<const uint16_t*>(gate_bf16), static_cast<const uint16_t*>(resid_bf16), (int)rows_per_group};
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
-    if (big_tiles >= 512) launch_resid<4, 4>(xq, wq, xs, ws, out_bf16, (int)M, (int)N, (int)K, r, s);
-    else launch_resid<2, 2>(xq, wq, xs, ws, out_bf16, (int)M, (int)N, (int)K, r, s);
+    dispatch_resid(xq, wq, xs, ws, out_bf16, (int)M, (int)N, (int)K, r, s);
     WF_LAUNCH_CHECK("wf_linear_i8_residual launch");
     return WF_OK;
 }
