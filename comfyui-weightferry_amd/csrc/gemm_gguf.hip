@@ -4,18 +4,12 @@
 // The reference does the dequantisation into a bf16 weight in HBM and then ComfyUI-GGUF's F.linear; here the
 // weight never leaves the chip in bf16.
 //
-// Tiling: a 256-thread workgroup computes a 256 x 128 tile with 2 x 2 waves of 128 x 64 (4 x 2 tiles of
-// v_mfma_f32_32x32x16_bf16), and two workgroups share a CU (48 KB of LDS and at most 256 registers per lane each),
-// so one workgroup's barrier waits, dequantisation and LDS writes run while the other's MFMAs do. K advances in
-// stages of 64 (128 bytes of bf16 per row): the next stage's activations (buffer loads; rows past M read as zeros)
-// and raw weight blocks come into registers while the current stage's MFMAs run; after a barrier the stage is
-// written to the single LDS tile -- threads 2r and 2r + 1 take the two halves of weight row n0 + r (for Q4_K / Q5_K
-// exactly one 32-value sub-block each) and dequantise them on the way -- and a second barrier publishes it. A
-// 16-byte chunk swizzle keeps the LDS writes and fragment reads conflict-free. Fragment layout: lane l holds 8 bf16
-// of row l % 32 at K offset 8 * (l / 32) of the 16-wide step; result layout: lane l, register i -> row
-// 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32.
+// Fragment layout of v_mfma_f32_32x32x16_bf16: lane l holds 8 bf16 of row l % 32 at K offset 8 * (l / 32) of the
+// 16-wide step; result layout: lane l, register i -> row 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32. The tiling
+// and the pipeline are described at gemm_gguf_dl below.
 
 #include "kquant.h"
+#include "lds_ring.h"
 
 namespace wf {
 
@@ -24,8 +18,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kGroupMG = 8;
 
-__device__ __forceinline__ int swz8(int row, int chunk) { return chunk ^ (((row >> 1) ^ ((row & 1) << 2)) & 7); }
-
+// tile index of workgroup w among T tiles: XCD-aware (workgroup w runs on XCD w % 8, so one XCD's workgroups take
+// consecutive tiles and share their activation / weight rows in its L2), then groups of kGroupMG tile-rows
 __device__ __forceinline__ void tile_order(int w, int T, int ntm, int ntn, int& tm, int& tn) {
     int L = w;
     if ((T & 7) == 0) L = (w & 7) * (T >> 3) + (w >> 3);
@@ -38,86 +32,93 @@ __device__ __forceinline__ void tile_order(int w, int T, int ntm, int ntn, int& 
     tn = in / gm;
 }
 
-// ND dwords of the bytes at p + o (an even address): loads the ND + 1 aligned dwords from a = (p + o) & ~3, i.e.
-// [a, a + 4 ND + 4), which is [p + o - 2, p + o + 4 ND + 2) or [p + o, p + o + 4 ND + 4) -- callers keep both
-// inside the super-block -- and shifts them into place.
-template <int ND>
-__device__ __forceinline__ void load_words(const uint8_t* p, uint32_t o, uint32_t (&w)[ND]) {
-    const uintptr_t addr = reinterpret_cast<uintptr_t>(p + o);
-    const uint32_t* d = reinterpret_cast<const uint32_t*>(addr & ~(uintptr_t)3);
-    const uint32_t sh = (uint32_t)(addr & 3u) * 8u;
-    uint32_t raw[ND + 1];
-#pragma unroll
-    for (int i = 0; i <= ND; i++) raw[i] = d[i];
-#pragma unroll
-    for (int i = 0; i < ND; i++) w[i] = __builtin_amdgcn_alignbit(raw[i + 1], raw[i], sh);
+template <int QT>
+struct GGUFTs { static constexpr int TS = QT == 12 ? 144 : QT == 13 ? 176 : 210; };
+
+// ------------------------------------------------------------------------- direct-to-LDS ring (K % 256 == 0)
+// 256 x 256 tiles of 8 waves (2 x 4 waves of 4 x 2 MFMA tiles, two waves per SIMD), K in stages of 32 values through
+// a 4-stage LDS ring. The activation stage (256 rows x 64 bytes) goes global -> LDS by the load unit (buffer_load ...
+// lds), two 1 KiB instructions per wave; the weight stage is dequantised by the threads: thread t takes half
+// (16 values) of stage kt's 32-value sub-block of weight row t / 2, from raw bytes loaded one step earlier, and
+// writes 32 bytes of bf16 into the ring slot three stages ahead. Step s: barrier; issue activations of stage s + 3;
+// first MFMA half of stage s; wait until only those activation loads are in flight (so the raw bytes of stage s + 3
+// have landed -- the wait counts only the fixed number of activation loads); load the raw bytes of stage s + 4;
+// dequantise stage s + 3's into the free slot; second MFMA half, prefetching stage s + 1's first fragments. Stages at or past K
+// are still issued (reads past a row land in a slot never read, or read as zeros past the buffer), which keeps the
+// waits exact and the compiler's per-slot load tracking branch-free.
+template <int QT>
+struct QRaw;
+template <> struct QRaw<12> { uint4 hdr, q; };
+template <> struct QRaw<13> { uint4 hdr, q, qh; };
+template <> struct QRaw<14> { uint4 ql; uint32_t ql4; uint4 qh; uint32_t qh4; uint32_t sc, d, sh; };
+
+__device__ __forceinline__ uint4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t o) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0));
+}
+__device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t o) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0);
 }
 
-// Raw bytes a thread needs for its 32 values of a stage: half h (0 / 1) of the stage's 64-value slice `part`
-// (0..3) of one super-block.
+// raw bytes of values [16 h, 16 h + 16) of sub-block g (32 values) of the super-block at byte offset b
 template <int QT>
-struct HalfRaw;
-template <> struct HalfRaw<12> { uint4 hdr; uint32_t q[8]; };
-template <> struct HalfRaw<13> { uint4 hdr; uint32_t q[8]; uint32_t qh[8]; };
-template <> struct HalfRaw<14> { uint32_t ql[8]; uint32_t qh[8]; uint32_t sc; uint32_t d; };
-
-template <int QT>
-__device__ __forceinline__ void half_load(const uint8_t* sbp, int part, int h, HalfRaw<QT>& r) {
+__device__ __forceinline__ void q_load(__amdgpu_buffer_rsrc_t r, uint32_t b, int g, int h, QRaw<QT>& w) {
     if constexpr (QT == 12 || QT == 13) {
-        // Q4_K / Q5_K: sub-block 2 part + h = nibble h of qs[32 part .. 32 part + 32); Q5_K bit (2 part + h) of qh
-        constexpr int QS = QT == 12 ? 16 : 48;
-        r.hdr = *reinterpret_cast<const uint4*>(sbp);
-        const uint4 a = *reinterpret_cast<const uint4*>(sbp + QS + 32 * part);
-        const uint4 b = *reinterpret_cast<const uint4*>(sbp + QS + 32 * part + 16);
-        r.q[0] = a.x; r.q[1] = a.y; r.q[2] = a.z; r.q[3] = a.w;
-        r.q[4] = b.x; r.q[5] = b.y; r.q[6] = b.z; r.q[7] = b.w;
-        if constexpr (QT == 13) {
-            const uint4 c = *reinterpret_cast<const uint4*>(sbp + 16);
-            const uint4 e = *reinterpret_cast<const uint4*>(sbp + 32);
-            r.qh[0] = c.x; r.qh[1] = c.y; r.qh[2] = c.z; r.qh[3] = c.w;
-            r.qh[4] = e.x; r.qh[5] = e.y; r.qh[6] = e.z; r.qh[7] = e.w;
-        }
+        // Q4_K / Q5_K: qs[32 (g / 2) + 16 h ..] nibble g % 2; Q5_K qh[16 h ..] bit g (16-byte aligned blocks)
+        constexpr uint32_t QS = QT == 12 ? 16 : 48;
+        w.hdr = ld128(r, b);
+        w.q = ld128(r, b + QS + 32 * (g >> 1) + 16 * h);
+        if constexpr (QT == 13) w.qh = ld128(r, b + 16 + 16 * h);
     } else {
-        // Q6_K values 64 part + 32 h + i: ql[64 (part / 2) + 32 h + i] nibble (part & 1); qh[32 (part / 2) + i] at
-        // shift 2 (2 (part & 1) + h); scales 4 part + 2 h + i / 16; d. Reads stay inside the 210-byte block.
-        const int hh = part >> 1;
-        load_words<8>(sbp, 64 * hh + 32 * h, r.ql);       // bytes up to 96 + 36 = 132
-        load_words<8>(sbp, 128 + 32 * hh, r.qh);          // bytes up to 160 + 36 = 196
-        r.sc = *reinterpret_cast<const uint16_t*>(sbp + 192 + 4 * part + 2 * h);
-        r.d = *reinterpret_cast<const uint16_t*>(sbp + 208);
+        // Q6_K (210-byte blocks, 2-byte aligned): ql[64 hh + rr % 64 ..] nibble rr / 64, qh[128 + 32 hh + rr % 32 ..]
+        // at shift 2 (rr / 32), scale byte 192 + v0 / 16, d at 208; v0 = 32 g + 16 h, hh = v0 / 128, rr = v0 % 128.
+        // ql and qh are read as 20 bytes from their aligned-down dword (the shifts kept in sh; the window stays
+        // inside the block), the scale and d at their exact widths.
+        const int v0 = 32 * g + 16 * h, hh = v0 >> 7, rr = v0 & 127;
+        const uint32_t oql = b + 64 * hh + (rr & 63), oqh = b + 128 + 32 * hh + (rr & 31);
+        const uint32_t osc = b + 192 + (v0 >> 4), od = b + 208;
+        w.ql = ld128(r, oql & ~3u);
+        w.ql4 = ld32(r, (oql & ~3u) + 16);
+        w.qh = ld128(r, oqh & ~3u);
+        w.qh4 = ld32(r, (oqh & ~3u) + 16);
+        w.sc = __builtin_amdgcn_raw_buffer_load_b8(r, osc, 0, 0);     // exact widths: the block's last bytes
+        w.d = __builtin_amdgcn_raw_buffer_load_b16(r, od, 0, 0);      // never read past its end
+        w.sh = (oql & 3) | ((oqh & 3) << 8);
     }
 }
 
-// 32 values as 16 packed bf16 pairs (values 2i, 2i + 1 in o[i])
+// the 16 values as 8 packed bf16 pairs (values 2i, 2i + 1 in o[i]), the reference's rounding chain in MID
 template <int QT, int MID>
-__device__ __forceinline__ void half_dequant(const HalfRaw<QT>& r, int part, int h, uint32_t (&o)[16]) {
+__device__ __forceinline__ void q_dequant(const QRaw<QT>& w, int g, uint32_t (&o)[8]) {
     if constexpr (QT == 12 || QT == 13) {
-        const int sub = 2 * part + h;
-        const uint32_t ns = 4u * (uint32_t)h;
-        uint32_t q[8];
+        const uint32_t ns = 4u * (uint32_t)(g & 1);
+        const uint32_t qa[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+        uint32_t q[4];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            q[i] = (r.q[i] >> ns) & 0x0f0f0f0fu;
-            if constexpr (QT == 13) q[i] |= ((r.qh[i] >> sub) & 0x01010101u) << 4;
+        for (int i = 0; i < 4; i++) {
+            q[i] = (qa[i] >> ns) & 0x0f0f0f0fu;
+            if constexpr (QT == 13) {
+                const uint32_t qh[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
+                q[i] |= ((qh[i] >> g) & 0x01010101u) << 4;
+            }
         }
         uint32_t sc, m;
-        scale_min(r.hdr.y, r.hdr.z, r.hdr.w, sub, sc, m);
+        scale_min_nb(w.hdr.y, w.hdr.z, w.hdr.w, g, sc, m);
         if constexpr (MID == WF_F16) {
             const h2 off = h2s(-1024.0f);
-            const h2 pr = as_h2(r.hdr.x) * (as_h2(sc | (m << 16) | 0x64006400u) + off);   // (d * sc, dmin * m)
+            const h2 pr = as_h2(w.hdr.x) * (as_h2(sc | (m << 16) | 0x64006400u) + off);   // (d * sc, dmin * m)
             const h2 ds = lo2(pr), dm = hi2(pr);
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
+            for (int i = 0; i < 4; i++) {
                 const h2 v0 = ds * (biased_lo(q[i]) + off) - dm, v1 = ds * (biased_hi(q[i]) + off) - dm;
                 o[2 * i] = pack_bf16((float)v0[0], (float)v0[1]);
                 o[2 * i + 1] = pack_bf16((float)v1[0], (float)v1[1]);
             }
         } else {
-            const float d = round_to<MID>(f16_bits_to_f32(r.hdr.x & 0xffffu));
-            const float dmin = round_to<MID>(f16_bits_to_f32(r.hdr.x >> 16));
+            const float d = round_to<MID>(f16_bits_to_f32(w.hdr.x & 0xffffu));
+            const float dmin = round_to<MID>(f16_bits_to_f32(w.hdr.x >> 16));
             const float ds = round_to<MID>(d * (float)sc), dm = round_to<MID>(dmin * (float)m);
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
+            for (int i = 0; i < 4; i++) {
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; e++) v[e] = round_to<MID>(round_to<MID>(ds * (float)byte_of(q[i], e)) - dm);
@@ -126,34 +127,34 @@ __device__ __forceinline__ void half_dequant(const HalfRaw<QT>& r, int part, int
             }
         }
     } else {
-        const uint32_t ns = 4u * (uint32_t)(part & 1);
-        const uint32_t hs = 2u * (2u * (uint32_t)(part & 1) + (uint32_t)h);
-        uint32_t code[8];
+        const uint32_t shl = 8u * (w.sh & 3u), shh = 8u * ((w.sh >> 8) & 3u);
+        const uint32_t la[5] = {w.ql.x, w.ql.y, w.ql.z, w.ql.w, w.ql4};
+        const uint32_t ha[5] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w, w.qh4};
+        const uint32_t ns = 4u * (uint32_t)((g & 3) >> 1), hs = 2u * (uint32_t)(g & 3);
+        uint32_t code[4];
 #pragma unroll
-        for (int i = 0; i < 8; i++)
-            code[i] = ((r.ql[i] >> ns) & 0x0f0f0f0fu) | (((r.qh[i] >> hs) & 0x03030303u) << 4);
+        for (int i = 0; i < 4; i++) {
+            const uint32_t ql = __builtin_amdgcn_alignbit(la[i + 1], la[i], shl);
+            const uint32_t qh = __builtin_amdgcn_alignbit(ha[i + 1], ha[i], shh);
+            code[i] = ((ql >> ns) & 0x0f0f0f0fu) | (((qh >> hs) & 0x03030303u) << 4);
+        }
+        const int sc = (int8_t)(w.sc & 0xffu);
+        const uint32_t dbits = w.d & 0xffffu;
         if constexpr (MID == WF_F16) {
-            const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)r.d);
+            const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)dbits);
+            const _Float16 ds1 = d * (_Float16)(float)sc;                 // d * sc rounded to f16
+            h2 ds; ds[0] = ds1; ds[1] = ds1;
             const h2 off = h2s(-1056.0f);
-            h2 dd; dd[0] = d; dd[1] = d;
-            h2 sc2;
-            sc2[0] = (_Float16)(float)(int8_t)byte_of(r.sc, 0);
-            sc2[1] = (_Float16)(float)(int8_t)byte_of(r.sc, 1);
-            const h2 pd = dd * sc2;                       // (d * sc[first 16], d * sc[second 16]), rounded to f16
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const h2 ds = i < 4 ? lo2(pd) : hi2(pd);
+            for (int i = 0; i < 4; i++) {
                 const h2 v0 = ds * (biased_lo(code[i]) + off), v1 = ds * (biased_hi(code[i]) + off);
                 o[2 * i] = pack_bf16((float)v0[0], (float)v0[1]);
                 o[2 * i + 1] = pack_bf16((float)v1[0], (float)v1[1]);
             }
         } else {
-            const float d = round_to<MID>(f16_bits_to_f32(r.d));
-            const float ds0 = round_to<MID>(d * (float)(int8_t)byte_of(r.sc, 0));
-            const float ds1 = round_to<MID>(d * (float)(int8_t)byte_of(r.sc, 1));
+            const float ds = round_to<MID>(round_to<MID>(f16_bits_to_f32(dbits)) * (float)sc);
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float ds = i < 4 ? ds0 : ds1;
+            for (int i = 0; i < 4; i++) {
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; e++) v[e] = round_to<MID>(ds * (float)((int)byte_of(code[i], e) - 32));
@@ -164,88 +165,71 @@ __device__ __forceinline__ void half_dequant(const HalfRaw<QT>& r, int part, int
     }
 }
 
-template <int QT>
-struct GGUFTs { static constexpr int TS = QT == 12 ? 144 : QT == 13 ? 176 : 210; };
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int64_t bytes) {
-    const int32_t n = bytes > 0x7fffffff ? 0x7fffffff : (int32_t)bytes;
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, n, 0x00020000);
-}
-
-// VM x VN waves of WM x WN 32x32 tiles; 64 VM VN threads; stage = 64 K values. Thread t dequantises half h = t & 1
-// of weight row t >> 1 of the stage (BN = 32 VN WN = NT / 2 rows). WPE workgroups' waves share each SIMD.
-template <int VM, int VN, int WM, int WN, int QT, int MID, bool BIAS, int WPE>
-__global__ __launch_bounds__(64 * VM * VN) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void gemm_gguf(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
-                                                          const uint16_t* __restrict__ bias, uint16_t* __restrict__ Y,
-                                                          int M, int N, int K) {
-    constexpr int NT = 64 * VM * VN;
-    constexpr int BM = VM * WM * 32, BN = VN * WN * 32;
-    static_assert(BN * 2 == NT, "two threads per weight row");
+template <int QT, int MID, bool BIAS>
+__global__ __launch_bounds__(512) void gemm_gguf_dl(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
+                                                    const uint16_t* __restrict__ bias, uint16_t* __restrict__ Y,
+                                                    int M, int N, int K) {
+    constexpr int VN = 4, WM = 4, WN = 2;
+    constexpr int BM = 256, BN = 256;
     constexpr int TS = GGUFTs<QT>::TS;
-    constexpr int ACH = BM * 8 / NT;                   // 16-byte activation chunks per thread per stage
-    __shared__ uint4 lds[(BM + BN) * 8];
+    constexpr int IX = BM / 16 / 8;                    // activation DMA instructions per wave per stage
+    // separate activation and weight rings: the weight writes never alias an in-flight activation load
+    __shared__ uint4 xs0[BM * 4], xs1[BM * 4], xs2[BM * 4], xs3[BM * 4];
+    __shared__ uint4 ws0[BN * 4], ws1[BN * 4], ws2[BN * 4], ws3[BN * 4];
     const int ntm = (M + BM - 1) / BM, ntn = (N + BN - 1) / BN;
     int tm, tn;
     tile_order(blockIdx.x, ntm * ntn, ntm, ntn, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / VN, wn = wave % VN;
-    const int nk = K / 64;
-    const int sbs_per_row = K / 256;
-    const int wr = tid >> 1, wh = tid & 1;             // this thread's weight row in the tile, and its half
-    const bool wlive = n0 + wr < N;
-    const uint8_t* wrow_p = W + (int64_t)(wlive ? n0 + wr : 0) * sbs_per_row * TS;
-    const __amdgpu_buffer_rsrc_t xr = rows_rsrc(X + (int64_t)m0 * K, (int64_t)(M - m0) * K * 2);
-
-    uint32_t xoff[ACH];
-    int xslot[ACH];
+    const int nk = K / 32;
+    const uint32_t row_bytes = (uint32_t)(K / 256) * TS;
+    const __amdgpu_buffer_rsrc_t rx = tile_rsrc(X + (int64_t)m0 * K, (int64_t)(M - m0) * K * 2);
+    const __amdgpu_buffer_rsrc_t rw = tile_rsrc(W + (int64_t)n0 * row_bytes, (int64_t)(N - n0) * row_bytes);
+    uint32_t xoff[IX];
 #pragma unroll
-    for (int i = 0; i < ACH; i++) {
-        const int idx = tid + NT * i, r = idx >> 3, c = idx & 7;
-        xoff[i] = (uint32_t)(r * K + 8 * c) * 2u;
-        xslot[i] = r * 8 + swz8(r, c);
+    for (int q = 0; q < IX; q++) {
+        const int r = (wave * IX + q) * 16 + (lane >> 2);
+        xoff[q] = (uint32_t)r * (uint32_t)K * 2u + 16u * (uint32_t)swz4(r, lane & 3);
     }
-    uint4 ra[ACH];
-    HalfRaw<QT> rw;
-    auto gload = [&](int kt) {
-        const uint32_t k0 = (uint32_t)kt * 128u;       // bytes of bf16
+    auto issue_x = [&](uint4* st, int kt) {
 #pragma unroll
-        for (int i = 0; i < ACH; i++)
-            ra[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[i] + k0, 0, 0));
-        if (wlive) half_load<QT>(wrow_p + (kt >> 2) * TS, kt & 3, wh, rw);
+        for (int q = 0; q < IX; q++) lds_dma16(rx, st + 64 * (wave * IX + q), xoff[q] + (uint32_t)kt * 64u);
     };
-    auto lstore = [&](int kt) {
+    const int wr = tid >> 1, wh = tid & 1;
+    const uint32_t wbase = (uint32_t)wr * row_bytes;
+    auto wload = [&](QRaw<QT>& raw, int kt) { q_load<QT>(rw, wbase + (uint32_t)(kt >> 3) * TS, kt & 7, wh, raw); };
+    int wslot[2];
 #pragma unroll
-        for (int i = 0; i < ACH; i++) lds[xslot[i]] = ra[i];
-        uint32_t o[16];
-        if (wlive) {
-            half_dequant<QT, MID>(rw, kt & 3, wh, o);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; i++) o[i] = 0;
-        }
-        uint4* sb = lds + BM * 8 + wr * 8;
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-            sb[swz8(wr, 4 * wh + c)] = make_uint4(o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]);
+    for (int c = 0; c < 2; c++) wslot[c] = wr * 4 + swz4(wr, 2 * wh + c);
+    auto wstore = [&](uint4* st, const QRaw<QT>& raw, int kt) {
+        uint32_t o[8];
+        q_dequant<QT, MID>(raw, kt & 7, o);
+        lds_write16(st + wslot[0], make_uint4(o[0], o[1], o[2], o[3]));
+        lds_write16(st + wslot[1], make_uint4(o[4], o[5], o[6], o[7]));
     };
     const int lr = lane & 31, lk = lane >> 5;
-    int arow[WM], brow[WN];
+    int aslot[WM][2], bslot[WN][2];
 #pragma unroll
-    for (int i = 0; i < WM; i++) arow[i] = wm * WM * 32 + i * 32 + lr;
+    for (int i = 0; i < WM; i++) {
+        const int row = wm * WM * 32 + i * 32 + lr;
 #pragma unroll
-    for (int j = 0; j < WN; j++) brow[j] = wn * WN * 32 + j * 32 + lr;
+        for (int ks = 0; ks < 2; ks++) aslot[i][ks] = row * 4 + swz4(row, 2 * ks + lk);
+    }
+#pragma unroll
+    for (int j = 0; j < WN; j++) {
+        const int row = wn * WN * 32 + j * 32 + lr;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) bslot[j][ks] = row * 4 + swz4(row, 2 * ks + lk);
+    }
     bf16x8 fa[2][WM], fb[2][WN];
-    auto fread = [&](int ks, int set) {
-        const int ch = 2 * ks + lk;
-        const uint4* sa = lds;
-        const uint4* sb = lds + BM * 8;
+    auto fread = [&](const uint4* xst, const uint4* wst, int ks, int set) {
 #pragma unroll
-        for (int i = 0; i < WM; i++) fa[set][i] = __builtin_bit_cast(bf16x8, sa[arow[i] * 8 + swz8(arow[i], ch)]);
+        for (int i = 0; i < WM; i++) fa[set][i] = __builtin_bit_cast(bf16x8, xst[aslot[i][ks]]);
 #pragma unroll
-        for (int j = 0; j < WN; j++) fb[set][j] = __builtin_bit_cast(bf16x8, sb[brow[j] * 8 + swz8(brow[j], ch)]);
+        for (int j = 0; j < WN; j++) fb[set][j] = __builtin_bit_cast(bf16x8, wst[bslot[j][ks]]);
     };
-
     f32x16 acc[WM][WN];
 #pragma unroll
     for (int i = 0; i < WM; i++)
@@ -253,46 +237,99 @@ __global__ __launch_bounds__(64 * VM * VN) __attribute__((amdgpu_waves_per_eu(WP
         for (int j = 0; j < WN; j++)
 #pragma unroll
             for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+    auto mfmas = [&](int set) {
+#pragma unroll
+        for (int i = 0; i < WM; i++)
+#pragma unroll
+            for (int j = 0; j < WN; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
+    };
 
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    fread(0, 0);
-    for (int kt = 0; kt < nk; kt++) {
-        const bool more = kt + 1 < nk;
-        if (more) gload(kt + 1);
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            const int set = ks & 1;
-            if (ks < 3) fread(ks + 1, set ^ 1);
-#pragma unroll
-            for (int i = 0; i < WM; i++)
-#pragma unroll
-                for (int j = 0; j < WN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
-        }
-        if (more) {
-            __syncthreads();          // every wave is done reading this stage
-            lstore(kt + 1);
-            __syncthreads();
-            fread(0, 0);
-        }
+    QRaw<QT> wa, wb;                                   // raw bytes of even / odd stages
+    issue_x(xs0, 0);
+    issue_x(xs1, 1);
+    issue_x(xs2, 2);
+    wload(wa, 0);
+    wait_vm<0>();
+    wstore(ws0, wa, 0);
+    wload(wa, 1);
+    wait_vm<0>();
+    wstore(ws1, wa, 1);
+    wload(wa, 2);
+    wait_vm<0>();
+    wstore(ws2, wa, 2);
+    wload(wb, 3);
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));   // lgkmcnt(0): this thread's LDS writes are done
+    wave_barrier_sync();
+    fread(xs0, ws0, 0, 0);
+    // ring step: stage s in slot C, s + 1 in slot NX, and slot F (stage s - 1's) receives stage s + 3; RC holds the
+    // raw bytes of stage s + 3, RN receives those of stage s + 4
+    auto step = [&](int s, uint4* xc, uint4* wc, uint4* xn, uint4* wn_, uint4* xf, uint4* wf, QRaw<QT>& rc,
+                    QRaw<QT>& rn) {
+        wave_barrier_sync();
+        issue_x(xf, s + 3);
+        fread(xc, wc, 1, 1);
+        mfmas(0);
+        wait_vm<IX>();                                 // all but this step's activation loads have landed
+        __builtin_amdgcn_sched_barrier(0);             // nothing that reads the raw bytes moves above the wait
+        wload(rn, s + 4);                              // a whole step ahead of its use
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(1);                                      // independent of the dequantisation: they overlap
+        wstore(wf, rc, s + 3);
+        fread(xn, wn_, 0, 0);                          // stage s + 1's first fragments for the next step
+    };
+    int kt = 0;
+    for (; kt + 4 <= nk; kt += 4) {
+        step(kt, xs0, ws0, xs1, ws1, xs3, ws3, wb, wa);
+        step(kt + 1, xs1, ws1, xs2, ws2, xs0, ws0, wa, wb);
+        step(kt + 2, xs2, ws2, xs3, ws3, xs1, ws1, wb, wa);
+        step(kt + 3, xs3, ws3, xs0, ws0, xs2, ws2, wa, wb);
     }
+    if (kt < nk) step(kt, xs0, ws0, xs1, ws1, xs3, ws3, wb, wa);
+    if (kt + 1 < nk) step(kt + 1, xs1, ws1, xs2, ws2, xs0, ws0, wa, wb);
+    if (kt + 2 < nk) step(kt + 2, xs2, ws2, xs3, ws3, xs1, ws1, wb, wa);
 
+    // epilogue through LDS (the ring is idle once every load has landed and every wave is past its reads): each
+    // wave rounds its 128 x 64 tile to bf16 into its own 16 KiB ring slot, then stores whole 16-byte runs of rows
+    constexpr int TR = WM * 32, TC = WN * 32;
+    wait_vm<0>();
+    wave_barrier_sync();
+    static_assert(TR * TC * 2 == BM * 4 * 16, "one ring slot per wave");
+    uint4* buf = wave == 0 ? xs0 : wave == 1 ? xs1 : wave == 2 ? xs2 : wave == 3 ? xs3
+               : wave == 4 ? ws0 : wave == 5 ? ws1 : wave == 6 ? ws2 : ws3;
+    uint16_t* ot = reinterpret_cast<uint16_t*>(buf);
+    const int mw = m0 + wm * TR, nw = n0 + wn * TC;
 #pragma unroll
     for (int j = 0; j < WN; j++) {
-        const int n = n0 + wn * WN * 32 + j * 32 + lr;
-        if (n >= N) continue;
-        const float bn = BIAS ? __uint_as_float((uint32_t)bias[n] << 16) : 0.0f;
+        const int n = nw + j * 32 + lr;
+        const float bn = BIAS && n < N ? __uint_as_float((uint32_t)bias[n] << 16) : 0.0f;
 #pragma unroll
-        for (int i = 0; i < WM; i++) {
+        for (int i = 0; i < WM; i++)
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                const int m = m0 + wm * WM * 32 + i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
-                if (m >= M) continue;
                 float t = acc[i][j][e];
                 if (BIAS) t = t + bn;
-                Y[(int64_t)m * N + n] = __builtin_bit_cast(uint16_t, (__bf16)t);
+                ot[(i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3)) * TC + j * 32 + lr] = __builtin_bit_cast(uint16_t, (__bf16)t);
+            }
+    }
+    const uint4* ov = reinterpret_cast<const uint4*>(ot);   // the wave's own region: in-order LDS writes and reads
+    constexpr int RUNS = TC / 8;
+    if ((N & 7) == 0) {
+#pragma unroll
+        for (int it = 0; it < TR * RUNS / 64; it++) {
+            const int q = it * 64 + lane, r = q / RUNS, c = q % RUNS;
+            const int m = mw + r, n = nw + 8 * c;
+            const uint4 v = ov[q];
+            if (m < M && n < N) *reinterpret_cast<uint4*>(Y + (int64_t)m * N + n) = v;
+        }
+    } else {
+        for (int it = 0; it < TR * RUNS / 64; it++) {
+            const int q = it * 64 + lane, r = q / RUNS, c = q % RUNS;
+            const int m = mw + r;
+            if (m >= M) continue;
+            for (int e = 0; e < 8; e++) {
+                const int n = nw + 8 * c + e;
+                if (n < N) Y[(int64_t)m * N + n] = ot[r * TC + 8 * c + e];
             }
         }
     }
@@ -301,10 +338,9 @@ __global__ __launch_bounds__(64 * VM * VN) __attribute__((amdgpu_waves_per_eu(WP
 template <int QT, int MID>
 static void launch(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
                    hipStream_t s) {
-    // 4 waves (2 x 2) of 4 x 2 tiles: a 256 x 128 tile, two workgroups per CU
-    const int tiles = ((M + 255) / 256) * ((N + 127) / 128);
-    if (bias) gemm_gguf<2, 2, 4, 2, QT, MID, true, 2><<<dim3(tiles), 256, 0, s>>>(X, W, bias, Y, M, N, K);
-    else gemm_gguf<2, 2, 4, 2, QT, MID, false, 2><<<dim3(tiles), 256, 0, s>>>(X, W, bias, Y, M, N, K);
+    const int tiles = ((M + 255) / 256) * ((N + 255) / 256);
+    if (bias) gemm_gguf_dl<QT, MID, true><<<dim3(tiles), 512, 0, s>>>(X, W, bias, Y, M, N, K);
+    else gemm_gguf_dl<QT, MID, false><<<dim3(tiles), 512, 0, s>>>(X, W, bias, Y, M, N, K);
 }
 
 template <int QT>

@@ -17,7 +17,7 @@
 // workgroups and that XCD's L2 sees neighbouring tiles (they share A rows / B rows); within the order, tiles are
 // grouped GROUP_M tile-rows at a time.
 
-#include "wf_common.h"
+#include "lds_ring.h"
 
 namespace wf {
 
@@ -177,12 +177,6 @@ __global__ __launch_bounds__(256) void gemm_i8(const int8_t* __restrict__ A, con
     }
 }
 
-// buffer resource over [base, base + bytes): loads past the end read as zeros, with no branch
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const int8_t* base, int64_t bytes) {
-    const int32_t n = bytes > 0x7fffffff ? 0x7fffffff : (int32_t)bytes;
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(base), 0, n, 0x00020000);
-}
-
 // ------------------------------------------------------------------------- K % 64 == 0: direct-to-LDS ring
 // The same tiling with the operands streamed through a 4-stage LDS ring of 64-byte K stages. The loads go from
 // global memory straight into LDS (buffer_load_dwordx4 ... lds: lane l of an instruction writes the 16 bytes at LDS
@@ -194,23 +188,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const int8_t* base, 
 // of row r sits at slot c ^ ((r >> 2) & 3), conflict-free for the 16 lanes that read 16 rows' same chunk.
 constexpr int kDlBK = 64;
 constexpr int kDlStages = 4;
-
-__device__ __forceinline__ int swz4(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
-
-// 16 bytes per lane from buffer r at voffset + soffset into LDS slot `lane` of the 1 KiB run at lds (wave-uniform).
-// The address-space cast is device code only; the host pass of this file never sees it.
-__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset, int soffset) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, soffset,
-                                             0, 0);
-#endif
-}
-
-__device__ __forceinline__ void wave_barrier_sync() {
-    // s_barrier without the workgroup fence __syncthreads adds (that fence waits for every outstanding load,
-    // which would drain the ring); the memory clobber keeps the compiler from moving LDS accesses across it
-    asm volatile("s_barrier" ::: "memory");
-}
 
 template <int VM, int VN, int WM, int WN, int OUT, bool BIAS, bool RESID>
 __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
@@ -248,7 +225,7 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
 #pragma unroll
         for (int q = 0; q < IPW; q++) {
             const int gi = wave * IPW + q;
-            lds_dma16(gi < AI ? ra : rb, st + 64 * gi, voff[q] + (uint32_t)k0, 0);   // k0 inside the range check
+            lds_dma16(gi < AI ? ra : rb, st + 64 * gi, voff[q] + (uint32_t)k0);
         }
     };
     const int lr = lane & 31, lk = lane >> 5;
@@ -286,22 +263,18 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
             for (int j = 0; j < WN; j++)
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
     };
-    // vmcnt waits (lgkmcnt and expcnt left at their maxima)
-    constexpr int kWaitIPW = (IPW & 15) | ((IPW >> 4) << 14) | (7 << 4) | (15 << 8);
-
-    constexpr int kWait2IPW = ((2 * IPW) & 15) | (((2 * IPW) >> 4) << 14) | (7 << 4) | (15 << 8);
     // The ring always issues: stages at or past K read past the row's end -- inside the buffer range (other rows'
     // bytes) or past it (zeros) -- into a buffer no later stage reads. Branch-free issue keeps the compiler's
     // per-buffer tracking of the outstanding loads exact, so it adds no waits of its own before LDS reads.
     issue(st0, 0);
     issue(st1, 1);
     issue(st2, 2);
-    __builtin_amdgcn_s_waitcnt(kWait2IPW);                       // stage 0 landed; 1 and 2 may be in flight
+    wait_vm<2 * IPW>();                                          // stage 0 landed; 1 and 2 may be in flight
     wave_barrier_sync();
     fread(st0, 0, 0);
     // one ring step: stage kt in buffer CUR; NXT holds kt + 1, FREE (kt - 1) receives kt + 3
     auto step = [&](int kt, i32x4* cur, i32x4* nxt, i32x4* free_) {
-        __builtin_amdgcn_s_waitcnt(kWaitIPW);                    // stage kt + 1 landed (kt + 2 may be in flight)
+        wait_vm<IPW>();                                          // stage kt + 1 landed (kt + 2 may be in flight)
         wave_barrier_sync();
         issue(free_, kt + 3);
         fread(cur, 1, 1);

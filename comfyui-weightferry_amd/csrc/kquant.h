@@ -31,4 +31,15 @@ __device__ __forceinline__ void scale_min(uint32_t s0, uint32_t s1, uint32_t s2,
     }
 }
 
+// the same without a branch on sub (for a sub-block index that is uniform but unknown at compile time: a branch
+// there would split the caller's straight-line code)
+__device__ __forceinline__ void scale_min_nb(uint32_t s0, uint32_t s1, uint32_t s2, int sub, uint32_t& sc,
+                                             uint32_t& m) {
+    const int j = sub & 3;
+    const uint32_t a = byte_of(s0, j), b = byte_of(s1, j), c = byte_of(s2, j);
+    const uint32_t hi = 0u - (uint32_t)((sub >> 2) & 1);       // all ones for sub >= 4
+    sc = ((a & 63u) & ~hi) | (((c & 0xfu) | ((a >> 2) & 0x30u)) & hi);
+    m = ((b & 63u) & ~hi) | (((c >> 4) | ((b >> 2) & 0x30u)) & hi);
+}
+
 }  // namespace wf
