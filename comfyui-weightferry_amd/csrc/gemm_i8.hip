@@ -6,9 +6,10 @@
 // 4 (l / 32) + i % 4, column l % 32 of the 32x32 tile.
 //
 // Two kernels:
-//  * gemm_i8_dl (K % 64 == 0, the workload): 256 x 256 tiles of 8 waves (4 x 2 MFMA tiles each), operands streamed
-//    global -> LDS by the load unit (no register staging) through a 4-stage ring of 64-byte K stages, and an
-//    epilogue that stages the rounded tile in LDS and stores whole 16-byte runs of output rows.
+//  * gemm_i8_dl (K % 64 == 0, the workload): 256 x 320, 256 x 256 or 256 x 128 tiles (chosen per shape, see
+//    launch_dl), operands streamed global -> LDS by the load unit (no register staging) through a 4-stage ring of
+//    64-byte K stages, and an epilogue that stages the rounded tile in LDS and stores whole 16-byte runs of output
+//    rows.
 //  * gemm_i8 (K % 16 == 0 otherwise): 2 x 2 waves, predicated loads staged through registers into a
 //    double-buffered LDS tile of 128-byte K stages. Rows are 8 chunks of 16 bytes; chunk c of row r sits at slot
 //    c ^ (((r >> 1) ^ ((r & 1) << 2)) & 7), conflict-free for stage writes and fragment reads.
@@ -178,16 +179,17 @@ __global__ __launch_bounds__(256) void gemm_i8(const int8_t* __restrict__ A, con
 }
 
 // ------------------------------------------------------------------------- K % 64 == 0: direct-to-LDS ring
-// The same tiling with the operands streamed through a 4-stage LDS ring of 64-byte K stages. The loads go from
-// global memory straight into LDS (buffer_load_dwordx4 ... lds: lane l of an instruction writes the 16 bytes at LDS
-// slot l of a 1 KiB run, so the swizzle is applied on the global side -- lane l loads the chunk that belongs in slot
-// l), with no register staging and no LDS write instructions; rows past M or N read as zeros. Stage kt + 3 is issued
+// VM x VN waves of WM x WN MFMA tiles, the operands streamed through a 4-stage LDS ring of 64-byte K stages. The
+// loads go from global memory straight into LDS (buffer_load_dwordx4 ... lds: lane l of an instruction writes the 16
+// bytes at LDS slot l of a 1 KiB run, so the swizzle is applied on the global side -- lane l loads the chunk that
+// belongs in slot l), with no register staging and no LDS write instructions; rows past M or N read as zeros. When
+// the stage's 1 KiB runs do not divide evenly over the waves, the last waves' spare issues repeat the final run into
+// pad slots after the stage, so every wave issues (and waits for) the same count. Stage kt + 3 is issued
 // while stage kt is computed. The barrier at the top of stage kt certifies that stage kt + 1 has landed (every wave
 // waited for its own loads) and that stage kt - 1 is no longer read, so the wave can prefetch stage kt + 1's first
 // fragments during stage kt and never waits on LDS right after a barrier. Rows are 64 bytes = 4 chunks; chunk c
 // of row r sits at slot c ^ ((r >> 2) & 3), conflict-free for the 16 lanes that read 16 rows' same chunk.
 constexpr int kDlBK = 64;
-constexpr int kDlStages = 4;
 
 template <int VM, int VN, int WM, int WN, int OUT, bool BIAS, bool RESID>
 __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
@@ -198,9 +200,9 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
     constexpr int NT = 64 * VM * VN, NW = NT / 64;
     constexpr int BM = VM * WM * 32, BN = VN * WN * 32;
     constexpr int AI = BM / 16, BI = BN / 16;             // 1 KiB load instructions per stage (16 rows each)
-    constexpr int IPW = (AI + BI) / NW;                   // per wave
-    static_assert((AI + BI) % NW == 0, "whole load instructions per wave");
-    constexpr int SLOTS = (BM + BN) * 4;                  // 16-byte slots per stage
+    constexpr int IPW = (AI + BI + NW - 1) / NW;          // per wave; spare issues of the last waves fill pad slots
+    constexpr int SLOTS = NW * IPW * 64;                  // 16-byte slots per stage, pad slots after the B rows
+    static_assert(4 * SLOTS * 16 <= 160 * 1024, "the ring fits the LDS");
     __shared__ i32x4 st0[SLOTS], st1[SLOTS], st2[SLOTS], st3[SLOTS];
     const int ntm = (M + BM - 1) / BM, ntn = (N + BN - 1) / BN;
     int tm, tn;
@@ -216,7 +218,7 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
     uint32_t voff[IPW];
 #pragma unroll
     for (int q = 0; q < IPW; q++) {
-        const int gi = wave * IPW + q;
+        const int gi = min(wave * IPW + q, AI + BI - 1);  // a pad issue repeats the last B run into its pad slot
         const int r = (gi < AI ? gi : gi - AI) * 16 + (lane >> 2);
         voff[q] = (uint32_t)(r * K + 16 * swz4(r, lane & 3));
     }
@@ -299,11 +301,12 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
         // WN*32 values a row), then stores whole 16-byte runs of output rows. The ring is idle by now: every
         // wave's last loads have landed (s_waitcnt) and every wave is past its last fragment reads (barrier).
         constexpr int TR = WM * 32, TC = WN * 32;          // this wave's rows and columns
-        static_assert(TR * TC * 2 <= SLOTS * 16 * 4 / NW, "the output tile fits in the ring");
+        constexpr int PER_BUF = SLOTS * 16 / (TR * TC * 2); // wave regions per ring buffer
+        static_assert(PER_BUF >= 1 && NW <= PER_BUF * 4, "the output tiles fit in the ring");
         __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
         wave_barrier_sync();
-        constexpr int PER_BUF = SLOTS * 16 / (TR * TC * 2); // wave regions per ring buffer
-        i32x4* buf = wave / PER_BUF == 0 ? st0 : wave / PER_BUF == 1 ? st1 : wave / PER_BUF == 2 ? st2 : st3;
+        const int wb = wave / PER_BUF;
+        i32x4* buf = wb == 0 ? st0 : wb == 1 ? st1 : wb == 2 ? st2 : st3;
         uint16_t* ot = reinterpret_cast<uint16_t*>(buf) + (wave % PER_BUF) * TR * TC;
         const int mw = m0 + wm * TR, nw = n0 + wn * TC;
 #pragma unroll
@@ -386,8 +389,12 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
     }
 }
 
-// K % 64 == 0: the direct-to-LDS kernel. 256 x 256 tiles (8 waves of 4 x 2 MFMA tiles) for all but the smallest
-// outputs; below 128 such tiles, 256 x 128 tiles (4 waves, one per SIMD) put more workgroups on the chip.
+// K % 64 == 0: the direct-to-LDS kernel in one of three tilings, chosen by the modelled time: rounds of 256 workgroups
+// (one per CU) times the tile's area, over the tiling's measured MFMA efficiency.
+//   256 x 320: 8 waves of 2 x 5 MFMA tiles (64 x 160); fewest LDS fragment reads per MFMA, and 4096 x 5120 outputs
+//              make exactly 256 tiles.
+//   256 x 256: 8 waves of 4 x 2 MFMA tiles (128 x 64).
+//   256 x 128: 4 waves of 4 x 2 MFMA tiles, one per SIMD: more workgroups for small outputs.
 template <int VM, int VN, int WM, int WN, int OUT>
 static void launch_dl_shape(const int8_t* A, const int8_t* B, const float* xs, const float* ws, const void* bias,
                             void* out, int M, int N, int K, Residual r, bool resid, hipStream_t s) {
@@ -398,12 +405,20 @@ static void launch_dl_shape(const int8_t* A, const int8_t* B, const float* xs, c
     else gemm_i8_dl<VM, VN, WM, WN, OUT, false, false><<<dim3(tiles), NT, 0, s>>>(A, B, xs, ws, bias, out, M, N, K, r);
 }
 
+// modelled time of a tiling: whole rounds of 256 workgroups x tile area / relative efficiency (per mille)
+static int64_t dl_cost(int M, int N, int bm, int bn, int64_t eff) {
+    const int64_t tiles = (int64_t)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    return (tiles + 255) / 256 * bm * bn * 1000 / eff;
+}
+
 template <int OUT>
 static void launch_dl(const int8_t* A, const int8_t* B, const float* xs, const float* ws, const void* bias,
                       void* out, int M, int N, int K, Residual r, bool resid, hipStream_t s) {
-    const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
-    if (big_tiles < 128) launch_dl_shape<2, 2, 4, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
-    else launch_dl_shape<2, 4, 4, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
+    const int64_t c320 = dl_cost(M, N, 256, 320, 1030), c256 = dl_cost(M, N, 256, 256, 1000);
+    const int64_t c128 = dl_cost(M, N, 256, 128, 780);
+    if (c128 < c256 && c128 < c320) launch_dl_shape<2, 2, 4, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
+    else if (c256 < c320) launch_dl_shape<2, 4, 4, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
+    else launch_dl_shape<4, 2, 2, 5, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
 }
 
 // K % 16 == 0 otherwise: the predicated register-staged kernel
