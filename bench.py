@@ -124,8 +124,8 @@ def fused_leg(torch, native):
             def two_step():
                 lib.wf_dequant(raw.data_ptr(), raw.numel(), qt, 0, 1, w.data_ptr(), N * K, st)
                 torch.matmul(x, w.t(), out=y)
-            tf += _timed(torch, fused, 5, 1)
-            tu += _timed(torch, two_step, 5, 1)
+            tf += _timed(torch, fused, 10, 2)
+            tu += _timed(torch, two_step, 10, 2)
             flops += 2 * M * N * K
             wbytes += raw.numel()
             del raw, x, y, w

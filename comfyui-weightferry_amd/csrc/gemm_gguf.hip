@@ -36,16 +36,17 @@ template <int QT>
 struct GGUFTs { static constexpr int TS = QT == 12 ? 144 : QT == 13 ? 176 : 210; };
 
 // ------------------------------------------------------------------------- direct-to-LDS ring (K % 256 == 0)
-// 256 x 256 tiles of 8 waves (2 x 4 waves of 4 x 2 MFMA tiles, two waves per SIMD), K in stages of 32 values through
-// a 4-stage LDS ring. The activation stage (256 rows x 64 bytes) goes global -> LDS by the load unit (buffer_load ...
-// lds), two 1 KiB instructions per wave; the weight stage is dequantised by the threads: thread t takes half
-// (16 values) of stage kt's 32-value sub-block of weight row t / 2, from raw bytes loaded one step earlier, and
-// writes 32 bytes of bf16 into the ring slot three stages ahead. Step s: barrier; issue activations of stage s + 3;
-// first MFMA half of stage s; wait until only those activation loads are in flight (so the raw bytes of stage s + 3
-// have landed -- the wait counts only the fixed number of activation loads); load the raw bytes of stage s + 4;
-// dequantise stage s + 3's into the free slot; second MFMA half, prefetching stage s + 1's first fragments. Stages at or past K
-// are still issued (reads past a row land in a slot never read, or read as zeros past the buffer), which keeps the
-// waits exact and the compiler's per-slot load tracking branch-free.
+// 256 x 256 tiles (2 x 4 waves of 4 x 2 MFMA tiles) or 256 x 320 tiles (4 x 2 waves of 2 x 5), 8 waves, two per
+// SIMD; K in stages of 32 values through a 4-stage LDS ring. The activation stage (256 rows x 64 bytes) goes
+// global -> LDS by the load unit (buffer_load ... lds), two 1 KiB instructions per wave; the weight stage is
+// dequantised by the threads: thread t takes half (16 values) of the stage's 32-value sub-block of weight row t / 2
+// (with 320 rows, threads t < 128 -- waves 0 and 1 -- also take half t & 1 of row 256 + t / 2), from raw bytes loaded
+// a step earlier, and writes 32 bytes of bf16 into the ring slot three stages ahead. Step s: barrier; issue the
+// activations of stage s + 3; both MFMA halves of stage s; wait until only those activation loads are in flight
+// (so the raw bytes of stage s + 3 have landed -- the wait counts only the fixed number of activation loads);
+// dequantise them into the free slot; load the raw bytes of stage s + 4; prefetch stage s + 1's first fragments.
+// Stages at or past K are still issued (reads past a row land in a slot never read, or read as zeros past the
+// buffer), which keeps the waits exact and the compiler's per-slot load tracking branch-free.
 template <int QT>
 struct QRaw;
 template <> struct QRaw<12> { uint4 hdr, q; };
@@ -165,14 +166,16 @@ __device__ __forceinline__ void q_dequant(const QRaw<QT>& w, int g, uint32_t (&o
     }
 }
 
-template <int QT, int MID, bool BIAS>
+template <int QT, int MID, bool BIAS, int VM, int VN, int WM, int WN>
 __global__ __launch_bounds__(512) void gemm_gguf_dl(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
                                                     const uint16_t* __restrict__ bias, uint16_t* __restrict__ Y,
                                                     int M, int N, int K) {
-    constexpr int VN = 4, WM = 4, WN = 2;
-    constexpr int BM = 256, BN = 256;
+    static_assert(VM * VN == 8, "8 waves");
+    constexpr int BM = VM * WM * 32, BN = VN * WN * 32;
     constexpr int TS = GGUFTs<QT>::TS;
     constexpr int IX = BM / 16 / 8;                    // activation DMA instructions per wave per stage
+    constexpr int T2 = 2 * BN - 512;                   // half-row tasks beyond one per thread (waves 0, 1)
+    static_assert(BM == 256 && (T2 == 0 || T2 == 128), "256 x 256 or 256 x 320 tiles");
     // separate activation and weight rings: the weight writes never alias an in-flight activation load
     __shared__ uint4 xs0[BM * 4], xs1[BM * 4], xs2[BM * 4], xs3[BM * 4];
     __shared__ uint4 ws0[BN * 4], ws1[BN * 4], ws2[BN * 4], ws3[BN * 4];
@@ -197,38 +200,42 @@ __global__ __launch_bounds__(512) void gemm_gguf_dl(const uint16_t* __restrict__
 #pragma unroll
         for (int q = 0; q < IX; q++) lds_dma16(rx, st + 64 * (wave * IX + q), xoff[q] + (uint32_t)kt * 64u);
     };
-    const int wr = tid >> 1, wh = tid & 1;
-    const uint32_t wbase = (uint32_t)wr * row_bytes;
+    // thread t dequantises half t & 1 of weight row t / 2; with 320 rows, threads t < 128 also take half t & 1 of
+    // row 256 + t / 2
+    const int wh = tid & 1;
+    const int wr = tid >> 1, wr2 = 256 + ((tid >> 1) & 63);
+    const uint32_t wbase = (uint32_t)wr * row_bytes, wbase2 = (uint32_t)wr2 * row_bytes;
     auto wload = [&](QRaw<QT>& raw, int kt) { q_load<QT>(rw, wbase + (uint32_t)(kt >> 3) * TS, kt & 7, wh, raw); };
-    int wslot[2];
+    auto wload2 = [&](QRaw<QT>& raw, int kt) { q_load<QT>(rw, wbase2 + (uint32_t)(kt >> 3) * TS, kt & 7, wh, raw); };
+    int wslot[2], wslot2[2];
 #pragma unroll
-    for (int c = 0; c < 2; c++) wslot[c] = wr * 4 + swz4(wr, 2 * wh + c);
-    auto wstore = [&](uint4* st, const QRaw<QT>& raw, int kt) {
+    for (int c = 0; c < 2; c++) {
+        wslot[c] = wr * 4 + swz4(wr, 2 * wh + c);
+        wslot2[c] = wr2 * 4 + swz4(wr2, 2 * wh + c);
+    }
+    auto wstore_at = [&](uint4* st, const int (&slot)[2], const QRaw<QT>& raw, int kt) {
         uint32_t o[8];
         q_dequant<QT, MID>(raw, kt & 7, o);
-        lds_write16(st + wslot[0], make_uint4(o[0], o[1], o[2], o[3]));
-        lds_write16(st + wslot[1], make_uint4(o[4], o[5], o[6], o[7]));
+        lds_write16(st + slot[0], make_uint4(o[0], o[1], o[2], o[3]));
+        lds_write16(st + slot[1], make_uint4(o[4], o[5], o[6], o[7]));
     };
+    const bool two = T2 > 0 && wave < 2;               // wave-uniform
     const int lr = lane & 31, lk = lane >> 5;
-    int aslot[WM][2], bslot[WN][2];
+    // fragment slots: MFMA tile i's rows are 32 i past tile 0's, where the swizzle term (row >> 2) & 3 is the same,
+    // so one base per K half serves every tile (the 512-byte multiples fold into the LDS read offsets)
+    int abase[2], bbase[2];
 #pragma unroll
-    for (int i = 0; i < WM; i++) {
-        const int row = wm * WM * 32 + i * 32 + lr;
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) aslot[i][ks] = row * 4 + swz4(row, 2 * ks + lk);
-    }
-#pragma unroll
-    for (int j = 0; j < WN; j++) {
-        const int row = wn * WN * 32 + j * 32 + lr;
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) bslot[j][ks] = row * 4 + swz4(row, 2 * ks + lk);
+    for (int ks = 0; ks < 2; ks++) {
+        const int ra = wm * WM * 32 + lr, rb = wn * WN * 32 + lr;
+        abase[ks] = ra * 4 + swz4(ra, 2 * ks + lk);
+        bbase[ks] = rb * 4 + swz4(rb, 2 * ks + lk);
     }
     bf16x8 fa[2][WM], fb[2][WN];
     auto fread = [&](const uint4* xst, const uint4* wst, int ks, int set) {
 #pragma unroll
-        for (int i = 0; i < WM; i++) fa[set][i] = __builtin_bit_cast(bf16x8, xst[aslot[i][ks]]);
+        for (int i = 0; i < WM; i++) fa[set][i] = __builtin_bit_cast(bf16x8, xst[abase[ks] + 128 * i]);
 #pragma unroll
-        for (int j = 0; j < WN; j++) fb[set][j] = __builtin_bit_cast(bf16x8, wst[bslot[j][ks]]);
+        for (int j = 0; j < WN; j++) fb[set][j] = __builtin_bit_cast(bf16x8, wst[bbase[ks] + 128 * j]);
     };
     f32x16 acc[WM][WN];
 #pragma unroll
@@ -245,102 +252,133 @@ __global__ __launch_bounds__(512) void gemm_gguf_dl(const uint16_t* __restrict__
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
     };
 
-    QRaw<QT> wa, wb;                                   // raw bytes of even / odd stages
+    QRaw<QT> w1, w2;                                   // raw bytes of the next stage to dequantise (both tasks)
     issue_x(xs0, 0);
     issue_x(xs1, 1);
     issue_x(xs2, 2);
-    wload(wa, 0);
-    wait_vm<0>();
-    wstore(ws0, wa, 0);
-    wload(wa, 1);
-    wait_vm<0>();
-    wstore(ws1, wa, 1);
-    wload(wa, 2);
-    wait_vm<0>();
-    wstore(ws2, wa, 2);
-    wload(wb, 3);
+    uint4* const wring[3] = {ws0, ws1, ws2};
+#pragma unroll
+    for (int s0 = 0; s0 < 3; s0++) {
+        wload(w1, s0);
+        if (two) wload2(w2, s0);
+        wait_vm<0>();
+        wstore_at(wring[s0], wslot, w1, s0);
+        if (two) wstore_at(wring[s0], wslot2, w2, s0);
+    }
+    wload(w1, 3);
+    if (two) wload2(w2, 3);
     __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));   // lgkmcnt(0): this thread's LDS writes are done
     wave_barrier_sync();
     fread(xs0, ws0, 0, 0);
-    // ring step: stage s in slot C, s + 1 in slot NX, and slot F (stage s - 1's) receives stage s + 3; RC holds the
-    // raw bytes of stage s + 3, RN receives those of stage s + 4
-    auto step = [&](int s, uint4* xc, uint4* wc, uint4* xn, uint4* wn_, uint4* xf, uint4* wf, QRaw<QT>& rc,
-                    QRaw<QT>& rn) {
+    // ring step: stage s in slot C, s + 1 in slot NX, and slot F (stage s - 1's) receives stage s + 3. The raw
+    // weight bytes of stage s + 3 were loaded at the end of the previous step, before this step's activation loads,
+    // so waiting for all but those activation loads lands them; once dequantised, the registers take the raw bytes
+    // of stage s + 4 (one set of raw registers, each load a whole step ahead of its use).
+    auto step = [&](int s, uint4* xc, uint4* wc, uint4* xn, uint4* wn_, uint4* xf, uint4* wf) {
         wave_barrier_sync();
         issue_x(xf, s + 3);
         fread(xc, wc, 1, 1);
         mfmas(0);
+        mfmas(1);
+        __builtin_amdgcn_sched_barrier(0);
         wait_vm<IX>();                                 // all but this step's activation loads have landed
         __builtin_amdgcn_sched_barrier(0);             // nothing that reads the raw bytes moves above the wait
-        wload(rn, s + 4);                              // a whole step ahead of its use
-        __builtin_amdgcn_sched_barrier(0);
-        mfmas(1);                                      // independent of the dequantisation: they overlap
-        wstore(wf, rc, s + 3);
+        wstore_at(wf, wslot, w1, s + 3);
+        if (two) wstore_at(wf, wslot2, w2, s + 3);
+        __builtin_amdgcn_sched_barrier(0);             // the next loads reuse the raw registers
+        wload(w1, s + 4);
+        if (two) wload2(w2, s + 4);
         fread(xn, wn_, 0, 0);                          // stage s + 1's first fragments for the next step
     };
     int kt = 0;
     for (; kt + 4 <= nk; kt += 4) {
-        step(kt, xs0, ws0, xs1, ws1, xs3, ws3, wb, wa);
-        step(kt + 1, xs1, ws1, xs2, ws2, xs0, ws0, wa, wb);
-        step(kt + 2, xs2, ws2, xs3, ws3, xs1, ws1, wb, wa);
-        step(kt + 3, xs3, ws3, xs0, ws0, xs2, ws2, wa, wb);
+        step(kt, xs0, ws0, xs1, ws1, xs3, ws3);
+        step(kt + 1, xs1, ws1, xs2, ws2, xs0, ws0);
+        step(kt + 2, xs2, ws2, xs3, ws3, xs1, ws1);
+        step(kt + 3, xs3, ws3, xs0, ws0, xs2, ws2);
     }
-    if (kt < nk) step(kt, xs0, ws0, xs1, ws1, xs3, ws3, wb, wa);
-    if (kt + 1 < nk) step(kt + 1, xs1, ws1, xs2, ws2, xs0, ws0, wa, wb);
-    if (kt + 2 < nk) step(kt + 2, xs2, ws2, xs3, ws3, xs1, ws1, wb, wa);
+    if (kt < nk) step(kt, xs0, ws0, xs1, ws1, xs3, ws3);
+    if (kt + 1 < nk) step(kt + 1, xs1, ws1, xs2, ws2, xs0, ws0);
+    if (kt + 2 < nk) step(kt + 2, xs2, ws2, xs3, ws3, xs1, ws1);
 
     // epilogue through LDS (the ring is idle once every load has landed and every wave is past its reads): each
-    // wave rounds its 128 x 64 tile to bf16 into its own 16 KiB ring slot, then stores whole 16-byte runs of rows
+    // wave rounds its tile to bf16 into its own ring slot (waves 0-3 the activation slots, 4-7 the weight slots),
+    // IP MFMA rows (32 rows each) at a time, and stores whole 16-byte runs of rows
     constexpr int TR = WM * 32, TC = WN * 32;
+    constexpr int IP = (BM * 4 * 16) / (32 * TC * 2) < WM ? (BM * 4 * 16) / (32 * TC * 2) : WM;
+    static_assert(IP >= 1 && WM % IP == 0, "whole MFMA rows per pass");
     wait_vm<0>();
     wave_barrier_sync();
-    static_assert(TR * TC * 2 == BM * 4 * 16, "one ring slot per wave");
     uint4* buf = wave == 0 ? xs0 : wave == 1 ? xs1 : wave == 2 ? xs2 : wave == 3 ? xs3
                : wave == 4 ? ws0 : wave == 5 ? ws1 : wave == 6 ? ws2 : ws3;
     uint16_t* ot = reinterpret_cast<uint16_t*>(buf);
+    const uint4* ov = reinterpret_cast<const uint4*>(ot);   // the wave's own region: in-order LDS writes and reads
     const int mw = m0 + wm * TR, nw = n0 + wn * TC;
+    float bn[WN];
 #pragma unroll
     for (int j = 0; j < WN; j++) {
         const int n = nw + j * 32 + lr;
-        const float bn = BIAS && n < N ? __uint_as_float((uint32_t)bias[n] << 16) : 0.0f;
-#pragma unroll
-        for (int i = 0; i < WM; i++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                float t = acc[i][j][e];
-                if (BIAS) t = t + bn;
-                ot[(i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3)) * TC + j * 32 + lr] = __builtin_bit_cast(uint16_t, (__bf16)t);
-            }
+        bn[j] = BIAS && n < N ? __uint_as_float((uint32_t)bias[n] << 16) : 0.0f;
     }
-    const uint4* ov = reinterpret_cast<const uint4*>(ot);   // the wave's own region: in-order LDS writes and reads
-    constexpr int RUNS = TC / 8;
-    if ((N & 7) == 0) {
+    constexpr int PR = IP * 32, RUNS = TC / 8;        // rows per pass, 16-byte runs per row
 #pragma unroll
-        for (int it = 0; it < TR * RUNS / 64; it++) {
-            const int q = it * 64 + lane, r = q / RUNS, c = q % RUNS;
-            const int m = mw + r, n = nw + 8 * c;
-            const uint4 v = ov[q];
-            if (m < M && n < N) *reinterpret_cast<uint4*>(Y + (int64_t)m * N + n) = v;
+    for (int p = 0; p < WM / IP; p++) {
+#pragma unroll
+        for (int ii = 0; ii < IP; ii++) {
+            const int i = p * IP + ii;
+#pragma unroll
+            for (int j = 0; j < WN; j++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    float t = acc[i][j][e];
+                    if (BIAS) t = t + bn[j];
+                    ot[(ii * 32 + 8 * (e >> 2) + 4 * lk + (e & 3)) * TC + j * 32 + lr] =
+                        __builtin_bit_cast(uint16_t, (__bf16)t);
+                }
         }
-    } else {
-        for (int it = 0; it < TR * RUNS / 64; it++) {
-            const int q = it * 64 + lane, r = q / RUNS, c = q % RUNS;
-            const int m = mw + r;
-            if (m >= M) continue;
-            for (int e = 0; e < 8; e++) {
-                const int n = nw + 8 * c + e;
-                if (n < N) Y[(int64_t)m * N + n] = ot[r * TC + 8 * c + e];
+        const int mp = mw + p * PR;
+        if ((N & 7) == 0) {
+#pragma unroll
+            for (int it = 0; it < PR * RUNS / 64; it++) {
+                const int q = it * 64 + lane, r = q / RUNS, c = q % RUNS;
+                const int m = mp + r, n = nw + 8 * c;
+                const uint4 v = ov[q];
+                if (m < M && n < N) *reinterpret_cast<uint4*>(Y + (int64_t)m * N + n) = v;
+            }
+        } else {
+            for (int it = 0; it < PR * RUNS / 64; it++) {
+                const int q = it * 64 + lane, r = q / RUNS, c = q % RUNS;
+                const int m = mp + r;
+                if (m >= M) continue;
+                for (int e = 0; e < 8; e++) {
+                    const int n = nw + 8 * c + e;
+                    if (n < N) Y[(int64_t)m * N + n] = ot[r * TC + 8 * c + e];
+                }
             }
         }
     }
 }
 
+template <int QT, int MID, int VM, int VN, int WM, int WN>
+static void launch_shape(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
+                         hipStream_t s) {
+    constexpr int BM = VM * WM * 32, BN = VN * WN * 32;
+    const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    if (bias) gemm_gguf_dl<QT, MID, true, VM, VN, WM, WN><<<dim3(tiles), 512, 0, s>>>(X, W, bias, Y, M, N, K);
+    else gemm_gguf_dl<QT, MID, false, VM, VN, WM, WN><<<dim3(tiles), 512, 0, s>>>(X, W, bias, Y, M, N, K);
+}
+
+// 256 x 320 tiles (8 waves of 2 x 5 MFMA tiles; 4096 x 5120 outputs make exactly 256 tiles) or 256 x 256 (8 waves of
+// 4 x 2), whichever takes fewer modelled cycles: whole rounds of 256 workgroups (one per CU) x tile area
 template <int QT, int MID>
 static void launch(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
                    hipStream_t s) {
-    const int tiles = ((M + 255) / 256) * ((N + 255) / 256);
-    if (bias) gemm_gguf_dl<QT, MID, true><<<dim3(tiles), 512, 0, s>>>(X, W, bias, Y, M, N, K);
-    else gemm_gguf_dl<QT, MID, false><<<dim3(tiles), 512, 0, s>>>(X, W, bias, Y, M, N, K);
+    auto cost = [&](int bn) {
+        const int64_t tiles = (int64_t)((M + 255) / 256) * ((N + bn - 1) / bn);
+        return (tiles + 255) / 256 * bn;
+    };
+    if (cost(320) < cost(256)) launch_shape<QT, MID, 4, 2, 2, 5>(X, W, bias, Y, M, N, K, s);
+    else launch_shape<QT, MID, 2, 4, 4, 2>(X, W, bias, Y, M, N, K, s);
 }
 
 template <int QT>

@@ -68,6 +68,21 @@ def test_fused_bias_and_encoded_weights(native):
     check(y, x, weight_bf16(raw, 13, 0, N, K), bias=bias)
 
 
+@pytest.mark.parametrize("qtype", [12, 13, 14])
+@pytest.mark.parametrize("M,N,K,with_bias", [(4096, 4500, 256, False), (4000, 4480, 512, True)])
+def test_wide_tiles_whole_output(native, qtype, M, N, K, with_bias):
+    # outputs of more than one round of 256 x 256 tiles but one round of 256 x 320 tiles take the 320-row weight
+    # tiles (two dequantisation tasks for the first two waves); N = 4500 leaves a partial last tile and an odd row
+    # length (element stores), N = 4480 whole 16-byte runs; every output element is checked
+    raw = encode.random_blocks(qtype, N * K // 256, seed=qtype + N, family="normal")
+    g = torch.Generator().manual_seed(M + K)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16) if with_bias else None
+    y = fused(native, x.cuda(), torch.from_numpy(raw).cuda(), qtype, N,
+              bias=bias.cuda() if with_bias else None)
+    check(y, x, weight_bf16(raw, qtype, 0, N, K), bias=bias)
+
+
 @pytest.mark.parametrize("qtype", [13, 14])
 @pytest.mark.parametrize("N,K", [(5120, 5120), (13824, 5120), (5120, 13824)])
 def test_wan_block_shapes_sampled_rows(native, qtype, N, K):
