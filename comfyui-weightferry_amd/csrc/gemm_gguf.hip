@@ -8,6 +8,8 @@
 // 16-wide step; result layout: lane l, register i -> row 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32. The tiling
 // and the pipeline are described at gemm_gguf_dl below.
 
+#include <type_traits>
+
 #include "kquant.h"
 #include "lds_ring.h"
 
@@ -40,18 +42,27 @@ struct GGUFTs { static constexpr int TS = QT == 12 ? 144 : QT == 13 ? 176 : 210;
 // SIMD; K in stages of 32 values through a 4-stage LDS ring. The activation stage (256 rows x 64 bytes) goes
 // global -> LDS by the load unit (buffer_load ... lds), two 1 KiB instructions per wave; the weight stage is
 // dequantised by the threads: thread t takes half (16 values) of the stage's 32-value sub-block of weight row t / 2
-// (with 320 rows, threads t < 128 -- waves 0 and 1 -- also take half t & 1 of row 256 + t / 2), from raw bytes loaded
-// a step earlier, and writes 32 bytes of bf16 into the ring slot three stages ahead. Step s: barrier; issue the
-// activations of stage s + 3; both MFMA halves of stage s; wait until only those activation loads are in flight
-// (so the raw bytes of stage s + 3 have landed -- the wait counts only the fixed number of activation loads);
-// dequantise them into the free slot; load the raw bytes of stage s + 4; prefetch stage s + 1's first fragments.
-// Stages at or past K are still issued (reads past a row land in a slot never read, or read as zeros past the
-// buffer), which keeps the waits exact and the compiler's per-slot load tracking branch-free.
+// (with 320 rows, also the quarter task t % 8 -- 4 values -- of row 256 + t / 8), from raw bytes loaded a step
+// earlier, and writes its bf16 into the ring slot three stages ahead. The loop runs whole super-blocks (8 stages),
+// so each stage's sub-block index within its super-block is a compile-time constant: raw bytes shared by several
+// stages (headers, Q5_K high bits, the nibble bytes of a sub-block pair, Q6_K high bits) are loaded once and kept.
+// Step s: barrier; issue the activations of stage s + 3; both MFMA halves of stage s; wait until only those
+// activation loads are in flight (so the raw bytes of stage s + 3 have landed -- the wait counts only the fixed
+// number of activation loads); dequantise them into the free slot; load the raw bytes of stage s + 4; prefetch
+// stage s + 1's first fragments. Stages at or past K are still issued (reads past a row land in a slot never read,
+// or read as zeros past the buffer), which keeps the waits exact and the compiler's per-slot load tracking
+// branch-free.
 template <int QT>
 struct QRaw;
 template <> struct QRaw<12> { uint4 hdr, q; };
 template <> struct QRaw<13> { uint4 hdr, q, qh; };
-template <> struct QRaw<14> { uint4 ql; uint32_t ql4; uint4 qh; uint32_t qh4; uint32_t sc, d, sh; };
+template <> struct QRaw<14> { uint4 ql; uint32_t ql4; uint4 qh; uint32_t qh4; uint32_t sc, d; };
+// raw bytes of a quarter task (4 values)
+template <int QT>
+struct QRawQ;
+template <> struct QRawQ<12> { uint4 hdr; uint32_t q; };
+template <> struct QRawQ<13> { uint4 hdr; uint32_t q, qh; };
+template <> struct QRawQ<14> { uint32_t ql0, ql1, qh0, qh1, sc, d; };
 
 __device__ __forceinline__ uint4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t o) {
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0));
@@ -60,36 +71,67 @@ __device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t o) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0);
 }
 
-// raw bytes of values [16 h, 16 h + 16) of sub-block g (32 values) of the super-block at byte offset b
-template <int QT>
-__device__ __forceinline__ void q_load(__amdgpu_buffer_rsrc_t r, uint32_t b, int g, int h, QRaw<QT>& w) {
+// Raw bytes of values [16 h, 16 h + 16) of sub-block G (32 values) of the super-block at byte offset b, for stage
+// phase G (the stage's sub-block within its super-block, known at compile time). Only what changes at phase G is
+// loaded; the rest stays in the registers from an earlier phase of the same super-block (the caller loads the phases
+// of a super-block in order into the same QRaw).
+template <int QT, int G>
+__device__ __forceinline__ void q_load(__amdgpu_buffer_rsrc_t r, uint32_t b, int h, QRaw<QT>& w) {
     if constexpr (QT == 12 || QT == 13) {
-        // Q4_K / Q5_K: qs[32 (g / 2) + 16 h ..] nibble g % 2; Q5_K qh[16 h ..] bit g (16-byte aligned blocks)
+        // Q4_K / Q5_K: header (d, dmin, scales) at 0 once per super-block; qs[32 (G / 2) + 16 h ..] (nibble G % 2)
+        // once per two phases; Q5_K qh[16 h ..] (bit G) once per super-block (16-byte aligned blocks)
         constexpr uint32_t QS = QT == 12 ? 16 : 48;
-        w.hdr = ld128(r, b);
-        w.q = ld128(r, b + QS + 32 * (g >> 1) + 16 * h);
-        if constexpr (QT == 13) w.qh = ld128(r, b + 16 + 16 * h);
+        if constexpr (G == 0) w.hdr = ld128(r, b);
+        if constexpr (QT == 13 && G == 0) w.qh = ld128(r, b + 16 + 16 * h);
+        if constexpr (G % 2 == 0) w.q = ld128(r, b + QS + 32 * (G >> 1) + 16 * h);
     } else {
-        // Q6_K (210-byte blocks, 2-byte aligned): ql[64 hh + rr % 64 ..] nibble rr / 64, qh[128 + 32 hh + rr % 32 ..]
-        // at shift 2 (rr / 32), scale byte 192 + v0 / 16, d at 208; v0 = 32 g + 16 h, hh = v0 / 128, rr = v0 % 128.
-        // ql and qh are read as 20 bytes from their aligned-down dword (the shifts kept in sh; the window stays
-        // inside the block), the scale and d at their exact widths.
-        const int v0 = 32 * g + 16 * h, hh = v0 >> 7, rr = v0 & 127;
-        const uint32_t oql = b + 64 * hh + (rr & 63), oqh = b + 128 + 32 * hh + (rr & 31);
-        const uint32_t osc = b + 192 + (v0 >> 4), od = b + 208;
+        // Q6_K (210-byte blocks, 2-byte aligned). Values v0 = 32 G + 16 h ..: hh = v0 / 128 = G / 4, rr = v0 % 128 =
+        // 32 (G % 4) + 16 h; ql[64 hh + rr % 64 ..] (nibble rr / 64) every phase, qh[128 + 32 hh + rr % 32 ..] (shift
+        // 2 (rr / 32)) once per four phases, both read as 20 bytes from their aligned-down dword (the window stays
+        // inside the block; the offsets within the block are multiples of 16, so the shift is b % 4 for both); the
+        // scale byte 192 + v0 / 16 every phase, d at 208 once per super-block -- at their exact widths, as the
+        // block's last bytes must not be read past its end.
+        constexpr uint32_t hh = G >> 2;
+        const uint32_t oql = b + 64 * hh + 32 * (G & 1) + 16 * h;
         w.ql = ld128(r, oql & ~3u);
         w.ql4 = ld32(r, (oql & ~3u) + 16);
-        w.qh = ld128(r, oqh & ~3u);
-        w.qh4 = ld32(r, (oqh & ~3u) + 16);
-        w.sc = __builtin_amdgcn_raw_buffer_load_b8(r, osc, 0, 0);     // exact widths: the block's last bytes
-        w.d = __builtin_amdgcn_raw_buffer_load_b16(r, od, 0, 0);      // never read past its end
-        w.sh = (oql & 3) | ((oqh & 3) << 8);
+        if constexpr ((G & 3) == 0) {
+            const uint32_t oqh = b + 128 + 32 * hh + 16 * h;
+            w.qh = ld128(r, oqh & ~3u);
+            w.qh4 = ld32(r, (oqh & ~3u) + 16);
+        }
+        w.sc = __builtin_amdgcn_raw_buffer_load_b8(r, b + 192 + 2 * G + h, 0, 0);
+        if constexpr (G == 0) w.d = __builtin_amdgcn_raw_buffer_load_b16(r, b + 208, 0, 0);
+    }
+}
+
+// Raw bytes of the quarter task: values [4 qq, 4 qq + 4) of sub-block G of the super-block at byte offset b, by the
+// same rules as q_load (one dword of nibbles / high bits; Q6_K's ql and qh as 8 bytes from their aligned-down dword).
+template <int QT, int G>
+__device__ __forceinline__ void q_load_q(__amdgpu_buffer_rsrc_t r, uint32_t b, int qq, QRawQ<QT>& w) {
+    if constexpr (QT == 12 || QT == 13) {
+        constexpr uint32_t QS = QT == 12 ? 16 : 48;
+        if constexpr (G == 0) w.hdr = ld128(r, b);
+        if constexpr (QT == 13 && G == 0) w.qh = ld32(r, b + 16 + 4 * qq);
+        if constexpr (G % 2 == 0) w.q = ld32(r, b + QS + 32 * (G >> 1) + 4 * qq);
+    } else {
+        constexpr uint32_t hh = G >> 2;
+        const uint32_t oql = (b + 64 * hh + 32 * (G & 1) + 4 * qq) & ~3u;
+        w.ql0 = ld32(r, oql);
+        w.ql1 = ld32(r, oql + 4);
+        if constexpr ((G & 3) == 0) {
+            const uint32_t oqh = (b + 128 + 32 * hh + 4 * qq) & ~3u;
+            w.qh0 = ld32(r, oqh);
+            w.qh1 = ld32(r, oqh + 4);
+        }
+        w.sc = __builtin_amdgcn_raw_buffer_load_b8(r, b + 192 + 2 * G + (qq >> 2), 0, 0);
+        if constexpr (G == 0) w.d = __builtin_amdgcn_raw_buffer_load_b16(r, b + 208, 0, 0);
     }
 }
 
 // the 16 values as 8 packed bf16 pairs (values 2i, 2i + 1 in o[i]), the reference's rounding chain in MID
-template <int QT, int MID>
-__device__ __forceinline__ void q_dequant(const QRaw<QT>& w, int g, uint32_t (&o)[8]) {
+template <int QT, int MID, int g>
+__device__ __forceinline__ void q_dequant(const QRaw<QT>& w, uint32_t sh, uint32_t (&o)[8]) {
     if constexpr (QT == 12 || QT == 13) {
         const uint32_t ns = 4u * (uint32_t)(g & 1);
         const uint32_t qa[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
@@ -128,7 +170,7 @@ __device__ __forceinline__ void q_dequant(const QRaw<QT>& w, int g, uint32_t (&o
             }
         }
     } else {
-        const uint32_t shl = 8u * (w.sh & 3u), shh = 8u * ((w.sh >> 8) & 3u);
+        const uint32_t shl = 8u * sh, shh = shl;         // Q6_K: sh = block offset % 4 (0 or 2)
         const uint32_t la[5] = {w.ql.x, w.ql.y, w.ql.z, w.ql.w, w.ql4};
         const uint32_t ha[5] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w, w.qh4};
         const uint32_t ns = 4u * (uint32_t)((g & 3) >> 1), hs = 2u * (uint32_t)(g & 3);
@@ -162,6 +204,57 @@ __device__ __forceinline__ void q_dequant(const QRaw<QT>& w, int g, uint32_t (&o
                 o[2 * i] = pack_bf16(v[0], v[1]);
                 o[2 * i + 1] = pack_bf16(v[2], v[3]);
             }
+        }
+    }
+}
+
+// the quarter task's 4 values as 2 packed bf16 pairs (values 0, 1 in o0; 2, 3 in o1), as q_dequant
+template <int QT, int MID, int g>
+__device__ __forceinline__ void q_dequant_q(const QRawQ<QT>& w, uint32_t sh, uint32_t& o0, uint32_t& o1) {
+    if constexpr (QT == 12 || QT == 13) {
+        uint32_t q = (w.q >> (4 * (g & 1))) & 0x0f0f0f0fu;
+        if constexpr (QT == 13) q |= ((w.qh >> g) & 0x01010101u) << 4;
+        uint32_t sc, m;
+        scale_min_nb(w.hdr.y, w.hdr.z, w.hdr.w, g, sc, m);
+        if constexpr (MID == WF_F16) {
+            const h2 off = h2s(-1024.0f);
+            const h2 pr = as_h2(w.hdr.x) * (as_h2(sc | (m << 16) | 0x64006400u) + off);   // (d * sc, dmin * m)
+            const h2 ds = lo2(pr), dm = hi2(pr);
+            const h2 v0 = ds * (biased_lo(q) + off) - dm, v1 = ds * (biased_hi(q) + off) - dm;
+            o0 = pack_bf16((float)v0[0], (float)v0[1]);
+            o1 = pack_bf16((float)v1[0], (float)v1[1]);
+        } else {
+            const float d = round_to<MID>(f16_bits_to_f32(w.hdr.x & 0xffffu));
+            const float dmin = round_to<MID>(f16_bits_to_f32(w.hdr.x >> 16));
+            const float ds = round_to<MID>(d * (float)sc), dm = round_to<MID>(dmin * (float)m);
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[e] = round_to<MID>(round_to<MID>(ds * (float)byte_of(q, e)) - dm);
+            o0 = pack_bf16(v[0], v[1]);
+            o1 = pack_bf16(v[2], v[3]);
+        }
+    } else {
+        const uint32_t shb = 8u * sh;
+        const uint32_t ql = __builtin_amdgcn_alignbit(w.ql1, w.ql0, shb);
+        const uint32_t qh = __builtin_amdgcn_alignbit(w.qh1, w.qh0, shb);
+        const uint32_t code = ((ql >> (4 * ((g & 3) >> 1))) & 0x0f0f0f0fu) | (((qh >> (2 * (g & 3))) & 0x03030303u) << 4);
+        const int sc = (int8_t)(w.sc & 0xffu);
+        const uint32_t dbits = w.d & 0xffffu;
+        if constexpr (MID == WF_F16) {
+            const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)dbits);
+            const _Float16 ds1 = d * (_Float16)(float)sc;
+            h2 ds; ds[0] = ds1; ds[1] = ds1;
+            const h2 off = h2s(-1056.0f);
+            const h2 v0 = ds * (biased_lo(code) + off), v1 = ds * (biased_hi(code) + off);
+            o0 = pack_bf16((float)v0[0], (float)v0[1]);
+            o1 = pack_bf16((float)v1[0], (float)v1[1]);
+        } else {
+            const float ds = round_to<MID>(round_to<MID>(f16_bits_to_f32(dbits)) * (float)sc);
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[e] = round_to<MID>(ds * (float)((int)byte_of(code, e) - 32));
+            o0 = pack_bf16(v[0], v[1]);
+            o1 = pack_bf16(v[2], v[3]);
         }
     }
 }
@@ -200,26 +293,33 @@ __global__ __launch_bounds__(512) void gemm_gguf_dl(const uint16_t* __restrict__
 #pragma unroll
         for (int q = 0; q < IX; q++) lds_dma16(rx, st + 64 * (wave * IX + q), xoff[q] + (uint32_t)kt * 64u);
     };
-    // thread t dequantises half t & 1 of weight row t / 2; with 320 rows, threads t < 128 also take half t & 1 of
-    // row 256 + t / 2
-    const int wh = tid & 1;
-    const int wr = tid >> 1, wr2 = 256 + ((tid >> 1) & 63);
+    // thread t dequantises half t & 1 of weight row t / 2; with 320 rows, it also takes the quarter task t % 8
+    // (values 4 (t % 8) ..) of row 256 + t / 8
+    const int wh = tid & 1, wr = tid >> 1;
+    const int qq = tid & 7, wr2 = 256 + ((tid >> 3) & 63);
     const uint32_t wbase = (uint32_t)wr * row_bytes, wbase2 = (uint32_t)wr2 * row_bytes;
-    auto wload = [&](QRaw<QT>& raw, int kt) { q_load<QT>(rw, wbase + (uint32_t)(kt >> 3) * TS, kt & 7, wh, raw); };
-    auto wload2 = [&](QRaw<QT>& raw, int kt) { q_load<QT>(rw, wbase2 + (uint32_t)(kt >> 3) * TS, kt & 7, wh, raw); };
-    int wslot[2], wslot2[2];
-#pragma unroll
-    for (int c = 0; c < 2; c++) {
-        wslot[c] = wr * 4 + swz4(wr, 2 * wh + c);
-        wslot2[c] = wr2 * 4 + swz4(wr2, 2 * wh + c);
-    }
-    auto wstore_at = [&](uint4* st, const int (&slot)[2], const QRaw<QT>& raw, int kt) {
-        uint32_t o[8];
-        q_dequant<QT, MID>(raw, kt & 7, o);
-        lds_write16(st + slot[0], make_uint4(o[0], o[1], o[2], o[3]));
-        lds_write16(st + slot[1], make_uint4(o[4], o[5], o[6], o[7]));
+    auto blk = [&](uint32_t base, int kt) { return base + (uint32_t)(kt >> 3) * TS; };
+    // raw loads and dequantisation of stage kt, whose phase (kt % 8) the caller passes as a compile-time constant
+    auto wload = [&](auto G, QRaw<QT>& raw, int kt) { q_load<QT, decltype(G)::value>(rw, blk(wbase, kt), wh, raw); };
+    auto wload2 = [&](auto G, QRawQ<QT>& raw, int kt) {
+        q_load_q<QT, decltype(G)::value>(rw, blk(wbase2, kt), qq, raw);
     };
-    const bool two = T2 > 0 && wave < 2;               // wave-uniform
+    int wslot[2];
+#pragma unroll
+    for (int c = 0; c < 2; c++) wslot[c] = wr * 4 + swz4(wr, 2 * wh + c);
+    const int wslot2 = (wr2 * 4 + swz4(wr2, qq >> 1)) * 2 + (qq & 1);     // in 8-byte units
+    auto wstore = [&](auto G, uint4* st, const QRaw<QT>& raw, int kt) {
+        uint32_t o[8];
+        q_dequant<QT, MID, decltype(G)::value>(raw, blk(wbase, kt) & 3u, o);
+        lds_write16(st + wslot[0], make_uint4(o[0], o[1], o[2], o[3]));
+        lds_write16(st + wslot[1], make_uint4(o[4], o[5], o[6], o[7]));
+    };
+    auto wstore2 = [&](auto G, uint4* st, const QRawQ<QT>& raw, int kt) {
+        uint32_t o0, o1;
+        q_dequant_q<QT, MID, decltype(G)::value>(raw, blk(wbase2, kt) & 3u, o0, o1);
+        lds_write8(reinterpret_cast<uint2*>(st) + wslot2, o0, o1);
+    };
+    constexpr bool two = T2 > 0;
     const int lr = lane & 31, lk = lane >> 5;
     // fragment slots: MFMA tile i's rows are 32 i past tile 0's, where the swizzle term (row >> 2) & 3 is the same,
     // so one base per K half serves every tile (the 512-byte multiples fold into the LDS read offsets)
@@ -252,29 +352,41 @@ __global__ __launch_bounds__(512) void gemm_gguf_dl(const uint16_t* __restrict__
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
     };
 
-    QRaw<QT> w1, w2;                                   // raw bytes of the next stage to dequantise (both tasks)
+    QRaw<QT> w1;                                       // raw bytes of the next stage to dequantise
+    QRawQ<QT> w2;                                      // the same for the quarter task (320-row tiles)
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    using P2 = std::integral_constant<int, 2>;
+    using P3 = std::integral_constant<int, 3>;
     issue_x(xs0, 0);
     issue_x(xs1, 1);
     issue_x(xs2, 2);
-    uint4* const wring[3] = {ws0, ws1, ws2};
-#pragma unroll
-    for (int s0 = 0; s0 < 3; s0++) {
-        wload(w1, s0);
-        if (two) wload2(w2, s0);
+    auto pro = [&](auto G, uint4* st) {
+        constexpr int g = decltype(G)::value;
+        wload(G, w1, g);
+        if constexpr (two) wload2(G, w2, g);
         wait_vm<0>();
-        wstore_at(wring[s0], wslot, w1, s0);
-        if (two) wstore_at(wring[s0], wslot2, w2, s0);
-    }
-    wload(w1, 3);
-    if (two) wload2(w2, 3);
+        wstore(G, st, w1, g);
+        if constexpr (two) wstore2(G, st, w2, g);
+    };
+    pro(P0{}, ws0);
+    pro(P1{}, ws1);
+    pro(P2{}, ws2);
+    wload(P3{}, w1, 3);
+    if constexpr (two) wload2(P3{}, w2, 3);
     __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));   // lgkmcnt(0): this thread's LDS writes are done
     wave_barrier_sync();
     fread(xs0, ws0, 0, 0);
-    // ring step: stage s in slot C, s + 1 in slot NX, and slot F (stage s - 1's) receives stage s + 3. The raw
-    // weight bytes of stage s + 3 were loaded at the end of the previous step, before this step's activation loads,
-    // so waiting for all but those activation loads lands them; once dequantised, the registers take the raw bytes
-    // of stage s + 4 (one set of raw registers, each load a whole step ahead of its use).
-    auto step = [&](int s, uint4* xc, uint4* wc, uint4* xn, uint4* wn_, uint4* xf, uint4* wf) {
+    // ring step J of the 8 in a super-block (stage s = kt + J): stage s in slot C, s + 1 in slot NX, and slot F
+    // (stage s - 1's) receives stage s + 3. The raw weight bytes of stage s + 3 were loaded at the end of the previous
+    // step, before this step's activation loads, so waiting for all but those activation loads lands them; once
+    // dequantised, the registers take what changes for stage s + 4 (one set of raw registers, each load a whole
+    // step ahead of its use).
+    auto step = [&](int kt, auto J, uint4* xc, uint4* wc, uint4* xn, uint4* wn_, uint4* xf, uint4* wf) {
+        constexpr int j = decltype(J)::value;
+        const int s = kt + j;
+        using G3 = std::integral_constant<int, (j + 3) & 7>;
+        using G4 = std::integral_constant<int, (j + 4) & 7>;
         wave_barrier_sync();
         issue_x(xf, s + 3);
         fread(xc, wc, 1, 1);
@@ -283,23 +395,24 @@ __global__ __launch_bounds__(512) void gemm_gguf_dl(const uint16_t* __restrict__
         __builtin_amdgcn_sched_barrier(0);
         wait_vm<IX>();                                 // all but this step's activation loads have landed
         __builtin_amdgcn_sched_barrier(0);             // nothing that reads the raw bytes moves above the wait
-        wstore_at(wf, wslot, w1, s + 3);
-        if (two) wstore_at(wf, wslot2, w2, s + 3);
+        wstore(G3{}, wf, w1, s + 3);
+        if constexpr (two) wstore2(G3{}, wf, w2, s + 3);
         __builtin_amdgcn_sched_barrier(0);             // the next loads reuse the raw registers
-        wload(w1, s + 4);
-        if (two) wload2(w2, s + 4);
+        wload(G4{}, w1, s + 4);
+        if constexpr (two) wload2(G4{}, w2, s + 4);
         fread(xn, wn_, 0, 0);                          // stage s + 1's first fragments for the next step
     };
-    int kt = 0;
-    for (; kt + 4 <= nk; kt += 4) {
-        step(kt, xs0, ws0, xs1, ws1, xs3, ws3);
-        step(kt + 1, xs1, ws1, xs2, ws2, xs0, ws0);
-        step(kt + 2, xs2, ws2, xs3, ws3, xs1, ws1);
-        step(kt + 3, xs3, ws3, xs0, ws0, xs2, ws2);
+    // K % 256 == 0: whole super-blocks of 8 stages
+    for (int kt = 0; kt < nk; kt += 8) {
+        step(kt, P0{}, xs0, ws0, xs1, ws1, xs3, ws3);
+        step(kt, P1{}, xs1, ws1, xs2, ws2, xs0, ws0);
+        step(kt, P2{}, xs2, ws2, xs3, ws3, xs1, ws1);
+        step(kt, P3{}, xs3, ws3, xs0, ws0, xs2, ws2);
+        step(kt, std::integral_constant<int, 4>{}, xs0, ws0, xs1, ws1, xs3, ws3);
+        step(kt, std::integral_constant<int, 5>{}, xs1, ws1, xs2, ws2, xs0, ws0);
+        step(kt, std::integral_constant<int, 6>{}, xs2, ws2, xs3, ws3, xs1, ws1);
+        step(kt, std::integral_constant<int, 7>{}, xs3, ws3, xs0, ws0, xs2, ws2);
     }
-    if (kt < nk) step(kt, xs0, ws0, xs1, ws1, xs3, ws3);
-    if (kt + 1 < nk) step(kt + 1, xs1, ws1, xs2, ws2, xs0, ws0);
-    if (kt + 2 < nk) step(kt + 2, xs2, ws2, xs3, ws3, xs1, ws1);
 
     // epilogue through LDS (the ring is idle once every load has landed and every wave is past its reads): each
     // wave rounds its tile to bf16 into its own ring slot (waves 0-3 the activation slots, 4-7 the weight slots),

@@ -43,6 +43,16 @@ __device__ __forceinline__ void lds_write16(void* p, uint4 v) {
 #endif
 }
 
+// the same for 8 bytes (ds_write_b64; p 8-byte aligned)
+__device__ __forceinline__ void lds_write8(void* p, uint32_t lo, uint32_t hi) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    const uint32_t a = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)p;
+    const u32x2_t d = {lo, hi};
+    asm volatile("ds_write_b64 %0, %1" ::"v"(a), "v"(d));
+#endif
+}
+
 // s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima), N a compile-time count
 template <int N>
 __device__ __forceinline__ void wait_vm() {
