@@ -44,6 +44,25 @@ EXPORTS = {
     "wf_event_query": (_int, [_p]),
     "wf_event_synchronize": (_int, [_p]),
     "wf_event_elapsed_ms": (_int, [_p, _p, ctypes.POINTER(ctypes.c_float)]),
+    "wf_gguf_open": (_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)]),
+    "wf_gguf_close": (_int, [_p]),
+    "wf_gguf_info": (_int, [_p, ctypes.POINTER(_int)] + [ctypes.POINTER(_i64)] * 5),
+    "wf_gguf_tensor": (_int, [_p, _i64, ctypes.c_char_p, _i64, ctypes.POINTER(_int), ctypes.POINTER(_int),
+                              ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
+    "wf_gguf_kv": (_int, [_p, _i64, ctypes.c_char_p, _i64, ctypes.POINTER(_int), ctypes.POINTER(_int),
+                          ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(ctypes.c_double),
+                          ctypes.c_char_p, _i64]),
+    "wf_ring_open": (_int, [ctypes.c_char_p, _i64, _p, _p, _p, _p, _int, _int, _int, _int,
+                            ctypes.POINTER(ctypes.c_void_p)]),
+    "wf_ring_acquire": (_int, [_p, _i64, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(_i64),
+                               ctypes.POINTER(_int)]),
+    "wf_ring_release": (_int, [_p, _int, _p]),
+    "wf_ring_submit": (_int, [_p, _i64, _p, _i64, _p, _p, _p, ctypes.POINTER(_i64)]),
+    "wf_ring_wait": (_int, [_p, _i64]),
+    "wf_ring_resync": (_int, [_p]),
+    "wf_ring_stats": (_int, [_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+                             ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
+    "wf_ring_close": (_int, [_p]),
 }
 
 _lib = None

@@ -37,6 +37,7 @@ class StreamedModel:
                 prof.end_forward(state.compute_stream())
             setattr(dit, _ACTIVE_ATTR, None)
             state.restore_rest_binding()
+            state.end_forward()
 
     def profile_summary(self):
         return self.state.profile_summary()
@@ -58,10 +59,19 @@ class StreamedModel:
             delattr(self.dit, _STATE_ATTR)
 
 
-def apply_streaming(dit, device="cuda", resident_blocks=0, prefetch_slots=2, pin_memory=True, profile=None):
+def apply_streaming(dit, device="cuda", resident_blocks=0, prefetch_slots=2, pin_memory=True, profile=None,
+                    model_file=None, ram_blocks=None, ssd_layout=None, ring_depth=2, ring_threads=1, direct_io=True,
+                    tensor_name=None):
     """Stream all but the first ``resident_blocks`` blocks of ``dit`` (which stay where they are, on ``device``)
     through ``prefetch_slots`` (>= 2) GPU slots. The reference keeps block 0 resident by default
-    (streaming/dit_node.py:237-267); here resident_blocks = 0 streams every block."""
+    (streaming/dit_node.py:237-267); here resident_blocks = 0 streams every block.
+
+    SSD tier: with a GGUF ``model_file`` holding the blocks' tensors and ``ram_blocks`` below the number of streamed
+    blocks, only ``ram_blocks`` blocks are captured into pinned RAM; the others (spread by ``ssd_layout``, see
+    core.tiers.plan.ssd_positions) are read from the file on every forward by a ring of ``ring_depth`` pinned
+    buffers and ``ring_threads`` readers (O_DIRECT when ``direct_io``). ``tensor_name(block_index, param_name)``
+    gives a parameter's tensor name in the file (default "<block list>.<index>.<param name>", ComfyUI-GGUF's
+    naming of a DiT's state dict)."""
     blocks = list(_blocks(dit))
     if not blocks:
         raise ValueError("the model has no block list (blocks / transformer_blocks / layers / block)")
@@ -73,7 +83,26 @@ def apply_streaming(dit, device="cuda", resident_blocks=0, prefetch_slots=2, pin
     for i in resident_idx:
         blocks[i].to(device)
     owner = object()
-    state = _build_state(owner, device, [blocks[i] for i in stream_idx], prefetch_slots, pin_memory, profile)
+    ssd = None
+    if model_file is not None and ram_blocks is not None and ram_blocks < len(stream_idx):
+        from ..core.tiers.plan import ssd_positions
+        from ..core.tiers.sources import gguf_block_source
+        from .common import _block_list_attr, _flat_layout, _specs
+        attr = _block_list_attr(dit)
+        name_of = tensor_name or (lambda i, p: f"{attr}.{i}.{p}")
+        positions = ssd_positions(len(stream_idx), len(stream_idx) - max(0, int(ram_blocks)), ssd_layout)
+        offsets, _ = _flat_layout(_specs(blocks[stream_idx[0]]))
+        pnames = [n for n, _ in blocks[stream_idx[0]].named_parameters()]
+        names = [[name_of(stream_idx[s], p) for p in pnames] for s in positions]
+        source, sizes = gguf_block_source(model_file, names, offsets)
+        want = [p.numel() * p.element_size() for p in blocks[stream_idx[0]].parameters()]
+        if sizes != want:
+            bad = next(i for i, (a, b) in enumerate(zip(sizes, want)) if a != b)
+            raise ValueError(f"{model_file}: tensor {names[0][bad]} holds {sizes[bad]} bytes, the parameter "
+                             f"{want[bad]}")
+        ssd = {"positions": positions, "source": source, "depth": ring_depth, "threads": ring_threads,
+               "direct": direct_io}
+    state = _build_state(owner, device, [blocks[i] for i in stream_idx], prefetch_slots, pin_memory, profile, ssd)
     _install_first_block_hook(dit, blocks[0], state, owner)
     _install_block_stream_hooks(dit, state, owner)
     setattr(dit, _STATE_ATTR, state)

@@ -22,11 +22,15 @@ def _check_block_layouts(blocks):
     return specs
 
 
-def _capture_streamed_blocks(blocks, specs, offsets, flat_bytes, pin_memory=True):
+def _capture_streamed_blocks(blocks, specs, offsets, flat_bytes, pin_memory=True, skip=()):
     """Copy each streamed block's parameters into its own flat host buffer (pinned when pin_memory); returns
-    (holders, host_flats, host_views)."""
+    (holders, host_flats, host_views). Blocks whose index is in ``skip`` (the SSD tier's) get no host flat."""
     holders, host_flats, host_views = [], [], []
-    for blk in blocks:
+    for i, blk in enumerate(blocks):
+        if i in skip:
+            host_flats.append(None)
+            host_views.append(None)
+            continue
         if pin_memory:
             holder = PinnedHost(flat_bytes)
             holders.append(holder)
@@ -49,20 +53,41 @@ def _num_slots(prefetch_slots):
     return n
 
 
-def _build_state(owner, device, blocks, prefetch_slots=2, pin_memory=True, profile=None):
+def _build_state(owner, device, blocks, prefetch_slots=2, pin_memory=True, profile=None, ssd=None):
     """Capture + slots + state for the given streamed blocks; the blocks' parameters end up bound to their host
-    views (their "rest" tensors) until a forward binds them to a slot."""
+    views (their "rest" tensors) until a forward binds them to a slot. ``ssd``: the SSD tier, a dict with
+    "positions" (streamed-block indices it serves, ascending) and "source" (its blocks' file ranges in that order,
+    see core.tiers.sources; each block's packed bytes in the flat layout), optional "depth", "threads", "direct" --
+    those blocks get no pinned host flat; their parameters keep their current tensors as rest binding (the
+    reference's _setup_ssd_tier, streaming/load_steps.py:806-860)."""
     specs = _check_block_layouts(blocks)
     offsets, flat_bytes = _flat_layout(specs)
-    holders, host_flats, host_views = _capture_streamed_blocks(blocks, specs, offsets, flat_bytes, pin_memory)
+    positions = list((ssd or {}).get("positions") or [])
+    holders, host_flats, host_views = _capture_streamed_blocks(blocks, specs, offsets, flat_bytes, pin_memory,
+                                                               skip=set(positions))
     num_slots = _num_slots(prefetch_slots)
     slot_flats = [torch.empty(flat_bytes, dtype=torch.uint8, device=device) for _ in range(num_slots)]
     slot_views = [_views(f, specs, offsets) for f in slot_flats]
+    rest = []
     for blk, views in zip(blocks, host_views):
+        if views is None:
+            rest.append([p.data for p in blk.parameters()])
+            continue
         for p, v in zip(blk.parameters(), views):
             p.data = v
-    state = _StreamState(owner, device, list(blocks), host_flats, host_views, host_views, slot_flats, slot_views,
-                         is_double=True)
+        rest.append(views)
+    ring = None
+    if positions:
+        from ..core.tiers.sources import DiskRing
+        source = ssd["source"]
+        if source.n_blocks != len(positions):
+            raise ValueError(f"the SSD source has {source.n_blocks} blocks for {len(positions)} positions")
+        if source.block_bytes > flat_bytes:
+            raise ValueError(f"SSD-tier blocks of {source.block_bytes} bytes do not fit the {flat_bytes}-byte slots")
+        ring = DiskRing(source, depth=int(ssd.get("depth", 2)), pin=True, threads=int(ssd.get("threads", 1)),
+                        direct=bool(ssd.get("direct", True)), device=device)
+    state = _StreamState(owner, device, list(blocks), host_flats, host_views, rest, slot_flats, slot_views,
+                         is_double=True, ring=ring, disk_index={s: k for k, s in enumerate(positions)})
     state.holders = holders
     state.flat_bytes = flat_bytes
     if profile is None:
@@ -99,6 +124,7 @@ def _install_block_stream_hooks(dit, state, owner):
             if state.is_double:
                 if not state.issued[cur_s]:
                     state.issue_prefetch(cur_s)      # the prefetch chain was broken (a block was skipped)
+                state.wait_transfer(cur_s)
                 if prof is not None:
                     prof.record(cur_s, "wait0", compute)
                 from .. import _native

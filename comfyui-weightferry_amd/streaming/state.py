@@ -1,6 +1,8 @@
 """Block streaming state: GPU slots, the copy stream and its event fences -- the drop-in for the reference's
-_StreamState (streaming/state.py:21-323), reduced to the direct path (host flats hold the block's compute bytes;
-one host -> GPU copy per block into its slot; no staging conversion, SSD tier or scaled-fp8 swaps).
+_StreamState (streaming/state.py:21-323), on the direct path (host flats hold the block's compute bytes; one
+host -> GPU copy per block into its slot; no staging conversion or scaled-fp8 swaps), with the SSD tier: blocks
+without a host flat are read from a file by the native ring, whose uploader thread makes the copy (the role of
+_SsdUploader, streaming/ssd_uploader.py:17-120).
 
 Protocol (streaming/state.py:133-161,239-256,294-299 and the hooks of streaming/load_steps.py:451-522):
   issue_prefetch(s): on the copy stream, wait for computed_events[slot] (the slot's previous reader finished),
@@ -8,6 +10,10 @@ Protocol (streaming/state.py:133-161,239-256,294-299 and the hooks of streaming/
   pre-hook of block s: issue the copy if the chain broke, the compute stream waits for transferred_events[s], the
       block's parameters are bound to the slot's views.
   post-hook of block s: record computed_events[slot] on the compute stream, issue the copy of block s + num_slots.
+SSD-tier block s: issue_prefetch records a fresh slot-free event of its own on the compute stream (the slot's
+computed event is re-recorded by later blocks, and a copy waiting on a later recording would wait for compute that
+needs the copy) and submits the copy to the ring; the pre-hook first waits (host side) until the uploader has put
+the copy on the copy stream, then the compute stream waits for transferred_events[s] as for any block.
 Copies run on the library's stream with hipMemcpyAsync; the compute stream is torch's current stream."""
 import torch
 
@@ -18,7 +24,7 @@ class _StreamState:
     """Per-model streaming state, owned by one owner token."""
 
     def __init__(self, owner, device, streaming_blocks, host_flats, host_views, rest, slot_flats, slot_views,
-                 is_double=True):
+                 is_double=True, ring=None, disk_index=None):
         self.owner = owner
         self.device = torch.device(device)
         self.streaming_blocks = streaming_blocks
@@ -42,6 +48,12 @@ class _StreamState:
         self.issued = [False] * self.num_stream
         self.slot_ptrs = {v.data_ptr() for views in slot_views for v in views}
         self.copies = 0
+        # SSD tier: stream index -> position in the ring's block order
+        self.ring = ring
+        self.disk_index = dict(disk_index or {})
+        self.free_events = {s: _native.Event() for s in self.disk_index}
+        self.tickets = {}
+        self.ssd_submitted = 0
 
     def compute_stream(self):
         return torch.cuda.current_stream(self.device).cuda_stream
@@ -69,14 +81,45 @@ class _StreamState:
             self.profiler.mark(s_idx, "cpu_issue")
         slot_idx = self.slot_of(s_idx)
         stream = self.prefetch_stream.handle
+        if s_idx in self.disk_index:
+            free = self.free_events[s_idx]
+            free.record(self.compute_stream())
+            self.tickets[s_idx] = self.ring.submit(self.disk_index[s_idx], self.slot_flats[slot_idx], free,
+                                                   self.transferred_events[s_idx], stream)
+            self.ssd_submitted += 1
+            self.copies += 1
+            self.issued[s_idx] = True
+            return
         _native.stream_wait(stream, self.computed_events[slot_idx])
         self.materialize(s_idx, slot_idx, stream)
         self.transferred_events[s_idx].record(stream)
         self.transferred_events[s_idx].query()        # forces submission without blocking the CPU
         self.issued[s_idx] = True
 
+    def wait_transfer(self, s_idx):
+        """Host side of the pre-hook for an SSD-tier block: its copy is on the copy stream (the event recorded)."""
+        if s_idx in self.disk_index:
+            self.ring.wait(self.tickets.pop(s_idx))
+
     def begin_forward(self):
         self.issued = [False] * self.num_stream
+        self.ssd_submitted = 0
+
+    def end_forward(self):
+        """After a forward: when it stopped part way through the SSD tier, let the submitted copies finish and restart
+        the ring's cycle at block 0 (DiskRing.restart_if_needed, core/tiers/sources.py:318-335)."""
+        if self.ring is None:
+            return
+        pending = list(self.tickets.values())
+        self.tickets.clear()
+        for t in pending:
+            try:
+                self.ring.wait(t)
+            except _native.NativeError:
+                pass
+        if pending or self.ssd_submitted % max(1, len(self.disk_index)) != 0:
+            self.prefetch_stream.synchronize()
+            self.ring.resync()
 
     def prefetch_first_slots(self):
         """Called when block 0 runs: the first num_slots copies."""
@@ -86,7 +129,8 @@ class _StreamState:
                     self.issue_prefetch(s_idx)
 
     def restore_rest_binding(self):
-        """Rebind every parameter that still points at a GPU slot to its rest tensor."""
+        """Rebind every parameter that still points at a GPU slot to its rest tensor (its host view, or for an
+        SSD-tier block the tensor it had before streaming)."""
         for blk, rest in zip(self.streaming_blocks, self.rest):
             for p, r in zip(blk.parameters(), rest):
                 if p.data.data_ptr() in self.slot_ptrs:
@@ -97,11 +141,21 @@ class _StreamState:
 
     def close(self):
         """Wait for the copies, remove the hooks, drop the events and the stream."""
+        if self.ring is not None:
+            for t in list(self.tickets.values()):
+                try:
+                    self.ring.wait(t)
+                except _native.NativeError:
+                    pass
+            self.tickets.clear()
         self.prefetch_stream.synchronize()
+        if self.ring is not None:
+            self.ring.close()
+            self.ring = None
         for h in self.handles:
             h.remove()
         self.handles = []
-        for e in self.transferred_events + self.computed_events:
+        for e in self.transferred_events + self.computed_events + list(self.free_events.values()):
             e.close()
         self.prefetch_stream.close()
         if self.profiler is not None:

@@ -63,6 +63,27 @@ class WanLikeBlock(torch.nn.Module):
         return x + self.down(torch.nn.functional.gelu(self.up(h), approximate="tanh"))
 
 
+def gguf_tensors(model, attr="blocks"):
+    """(name, GGML type, torch shape, bytes) of every parameter of the stack's blocks in parameters() order, named
+    "<attr>.<block index>.<parameter name>": GGUFLinear weights as their quantised blocks, bf16 biases as BF16."""
+    out = []
+    for i, blk in enumerate(getattr(model, attr)):
+        for mname, mod in blk.named_modules():
+            if not isinstance(mod, GGUFLinear):
+                continue
+            out.append((f"{attr}.{i}.{mname}.weight", mod.qtype, (mod.out_features, mod.in_features), mod.weight.data))
+            if mod.bias is not None:
+                out.append((f"{attr}.{i}.{mname}.bias", 30, (mod.out_features,), mod.bias.data))
+    return out
+
+
+def write_gguf_model(model, path, alignment=256):
+    """The stack's block parameters as a GGUF file (general.architecture "wan"), tensors in parameters() order at
+    ``alignment``: with the flat layout's 256-byte alignment a block is one contiguous range of the file."""
+    from ..core.tiers.gguf_file import write_gguf
+    return write_gguf(path, gguf_tensors(model), {"general.architecture": "wan"}, alignment=alignment)
+
+
 class WanLikeStack(torch.nn.Module):
     def __init__(self, n_blocks=40, dim=5120, heads=40, ffn=13824, qtype=12, mode="fused"):
         super().__init__()

@@ -125,6 +125,53 @@ int wf_event_query(void* event);
 int wf_event_synchronize(void* event);
 int wf_event_elapsed_ms(void* start, void* end, float* ms);
 
+/* ---------------------------------------------------------------------------------------------- GGUF files
+ * The tensor table of a GGUF model file (version 2 or 3): the reference reads GGUF files through ComfyUI-GGUF /
+ * gguf-py (not vendored; the files come from its tools/convert_to_gguf.py and llama.cpp's converters); these calls
+ * give the SSD tier each tensor's absolute byte range so streamed blocks are read straight from the model file
+ * (the role of file_block_layout / file_param_layout, core/tiers/plan.py:181-250, for GGUF instead of
+ * safetensors). The file is untrusted: a malformed header is WF_EINVAL with a message, never a read out of
+ * bounds. dims4: the tensor's dimensions, innermost first (GGUF order), padded with 1. Types: the GGML ids of
+ * weightferry's formats plus F32 0, F16 1, BF16 30. */
+int wf_gguf_open(const char* path, void** handle);
+int wf_gguf_close(void* handle);
+int wf_gguf_info(void* handle, int* version, int64_t* n_tensors, int64_t* n_kv, int64_t* alignment,
+                 int64_t* data_offset, int64_t* file_bytes);
+int wf_gguf_tensor(void* handle, int64_t i, char* name, int64_t name_cap, int* type, int* n_dims, int64_t* dims4,
+                   int64_t* offset, int64_t* nbytes);
+/* key/value i: type = GGUF value type (0-12); for arrays (9) elem_type and count; integers and bools in ival, floats
+ * in fval (integers too), strings in sval (count = its length). */
+int wf_gguf_kv(void* handle, int64_t i, char* key, int64_t key_cap, int* type, int* elem_type, int64_t* count,
+               int64_t* ival, double* fval, char* sval, int64_t sval_cap);
+
+/* ---------------------------------------------------------------------------------------------- SSD tier
+ * A ring of `depth` host buffers filled by `threads` reader threads with streamed blocks read from the file at
+ * `path`, in cyclic block order: the role of DiskRing (core/tiers/sources.py:165-355) with FileBlockSource /
+ * PieceFileSource (:87-152), and, with wf_ring_submit / wf_ring_wait, of _SsdUploader (streaming/ssd_uploader.py:
+ * 17-120). Block b is pieces piece_start[b] .. piece_start[b+1]-1: (file offset, bytes, offset in the packed block),
+ * in increasing block offset. Flags: WF_RING_PINNED (page-locked buffers; required for submit), WF_RING_DIRECT
+ * (O_DIRECT reads of 4 KiB aligned supersets through an aligned scratch buffer; ordinary reads where the file system
+ * refuses). Consumers take blocks in the ring's order (block = position % n_blocks), either with acquire / release
+ * from one thread (release's stream, if not NULL, must carry the copy out of the buffer: the buffer is refilled
+ * after it), or with submit / wait: an uploader thread waits for the block, makes `stream` wait for `wait_event`,
+ * copies into dst (dst_bytes >= the block), records `done_event` and returns the buffer to the readers; wait(ticket)
+ * returns once that copy is on the stream (done_event recorded). A read or copy failure fails the ring: blocks read
+ * before it are still served, later ones return an error until wf_ring_resync, which restarts the cycle at block 0
+ * (no copies pending). */
+#define WF_RING_PINNED 1
+#define WF_RING_DIRECT 2
+int wf_ring_open(const char* path, int64_t n_blocks, const int64_t* piece_start, const int64_t* piece_off,
+                 const int64_t* piece_len, const int64_t* piece_dst, int depth, int threads, int flags, int device,
+                 void** ring);
+int wf_ring_acquire(void* ring, int64_t block, void** ptr, int64_t* nbytes, int* slot);
+int wf_ring_release(void* ring, int slot, void* stream);
+int wf_ring_submit(void* ring, int64_t block, void* dst, int64_t dst_bytes, void* wait_event, void* done_event,
+                   void* stream, int64_t* ticket);
+int wf_ring_wait(void* ring, int64_t ticket);
+int wf_ring_resync(void* ring);
+int wf_ring_stats(void* ring, double* read_s, double* wait_s, int64_t* bytes, int64_t* reads);
+int wf_ring_close(void* ring);
+
 #ifdef __cplusplus
 }
 #endif
