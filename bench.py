@@ -15,10 +15,12 @@ Other rows of the workload list are reported under "also":
   * the LoRA add on a Q4_K 13824 x 5120 weight: the first LoRA fused into the dequantisation and a later LoRA
     onto the bf16 weight (float32 difference of n values each);
   * 40 streamed Wan-14B blocks of Q4_K from pinned host memory through 2 GPU slots, 4096 tokens (ms/step, H2D
-    GB/s, share of the copy time hidden behind compute).
+    GB/s, share of the copy time hidden behind compute);
+  * the SSD tier: the same 40 blocks as a GGUF file on local disk, the reader ring's O_DIRECT read rate, and the
+    streamed forward with half the blocks read from the file on every step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--only-headline] [--legs LEGS]
---legs (comma list of headline, lora, int8, fused, streaming; default all) runs only those legs, for profiling one
+--legs (comma list of headline, lora, int8, fused, streaming, ssd; default all) runs only those legs, for profiling one
 kernel family; without the headline leg the printed line holds the legs' figures only.
 """
 import argparse
@@ -41,10 +43,10 @@ def _args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true", help="leave out the CPU baseline leg")
     ap.add_argument("--only-headline", action="store_true", help="the Q4_K dequant leg only")
-    ap.add_argument("--legs", default="all", help="comma list: headline, lora, int8, fused, streaming")
+    ap.add_argument("--legs", default="all", help="comma list: headline, lora, int8, fused, streaming, ssd")
     a = ap.parse_args()
     a.legs = {"headline"} if a.only_headline else (
-        {"headline", "lora", "int8", "fused", "streaming"} if a.legs == "all" else set(a.legs.split(",")))
+        {"headline", "lora", "int8", "fused", "streaming", "ssd"} if a.legs == "all" else set(a.legs.split(",")))
     return a
 
 
@@ -167,6 +169,64 @@ def streaming_leg(torch, native, n_blocks=40, steps=10):
             "profiled": {"forward_ms": prof["forward_ms"], "dma_ms": prof["dma_ms"], "stall_ms": prof["stall_ms"],
                          "hidden_fraction": prof["overlap_ratio"], "dma_gbps": prof["dma_gbps"]},
             "linears": "wf_dequant + torch bf16 GEMM"}
+
+
+def ssd_leg(torch, native, n_blocks=40, ram_blocks=20, steps=3):
+    """SSD tier: 40 Wan-14B blocks (Q4_K, 197.7 MB each) written as a GGUF model file to local disk
+    (WEIGHTFERRY_SSD_DIR, else the temp directory); the native ring's raw O_DIRECT read rate over the whole file with
+    1, 2 and 4 reader threads (4 pinned buffers), then a streamed forward (4096 tokens) with ``ram_blocks`` blocks in
+    pinned RAM and the others (interleaved) read from the file on every step through the ring (4 buffers, 2 readers)."""
+    import tempfile
+    syn = importlib.import_module(PKG + ".streaming.synthetic")
+    dn = importlib.import_module(PKG + ".streaming.dit_node")
+    src = importlib.import_module(PKG + ".core.tiers.sources")
+    common = importlib.import_module(PKG + ".streaming.common")
+    dev = torch.device("cuda:0")
+    path = os.path.join(os.environ.get("WEIGHTFERRY_SSD_DIR") or tempfile.gettempdir(), f"wf_ssd_{os.getpid()}.gguf")
+    model = syn.WanLikeStack(n_blocks=n_blocks, qtype=12, mode="dequant")
+    model.fill_random(1234)
+    t = time.perf_counter()
+    syn.write_gguf_model(model, path)
+    with open(path, "rb") as f:
+        os.fsync(f.fileno())
+    size = os.path.getsize(path)
+    _log(f"ssd: wrote {size / 1e9:.2f} GB GGUF in {time.perf_counter() - t:.1f} s")
+    try:
+        offsets, flat_bytes = common._flat_layout(common._specs(model.blocks[0]))
+        pnames = [n for n, _ in model.blocks[0].named_parameters()]
+        source, _ = src.gguf_block_source(path, [[f"blocks.{i}.{p}" for p in pnames] for i in range(n_blocks)],
+                                          offsets)
+        block_bytes = source.block_bytes
+        reads = {}
+        for threads in (1, 2, 4):
+            ring = src.DiskRing(source, depth=4, pin=True, threads=threads, direct=True, device=dev)
+            t0 = time.perf_counter()
+            for b in range(n_blocks):
+                _, slot = ring.acquire(b)
+                ring.release(slot)
+            dt = time.perf_counter() - t0
+            ring.close()
+            reads[f"threads_{threads}_GBps"] = round(block_bytes * n_blocks / dt / 1e9, 2)
+        _log(f"ssd: ring reads {reads}")
+        g = torch.Generator().manual_seed(99)
+        x = torch.randn((1, 4096, 5120), generator=g).to(torch.bfloat16).to(dev)
+        ctx = torch.randn((1, 512, 5120), generator=g).to(torch.bfloat16).to(dev)
+        sm = dn.apply_streaming(model, device=dev, prefetch_slots=2, profile=False, model_file=path,
+                                ram_blocks=ram_blocks, ring_depth=4, ring_threads=2)
+        n_disk = len(sm.state.disk_index)
+        with torch.no_grad():
+            ms = _timed(torch, lambda: sm(x, ctx), steps, 1)
+        st = sm.state.ring.stats()
+        sm.teardown(device="cpu")
+    finally:
+        os.remove(path)
+    del model
+    torch.cuda.empty_cache()
+    return {"file_GB": round(size / 1e9, 3), "ring_raw_read": reads, "ms_per_step": round(ms, 1),
+            "blocks": n_blocks, "ram_tier_blocks": n_blocks - n_disk, "ssd_tier_blocks": n_disk,
+            "ssd_bytes_per_step": block_bytes * n_disk,
+            "ssd_GBps_per_step": round(block_bytes * n_disk / (ms / 1e3) / 1e9, 2),
+            "ring_reads": st["reads"], "layout": "interleave", "direct_io": True}
 
 
 def _log(msg):
@@ -312,6 +372,8 @@ def main():
             also["fused_dequant_gemm_wan_block"] = fused_leg(torch, native)
         if "streaming" in args.legs:
             also["streamed_40_blocks_q4_k"] = streaming_leg(torch, native)
+        if "ssd" in args.legs:
+            also["ssd_tier_40_blocks_q4_k"] = ssd_leg(torch, native)
         print(json.dumps({"legs": sorted(args.legs), "also": also}), flush=True)
         return
 
@@ -357,6 +419,9 @@ def main():
     if "streaming" in args.legs:
         also["streamed_40_blocks_q4_k"] = streaming_leg(torch, native)
         _log("streaming leg done")
+    if "ssd" in args.legs:
+        also["ssd_tier_40_blocks_q4_k"] = ssd_leg(torch, native)
+        _log("ssd leg done")
     cpu = None
     if not args.skip_cpu:
         cpu = cpu_baseline_dequant(torch, raws[0], 12, 512, 5120)

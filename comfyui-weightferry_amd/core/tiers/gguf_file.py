@@ -169,14 +169,14 @@ def write_gguf(path, tensors, metadata=None, alignment=32, version=3):
         items.append((k, v))
     infos, datas, offset = [], [], 0
     for name, qtype, shape, data in tensors:
-        buf = _as_bytes(data)
+        buf = _as_buffer(data)
         need = tensor_nbytes(qtype, shape)
-        if len(buf) != need:
-            raise ValueError(f"tensor {name}: {len(buf)} bytes for {need}")
+        if buf.nbytes != need:
+            raise ValueError(f"tensor {name}: {buf.nbytes} bytes for {need}")
         offset = (offset + alignment - 1) // alignment * alignment
         infos.append((name, qtype, tuple(int(d) for d in shape)[::-1], offset))
         datas.append((offset, buf))
-        offset += len(buf)
+        offset += buf.nbytes
     head = b"GGUF" + struct.pack("<IQQ", version, len(infos), len(items))
     for k, v in items:
         head += _pack_string(k) + struct.pack("<I", v.type) + _pack_value(v.type, v.value, v.elem_type)
@@ -189,20 +189,21 @@ def write_gguf(path, tensors, metadata=None, alignment=32, version=3):
         pos = 0
         for off, buf in datas:
             f.write(b"\0" * (off - pos))
-            f.write(buf)
-            pos = off + len(buf)
+            f.write(memoryview(buf))
+            pos = off + buf.nbytes
     return data_start
 
 
-def _as_bytes(data):
+def _as_buffer(data):
+    """Contiguous uint8 numpy view of a tensor's bytes (no copy for contiguous CPU data)."""
     if isinstance(data, (bytes, bytearray, memoryview)):
-        return bytes(data)
+        return np.frombuffer(data, dtype=np.uint8)
     if isinstance(data, np.ndarray):
-        return np.ascontiguousarray(data).view(np.uint8).tobytes()
+        return np.ascontiguousarray(data).reshape(-1).view(np.uint8)
     try:
         import torch
         if isinstance(data, torch.Tensor):
-            return data.detach().contiguous().cpu().view(torch.uint8).numpy().tobytes()
+            return data.detach().contiguous().cpu().reshape(-1).view(torch.uint8).numpy()
     except ImportError:
         pass
     raise TypeError(f"tensor data of type {type(data).__name__}")
