@@ -33,7 +33,7 @@
 #include <thread>
 #include <vector>
 
-#include "wf_common.h"
+#include "host_common.h"
 
 namespace wf {
 namespace {

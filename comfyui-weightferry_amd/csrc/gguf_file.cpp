@@ -21,7 +21,7 @@
 #include <string>
 #include <vector>
 
-#include "wf_common.h"
+#include "host_common.h"
 
 namespace wf {
 namespace {
