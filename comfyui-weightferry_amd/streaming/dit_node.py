@@ -22,8 +22,13 @@ class StreamedModel:
         self.owner = owner
 
     def __call__(self, *args, **kwargs):
-        """One forward with streaming active (streaming_diffusion_model_wrapper, streaming/dit_node.py:414-455):
-        begin_forward, the owner token, and the slot bindings undone afterwards whatever happens."""
+        """One forward of the model with streaming active."""
+        return self.run(self.dit, *args, **kwargs)
+
+    def run(self, fn, *args, **kwargs):
+        """fn(*args, **kwargs) -- the model's forward, or the host application's executor of it -- with streaming
+        active (streaming_diffusion_model_wrapper, streaming/dit_node.py:414-455): begin_forward, the owner token,
+        and the slot bindings undone afterwards whatever happens."""
         dit, state = self.dit, self.state
         setattr(dit, _ACTIVE_ATTR, self.owner)
         prof = state.profiler
@@ -31,7 +36,7 @@ class StreamedModel:
             state.begin_forward()
             if prof is not None:
                 prof.begin_forward(state.compute_stream())
-            return dit(*args, **kwargs)
+            return fn(*args, **kwargs)
         finally:
             if prof is not None:
                 prof.end_forward(state.compute_stream())
@@ -61,7 +66,7 @@ class StreamedModel:
 
 def apply_streaming(dit, device="cuda", resident_blocks=0, prefetch_slots=2, pin_memory=True, profile=None,
                     model_file=None, ram_blocks=None, ssd_layout=None, ring_depth=2, ring_threads=1, direct_io=True,
-                    tensor_name=None):
+                    tensor_name=None, double_buffer=True):
     """Stream all but the first ``resident_blocks`` blocks of ``dit`` (which stay where they are, on ``device``)
     through ``prefetch_slots`` (>= 2) GPU slots. The reference keeps block 0 resident by default
     (streaming/dit_node.py:237-267); here resident_blocks = 0 streams every block.
@@ -102,7 +107,8 @@ def apply_streaming(dit, device="cuda", resident_blocks=0, prefetch_slots=2, pin
                              f"{want[bad]}")
         ssd = {"positions": positions, "source": source, "depth": ring_depth, "threads": ring_threads,
                "direct": direct_io}
-    state = _build_state(owner, device, [blocks[i] for i in stream_idx], prefetch_slots, pin_memory, profile, ssd)
+    state = _build_state(owner, device, [blocks[i] for i in stream_idx], prefetch_slots, pin_memory, profile, ssd,
+                         double_buffer)
     _install_first_block_hook(dit, blocks[0], state, owner)
     _install_block_stream_hooks(dit, state, owner)
     setattr(dit, _STATE_ATTR, state)

@@ -53,19 +53,22 @@ def _num_slots(prefetch_slots):
     return n
 
 
-def _build_state(owner, device, blocks, prefetch_slots=2, pin_memory=True, profile=None, ssd=None):
+def _build_state(owner, device, blocks, prefetch_slots=2, pin_memory=True, profile=None, ssd=None, double_buffer=True):
     """Capture + slots + state for the given streamed blocks; the blocks' parameters end up bound to their host
     views (their "rest" tensors) until a forward binds them to a slot. ``ssd``: the SSD tier, a dict with
     "positions" (streamed-block indices it serves, ascending) and "source" (its blocks' file ranges in that order,
     see core.tiers.sources; each block's packed bytes in the flat layout), optional "depth", "threads", "direct" --
     those blocks get no pinned host flat; their parameters keep their current tensors as rest binding (the
-    reference's _setup_ssd_tier, streaming/load_steps.py:806-860)."""
+    reference's _setup_ssd_tier, streaming/load_steps.py:806-860). double_buffer=False: one slot, each block copied
+    on the compute stream in its pre-hook (the reference's Single Buffer mode; not with an SSD tier)."""
     specs = _check_block_layouts(blocks)
     offsets, flat_bytes = _flat_layout(specs)
     positions = list((ssd or {}).get("positions") or [])
     holders, host_flats, host_views = _capture_streamed_blocks(blocks, specs, offsets, flat_bytes, pin_memory,
                                                                skip=set(positions))
-    num_slots = _num_slots(prefetch_slots)
+    if not double_buffer and positions:
+        raise ValueError("the SSD tier needs the double-buffered (prefetching) mode")
+    num_slots = _num_slots(prefetch_slots) if double_buffer else 1
     slot_flats = [torch.empty(flat_bytes, dtype=torch.uint8, device=device) for _ in range(num_slots)]
     slot_views = [_views(f, specs, offsets) for f in slot_flats]
     rest = []
@@ -87,7 +90,7 @@ def _build_state(owner, device, blocks, prefetch_slots=2, pin_memory=True, profi
         ring = DiskRing(source, depth=int(ssd.get("depth", 2)), pin=True, threads=int(ssd.get("threads", 1)),
                         direct=bool(ssd.get("direct", True)), device=device)
     state = _StreamState(owner, device, list(blocks), host_flats, host_views, rest, slot_flats, slot_views,
-                         is_double=True, ring=ring, disk_index={s: k for k, s in enumerate(positions)})
+                         is_double=double_buffer, ring=ring, disk_index={s: k for k, s in enumerate(positions)})
     state.holders = holders
     state.flat_bytes = flat_bytes
     if profile is None:

@@ -1,0 +1,104 @@
+"""The WeightFerryDiT node on the GPU through a stand-in ModelPatcher (ON_LOAD / ON_DETACH callbacks and the
+DIFFUSION_MODEL wrapper, as ComfyUI calls them): every forward is bit-identical to the same stack resident on the GPU
+(the reference's criterion, tests/test_streaming.py:222) -- after a load, twice; when ComfyUI skipped ON_LOAD (lazy
+capture in the wrapper); with Single Buffer; after a re-load; and with tiering Auto putting blocks over the RAM
+budget on the SSD tier (read from the GGUF file). A detach gives the weights back on the CPU."""
+import pytest
+import torch
+
+from conftest import sub
+
+import fake_comfy
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture
+def comfy():
+    fake_comfy.make_comfy_modules()
+    yield
+    fake_comfy.remove_comfy_modules()
+
+
+def _stack(n=6, seed=7):
+    syn = sub("streaming.synthetic")
+    torch.manual_seed(0)
+    m = syn.WanLikeStack(n_blocks=n, dim=512, heads=4, ffn=1024, qtype=12)
+    m.fill_random(seed)
+    return m
+
+
+def _inputs():
+    g = torch.Generator().manual_seed(99)
+    x = torch.randn((1, 256, 512), generator=g).to(torch.bfloat16).cuda()
+    ctx = torch.randn((1, 64, 512), generator=g).to(torch.bfloat16).cuda()
+    return x, ctx
+
+
+@pytest.fixture
+def reference():
+    x, ctx = _inputs()
+    with torch.no_grad():
+        ref = _stack().cuda()(x, ctx)
+    torch.cuda.synchronize()
+    return x, ctx, ref
+
+
+def _check(mp, x, ctx, ref, times=2):
+    for _ in range(times):
+        with torch.no_grad():
+            y = mp.apply_model(x, ctx)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("buffer_mode,slots", [("Double Buffer (Async Prefetch, Recommended)", 3),
+                                               ("Double Buffer (Async Prefetch, Recommended)", 2),
+                                               ("Single Buffer (Synchronous)", 3)])
+def test_load_forward_detach(native, comfy, reference, buffer_mode, slots):
+    x, ctx, ref = reference
+    node = sub("streaming.node")
+    model = _stack()
+    mp = node.WeightFerryDiT().apply_streaming(fake_comfy.FakeModelPatcher(model), resident_blocks=1,
+                                               buffer_mode=buffer_mode, prefetch_slots=slots)[0]
+    model.blocks[0].cuda()                      # ComfyUI loads the resident part before ON_LOAD
+    mp.load()
+    sm = getattr(model, node._NODE_ATTR)
+    assert len(sm.stream_idx) == 5 and sm.state.num_slots == (slots if "Double" in buffer_mode else 1)
+    _check(mp, x, ctx, ref)
+    mp.detach()
+    assert getattr(model, node._NODE_ATTR) is None
+    assert all(p.device.type == "cpu" for b in model.blocks[1:] for p in b.parameters())
+
+
+def test_skipped_on_load_captures_lazily(native, comfy, reference):
+    x, ctx, ref = reference
+    node = sub("streaming.node")
+    model = _stack()
+    mp = node.WeightFerryDiT().apply_streaming(fake_comfy.FakeModelPatcher(model), resident_blocks=2)[0]
+    model.blocks[0].cuda()
+    model.blocks[1].cuda()
+    _check(mp, x, ctx, ref)                     # no load(): the wrapper captures at the first forward
+    mp.load()                                   # a re-load tears the capture down and captures again
+    _check(mp, x, ctx, ref)
+    mp.detach()
+
+
+def test_tiering_auto_reads_blocks_over_the_budget_from_the_file(native, comfy, reference, tmp_path, monkeypatch):
+    x, ctx, ref = reference
+    node = sub("streaming.node")
+    syn = sub("streaming.synthetic")
+    model = _stack()
+    path = str(tmp_path / "wan6.gguf")
+    syn.write_gguf_model(model, path)
+    per_block = sum(p.numel() * p.element_size() for p in model.blocks[1].parameters())
+    monkeypatch.setenv("WEIGHTFERRY_MODEL_FILE", path)
+    mp = node.WeightFerryDiT().apply_streaming(fake_comfy.FakeModelPatcher(model), resident_blocks=1,
+                                               tiering="Auto (GPU / RAM / SSD)",
+                                               ram_budget_gb=2.5 * per_block / 1024 ** 3)[0]
+    model.blocks[0].cuda()
+    mp.load()
+    sm = getattr(model, node._NODE_ATTR)
+    assert len(sm.state.disk_index) == 3        # 5 streamed blocks, 2 fit the RAM budget
+    _check(mp, x, ctx, ref, times=3)
+    mp.detach()
