@@ -13,6 +13,12 @@ DEFAULTS = {
     # the reference's experimental prefetch-stream priority; every stream here keeps the default priority, so
     # the flag is read and ignored (streaming/state.py)
     "WEIGHTFERRY_PREFETCH_PRIORITY": None,
+    # SSD tier
+    "WEIGHTFERRY_TIERING": None,           # "auto" / "ram": overrides the node's tiering option
+    "WEIGHTFERRY_RAM_BUDGET_GB": None,     # overrides the node's ram_budget_gb
+    "WEIGHTFERRY_SSD_LAYOUT": None,        # "tail": the SSD tier is the last blocks (default: interleaved)
+    "WEIGHTFERRY_MODEL_FILE": None,        # the GGUF file the SSD tier reads blocks from (else a cache file)
+    "WEIGHTFERRY_CACHE_DIR": None,         # directory of the SSD tier's cache files (default: temp directory)
 }
 
 

@@ -66,17 +66,18 @@ class StreamedModel:
 
 def apply_streaming(dit, device="cuda", resident_blocks=0, prefetch_slots=2, pin_memory=True, profile=None,
                     model_file=None, ram_blocks=None, ssd_layout=None, ring_depth=2, ring_threads=1, direct_io=True,
-                    tensor_name=None, double_buffer=True):
+                    tensor_name=None, double_buffer=True, ssd_dir=None):
     """Stream all but the first ``resident_blocks`` blocks of ``dit`` (which stay where they are, on ``device``)
     through ``prefetch_slots`` (>= 2) GPU slots. The reference keeps block 0 resident by default
     (streaming/dit_node.py:237-267); here resident_blocks = 0 streams every block.
 
-    SSD tier: with a GGUF ``model_file`` holding the blocks' tensors and ``ram_blocks`` below the number of streamed
-    blocks, only ``ram_blocks`` blocks are captured into pinned RAM; the others (spread by ``ssd_layout``, see
-    core.tiers.plan.ssd_positions) are read from the file on every forward by a ring of ``ring_depth`` pinned
-    buffers and ``ring_threads`` readers (O_DIRECT when ``direct_io``). ``tensor_name(block_index, param_name)``
-    gives a parameter's tensor name in the file (default "<block list>.<index>.<param name>", ComfyUI-GGUF's
-    naming of a DiT's state dict)."""
+    SSD tier: with ``ram_blocks`` below the number of streamed blocks, only ``ram_blocks`` blocks are captured into
+    pinned RAM; the others (spread by ``ssd_layout``, see core.tiers.plan.ssd_positions) are read from disk on every
+    forward by a ring of ``ring_depth`` pinned buffers and ``ring_threads`` readers (O_DIRECT when ``direct_io``):
+    straight from a GGUF ``model_file`` holding the blocks' tensors, or else from a cache file the capture writes
+    into ``ssd_dir`` (default WEIGHTFERRY_CACHE_DIR / the temp directory). ``tensor_name(block_index,
+    param_name)`` gives a parameter's tensor name in the model file (default "<block list>.<index>.<param name>",
+    ComfyUI-GGUF's naming of a DiT's state dict)."""
     blocks = list(_blocks(dit))
     if not blocks:
         raise ValueError("the model has no block list (blocks / transformer_blocks / layers / block)")
@@ -89,7 +90,11 @@ def apply_streaming(dit, device="cuda", resident_blocks=0, prefetch_slots=2, pin
         blocks[i].to(device)
     owner = object()
     ssd = None
-    if model_file is not None and ram_blocks is not None and ram_blocks < len(stream_idx):
+    if model_file is None and ram_blocks is not None and ram_blocks < len(stream_idx):
+        from ..core.tiers.plan import ssd_positions
+        ssd = {"positions": ssd_positions(len(stream_idx), len(stream_idx) - max(0, int(ram_blocks)), ssd_layout),
+               "cache_dir": ssd_dir, "depth": ring_depth, "threads": ring_threads, "direct": direct_io}
+    elif model_file is not None and ram_blocks is not None and ram_blocks < len(stream_idx):
         from ..core.tiers.plan import ssd_positions
         from ..core.tiers.sources import gguf_block_source
         from .common import _block_list_attr, _flat_layout, _specs

@@ -57,8 +57,9 @@ def _build_state(owner, device, blocks, prefetch_slots=2, pin_memory=True, profi
     """Capture + slots + state for the given streamed blocks; the blocks' parameters end up bound to their host
     views (their "rest" tensors) until a forward binds them to a slot. ``ssd``: the SSD tier, a dict with
     "positions" (streamed-block indices it serves, ascending) and "source" (its blocks' file ranges in that order,
-    see core.tiers.sources; each block's packed bytes in the flat layout), optional "depth", "threads", "direct" --
-    those blocks get no pinned host flat; their parameters keep their current tensors as rest binding (the
+    see core.tiers.sources; each block's packed bytes in the flat layout) -- or, without a source, "cache_dir": the
+    blocks' captured bytes are written into a cache file there (core.tiers.cache_files) -- optional "depth",
+    "threads", "direct". Those blocks get no pinned host flat; their parameters keep their current tensors as rest binding (the
     reference's _setup_ssd_tier, streaming/load_steps.py:806-860). double_buffer=False: one slot, each block copied
     on the compute stream in its pre-hook (the reference's Single Buffer mode; not with an SSD tier)."""
     specs = _check_block_layouts(blocks)
@@ -79,10 +80,23 @@ def _build_state(owner, device, blocks, prefetch_slots=2, pin_memory=True, profi
         for p, v in zip(blk.parameters(), views):
             p.data = v
         rest.append(views)
-    ring = None
+    ring = store = None
     if positions:
         from ..core.tiers.sources import DiskRing
-        source = ssd["source"]
+        source = ssd.get("source")
+        if source is None:
+            # no model file to read: the SSD tier's blocks go into a cache file (their final bytes, as captured)
+            from ..core.tiers.cache_files import DiskBlockStore, default_cache_dir
+            store = DiskBlockStore(ssd.get("cache_dir") or default_cache_dir(), flat_bytes, len(positions))
+            stage = torch.empty(flat_bytes, dtype=torch.uint8)
+            views = _views(stage, specs, offsets)
+            for k, s_idx in enumerate(positions):
+                stage.zero_()
+                for p, v in zip(blocks[s_idx].parameters(), views):
+                    v.copy_(p.data)
+                store.write_block(k, stage)
+            store.finalize()
+            source = store.source()
         if source.n_blocks != len(positions):
             raise ValueError(f"the SSD source has {source.n_blocks} blocks for {len(positions)} positions")
         if source.block_bytes > flat_bytes:
@@ -91,6 +105,7 @@ def _build_state(owner, device, blocks, prefetch_slots=2, pin_memory=True, profi
                         direct=bool(ssd.get("direct", True)), device=device)
     state = _StreamState(owner, device, list(blocks), host_flats, host_views, rest, slot_flats, slot_views,
                          is_double=double_buffer, ring=ring, disk_index={s: k for k, s in enumerate(positions)})
+    state.disk_store = store
     state.holders = holders
     state.flat_bytes = flat_bytes
     if profile is None:

@@ -10,9 +10,9 @@ registers
     ON_LOAD (a clone switch).
 Block 0 stays resident (resident_blocks >= 1), as in the reference.
 
-Tiering "Auto" puts the streamed blocks over the RAM budget (``ram_budget_gb``; 0: all in RAM) on the SSD tier,
+Tiering "Auto" puts the streamed blocks over the RAM budget (``ram_budget_gb``; 0: all in RAM) on the SSD tier:
 read straight from the GGUF model file named by WEIGHTFERRY_MODEL_FILE (ComfyUI-GGUF's loaded tensors do not carry
-their file's path). Options of the reference that belong to other paths -- SageAttention, fp8 storage format,
+their file's path), or else from a cache file of their captured bytes (WEIGHTFERRY_CACHE_DIR). Options of the reference that belong to other paths -- SageAttention, fp8 storage format,
 self-managed residents, auto-configuration, the VRAM budget, chunk streaming -- are accepted and logged as not
 applied; the node then streams as with their defaults."""
 import math
@@ -123,9 +123,6 @@ class WeightFerryDiT:
         env_budget = _env.get("WEIGHTFERRY_RAM_BUDGET_GB")
         budget = float(env_budget) if env_budget else float(ram_budget_gb)
         model_file = _env.get("WEIGHTFERRY_MODEL_FILE") if tier_auto else None
-        if tier_auto and budget > 0 and not model_file:
-            log_warn("DiT Layer Streaming [tiers]: tiering Auto needs WEIGHTFERRY_MODEL_FILE (the GGUF file) for the "
-                     "SSD tier; all streamed blocks stay in RAM.")
         owner = object()
         log_info(f"DiT Layer Streaming: Registering Late Offload ({resident_k}/{len(blocks)} resident, {num_stream} "
                  f"streaming blocks, pin_memory={pin_memory}, double_buffer={double}, "
@@ -137,17 +134,18 @@ class WeightFerryDiT:
                 return
             _teardown(dit)                    # a previous capture of this model (or another config's)
             ram_blocks = None
-            if model_file and budget > 0:
+            if tier_auto and budget > 0:
                 per = sum(q.numel() * q.element_size() for q in blocks[resident_k].parameters())
                 ram_blocks = min(num_stream, int(math.floor(budget * 1024 ** 3 / max(1, per))))
             sm = dit_node.apply_streaming(dit, device=dev, resident_blocks=resident_k, prefetch_slots=prefetch_slots,
-                                          pin_memory=pin_memory, model_file=model_file if ram_blocks is not None
-                                          else None, ram_blocks=ram_blocks, double_buffer=double)
+                                          pin_memory=pin_memory, model_file=model_file or None, ram_blocks=ram_blocks,
+                                          double_buffer=double or (ram_blocks is not None and ram_blocks < num_stream))
             sm.owner_node = owner
             setattr(dit, _NODE_ATTR, sm)
             n_ssd = len(sm.state.disk_index)
+            src = model_file or (sm.state.disk_store.path if sm.state.disk_store is not None else "?")
             log_info(f"DiT Layer Streaming [Late Offload]: {num_stream} blocks offloaded ({num_stream - n_ssd} in "
-                     f"pinned RAM, {n_ssd} read from {model_file})." if n_ssd else
+                     f"pinned RAM, {n_ssd} read from {src})." if n_ssd else
                      f"DiT Layer Streaming [Late Offload]: {num_stream} blocks offloaded to pinned RAM.")
 
         def on_detach(p, unpatch_all=True, *args, **kwargs):

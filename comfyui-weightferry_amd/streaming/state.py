@@ -152,6 +152,10 @@ class _StreamState:
         if self.ring is not None:
             self.ring.close()
             self.ring = None
+        store = getattr(self, "disk_store", None)
+        if store is not None:
+            store.delete()
+            self.disk_store = None
         for h in self.handles:
             h.remove()
         self.handles = []

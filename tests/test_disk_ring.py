@@ -167,3 +167,43 @@ def test_pieces_larger_than_the_read_chunk(tmp_path, direct):
         consume(ring, source, data, 2)
     finally:
         ring.close()
+
+
+def test_cache_file_store_round_trip_and_stale_cleanup(tmp_path):
+    cf = sub("core.tiers.cache_files")
+    d = str(tmp_path / "cache")
+    os.makedirs(d)
+    dead = 4_194_301
+    while True:                                    # a pid that no process has
+        try:
+            os.kill(dead, 0)
+            dead -= 1
+        except ProcessLookupError:
+            break
+        except PermissionError:
+            dead -= 1
+    stale = os.path.join(d, f"wf_blocks_{dead}_0.bin")
+    mine = os.path.join(d, f"wf_blocks_{os.getpid()}_999.bin")
+    for p in (stale, mine):
+        open(p, "wb").write(b"x" * 10)
+    rng = np.random.default_rng(2)
+    block_bytes = 3 * 4096 + 123
+    store = cf.DiskBlockStore(d, block_bytes, 4)
+    assert not os.path.exists(stale) and os.path.exists(mine) and store.cleanup_freed == 10
+    data = [rng.integers(0, 256, block_bytes, dtype=np.uint8) for _ in range(4)]
+    for i, b in enumerate(data):
+        store.write_block(i, b)
+    store.finalize()
+    assert os.path.getsize(store.path) == 3 * store.stride + block_bytes and store.stride % 4096 == 0
+    ring = src.DiskRing(store.source(), depth=2, pin=False, threads=2, direct=True)
+    try:
+        for c in range(2):
+            for i in range(4):
+                v, s = ring.acquire(i)
+                assert np.array_equal(v.numpy(), data[i])
+                ring.release(s)
+    finally:
+        ring.close()
+    path = store.path
+    store.delete()
+    assert not os.path.exists(path)

@@ -102,3 +102,21 @@ def test_tiering_auto_reads_blocks_over_the_budget_from_the_file(native, comfy, 
     assert len(sm.state.disk_index) == 3        # 5 streamed blocks, 2 fit the RAM budget
     _check(mp, x, ctx, ref, times=3)
     mp.detach()
+
+
+def test_tiering_auto_without_a_model_file_uses_a_cache_file(native, comfy, reference, tmp_path, monkeypatch):
+    x, ctx, ref = reference
+    node = sub("streaming.node")
+    model = _stack()
+    per_block = sum(p.numel() * p.element_size() for p in model.blocks[1].parameters())
+    monkeypatch.delenv("WEIGHTFERRY_MODEL_FILE", raising=False)
+    monkeypatch.setenv("WEIGHTFERRY_CACHE_DIR", str(tmp_path / "cache"))
+    mp = node.WeightFerryDiT().apply_streaming(fake_comfy.FakeModelPatcher(model), resident_blocks=1,
+                                               tiering="Auto (GPU / RAM / SSD)",
+                                               ram_budget_gb=1.5 * per_block / 1024 ** 3)[0]
+    model.blocks[0].cuda()
+    mp.load()
+    sm = getattr(model, node._NODE_ATTR)
+    assert len(sm.state.disk_index) == 4 and sm.state.disk_store is not None
+    _check(mp, x, ctx, ref, times=2)
+    mp.detach()

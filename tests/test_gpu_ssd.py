@@ -136,3 +136,26 @@ def test_file_tensor_size_mismatch_is_rejected(native, tmp_path):
     gf.write_gguf(path, tensors, alignment=256)
     with pytest.raises(ValueError, match="bytes"):
         dn.apply_streaming(model, device="cuda", model_file=path, ram_blocks=0)
+
+
+def test_ssd_tier_from_a_cache_file(native, tmp_path):
+    dn = sub("streaming.dit_node")
+    x, ctx = _inputs()
+    with torch.no_grad():
+        ref = _stack().cuda()(x, ctx)
+    torch.cuda.synchronize()
+    model = _stack()
+    sm = dn.apply_streaming(model, device="cuda", prefetch_slots=2, profile=False, ram_blocks=2,
+                            ssd_dir=str(tmp_path / "cache"), ring_depth=2, ring_threads=2)
+    path = sm.state.disk_store.path
+    try:
+        assert len(sm.state.disk_index) == 4 and path.startswith(str(tmp_path))
+        for _ in range(3):
+            with torch.no_grad():
+                y = sm(x, ctx)
+            torch.cuda.synchronize()
+            assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+    finally:
+        sm.teardown()
+    import os
+    assert not os.path.exists(path)
