@@ -271,3 +271,33 @@ def test_pending_input_quantised_with_its_operation(native, kind):
                                     _bits(shift.reshape(B, K)), N, 1e-6)
     expect = lib.linear_i8(rq, w_q.numpy(), rs, ws.numpy(), out_dt=lib.BF16)
     assert np.array_equal(_bits(y.reshape(-1, 640)), expect)
+
+
+@pytest.mark.parametrize("N", [5000, 4992])
+def test_wide_tiles_bias_and_residual_whole_output(native, N):
+    # 4000 x N outputs take the 256 x 320 tiling (one round of 256 workgroups); N = 5000 leaves a partial last tile
+    # and an odd row length (element stores), N = 4992 whole 16-byte runs. Every element of the bias and the
+    # residual forms against the float32 epilogue in the kernel's order on an exact accumulator.
+    M, K, G = 4000, 512, 4
+    g = torch.Generator().manual_seed(N)
+    xq, wq = _rand_i8(g, (M, K)), _rand_i8(g, (N, K))
+    xs = torch.rand(M, generator=g) * 0.05 + 1e-3
+    ws = torch.rand(N, generator=g) * 0.002 + 1e-5
+    bias = torch.randn(N, generator=g).to(torch.bfloat16)
+    acc = (xq.double() @ wq.double().T).float()                   # exact: |acc| < 2^24 here
+    t = (acc * xs[:, None]) * ws[None, :]
+    out = gpu_linear(native, xq.cuda(), wq.cuda(), xs.cuda(), ws.cuda(), bias=bias.cuda()).cpu()
+    ref = (t + bias.float()[None, :]).to(torch.bfloat16)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    gate = torch.randn((G, N), generator=g).to(torch.bfloat16)
+    resid = torch.randn((M, N), generator=g).to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    d = {k: v.cuda() for k, v in dict(xq=xq, wq=wq, xs=xs, ws=ws, gate=gate, resid=resid).items()}
+    rc = native.lib().wf_linear_i8_residual(d["xq"].data_ptr(), d["wq"].data_ptr(), d["xs"].data_ptr(),
+                                            d["ws"].data_ptr(), d["gate"].data_ptr(), d["resid"].data_ptr(),
+                                            y.data_ptr(), M, N, K, M // G, native.stream_of(torch.device("cuda")))
+    assert rc == 0, native.last_error()
+    torch.cuda.synchronize()
+    gr = gate.float().repeat_interleave(M // G, dim=0)
+    ref_r = (resid.float() + gr * t).to(torch.bfloat16)
+    assert torch.equal(y.cpu().view(torch.int16), ref_r.view(torch.int16))
