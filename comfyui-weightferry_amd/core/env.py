@@ -19,6 +19,7 @@ DEFAULTS = {
     "WEIGHTFERRY_SSD_LAYOUT": None,        # "tail": the SSD tier is the last blocks (default: interleaved)
     "WEIGHTFERRY_MODEL_FILE": None,        # the GGUF file the SSD tier reads blocks from (else a cache file)
     "WEIGHTFERRY_CACHE_DIR": None,         # directory of the SSD tier's cache files (default: temp directory)
+    "WEIGHTFERRY_RAM_MARGIN_GB": "6",      # RAM kept free besides the RAM tier when its budget is automatic
 }
 
 

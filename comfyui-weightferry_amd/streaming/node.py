@@ -10,7 +10,8 @@ registers
     ON_LOAD (a clone switch).
 Block 0 stays resident (resident_blocks >= 1), as in the reference.
 
-Tiering "Auto" puts the streamed blocks over the RAM budget (``ram_budget_gb``; 0: all in RAM) on the SSD tier:
+Tiering "Auto" puts the streamed blocks over the RAM budget (``ram_budget_gb``; 0: the available RAM minus
+WEIGHTFERRY_RAM_MARGIN_GB, see core.tiers.plan.plan_tiers) on the SSD tier:
 read straight from the GGUF model file named by WEIGHTFERRY_MODEL_FILE (ComfyUI-GGUF's loaded tensors do not carry
 their file's path), or else from a cache file of their captured bytes (WEIGHTFERRY_CACHE_DIR). Options of the reference that belong to other paths -- SageAttention, fp8 storage format,
 self-managed residents, auto-configuration, the VRAM budget, chunk streaming -- are accepted and logged as not
@@ -133,13 +134,19 @@ class WeightFerryDiT:
             if not mm.is_device_cuda(dev):
                 return
             _teardown(dit)                    # a previous capture of this model (or another config's)
-            ram_blocks = None
-            if tier_auto and budget > 0:
+            ram_blocks, depth = None, 2
+            if tier_auto:
+                from ..core.tiers.plan import plan_tiers
                 per = sum(q.numel() * q.element_size() for q in blocks[resident_k].parameters())
-                ram_blocks = min(num_stream, int(math.floor(budget * 1024 ** 3 / max(1, per))))
+                plan = plan_tiers(num_stream, per, ram_budget_bytes=int(budget * 1024 ** 3) if budget > 0 else None)
+                ram_blocks, depth = plan["ram_blocks"], max(2, plan["ring_depth"])
+                log_info(f"DiT Layer Streaming [tiers]: RAM budget {plan['budget'] / 1024 ** 3:.1f} GB: "
+                         f"{plan['ram_blocks']} blocks in RAM, {plan['disk_blocks']} on the SSD tier"
+                         + (f" (ring of {plan['ring_depth']})." if plan["disk_blocks"] else "."))
             sm = dit_node.apply_streaming(dit, device=dev, resident_blocks=resident_k, prefetch_slots=prefetch_slots,
                                           pin_memory=pin_memory, model_file=model_file or None, ram_blocks=ram_blocks,
-                                          double_buffer=double or (ram_blocks is not None and ram_blocks < num_stream))
+                                          double_buffer=double or (ram_blocks is not None and ram_blocks < num_stream),
+                                          ring_depth=depth, ring_threads=2)
             sm.owner_node = owner
             setattr(dit, _NODE_ATTR, sm)
             n_ssd = len(sm.state.disk_index)

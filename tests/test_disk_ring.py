@@ -207,3 +207,24 @@ def test_cache_file_store_round_trip_and_stale_cleanup(tmp_path):
     path = store.path
     store.delete()
     assert not os.path.exists(path)
+
+
+def test_plan_tiers():
+    GB = 1 << 30
+    p = plan.plan_tiers(40, GB // 5, ram_budget_bytes=100 * GB)
+    assert p == {"ram_blocks": 40, "disk_blocks": 0, "ring_depth": 0, "budget": 100 * GB, "ssd_bound": False}
+    # 4 GB for 200 MB blocks: a ring of 4 (default) takes 0.8 GB, 16 blocks fit in the rest
+    p = plan.plan_tiers(40, 200 << 20, ram_budget_bytes=4 * GB)
+    assert p["ring_depth"] == 4 and p["ram_blocks"] == (4 * GB - 4 * (200 << 20)) // (200 << 20) == 16
+    assert p["disk_blocks"] == 24
+    # the ring covers one read with compute: 200 MB at 5 GB/s = 42 ms over 4 ms of compute -> 8 (the cap)
+    p = plan.plan_tiers(40, 200 << 20, ram_budget_bytes=4 * GB, disk_gbps=5.0, compute_ms_per_block=4.0)
+    assert p["ring_depth"] == 8 and p["ssd_bound"]
+    p = plan.plan_tiers(40, 200 << 20, ram_budget_bytes=4 * GB, disk_gbps=5.0, compute_ms_per_block=40.0)
+    assert p["ring_depth"] == 4 and not p["ssd_bound"]
+    # a budget below the ring: depth drops to 2, nothing in RAM
+    p = plan.plan_tiers(40, 200 << 20, ram_budget_bytes=300 << 20)
+    assert p["ring_depth"] == 2 and p["ram_blocks"] == 0 and p["disk_blocks"] == 40
+    # automatic budget: the available RAM minus the margin
+    p = plan.plan_tiers(2, 1, ram_margin_bytes=0)
+    assert p["ram_blocks"] == 2

@@ -84,39 +84,48 @@ def test_skipped_on_load_captures_lazily(native, comfy, reference):
     mp.detach()
 
 
-def test_tiering_auto_reads_blocks_over_the_budget_from_the_file(native, comfy, reference, tmp_path, monkeypatch):
-    x, ctx, ref = reference
+def _reference10():
+    x, ctx = _inputs()
+    with torch.no_grad():
+        ref = _stack(n=10).cuda()(x, ctx)
+    torch.cuda.synchronize()
+    return x, ctx, ref
+
+
+def test_tiering_auto_reads_blocks_over_the_budget_from_the_file(native, comfy, tmp_path, monkeypatch):
+    x, ctx, ref = _reference10()
     node = sub("streaming.node")
     syn = sub("streaming.synthetic")
-    model = _stack()
-    path = str(tmp_path / "wan6.gguf")
+    model = _stack(n=10)
+    path = str(tmp_path / "wan10.gguf")
     syn.write_gguf_model(model, path)
     per_block = sum(p.numel() * p.element_size() for p in model.blocks[1].parameters())
     monkeypatch.setenv("WEIGHTFERRY_MODEL_FILE", path)
     mp = node.WeightFerryDiT().apply_streaming(fake_comfy.FakeModelPatcher(model), resident_blocks=1,
                                                tiering="Auto (GPU / RAM / SSD)",
-                                               ram_budget_gb=2.5 * per_block / 1024 ** 3)[0]
+                                               ram_budget_gb=6.5 * per_block / 1024 ** 3)[0]
     model.blocks[0].cuda()
     mp.load()
     sm = getattr(model, node._NODE_ATTR)
-    assert len(sm.state.disk_index) == 3        # 5 streamed blocks, 2 fit the RAM budget
+    # 9 streamed blocks; the budget holds the ring (4 buffers) and 2 blocks
+    assert len(sm.state.disk_index) == 7 and sm.state.ring.depth == 4
     _check(mp, x, ctx, ref, times=3)
     mp.detach()
 
 
-def test_tiering_auto_without_a_model_file_uses_a_cache_file(native, comfy, reference, tmp_path, monkeypatch):
-    x, ctx, ref = reference
+def test_tiering_auto_without_a_model_file_uses_a_cache_file(native, comfy, tmp_path, monkeypatch):
+    x, ctx, ref = _reference10()
     node = sub("streaming.node")
-    model = _stack()
+    model = _stack(n=10)
     per_block = sum(p.numel() * p.element_size() for p in model.blocks[1].parameters())
     monkeypatch.delenv("WEIGHTFERRY_MODEL_FILE", raising=False)
     monkeypatch.setenv("WEIGHTFERRY_CACHE_DIR", str(tmp_path / "cache"))
     mp = node.WeightFerryDiT().apply_streaming(fake_comfy.FakeModelPatcher(model), resident_blocks=1,
                                                tiering="Auto (GPU / RAM / SSD)",
-                                               ram_budget_gb=1.5 * per_block / 1024 ** 3)[0]
+                                               ram_budget_gb=5.5 * per_block / 1024 ** 3)[0]
     model.blocks[0].cuda()
     mp.load()
     sm = getattr(model, node._NODE_ATTR)
-    assert len(sm.state.disk_index) == 4 and sm.state.disk_store is not None
+    assert len(sm.state.disk_index) == 8 and sm.state.disk_store is not None     # ring of 4 and 1 block in RAM
     _check(mp, x, ctx, ref, times=2)
     mp.detach()
