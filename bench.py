@@ -8,6 +8,8 @@ the timed region; each step works on the next of four copies of inputs and outpu
 
 Other rows of the workload list are reported under "also":
   * Q8_0 dequantisation of a 5120 x 5120 weight (MID float16 and float32);
+  * every other GGML format at 5120 x 5120 -> bf16 (MID float16): Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q5_K / Q6_K encoded
+    from the same N(0, 0.02) weights, Q2_K / Q3_K as random blocks with typical float16 scales;
   * the int8 W8A8 linear at M in {1024, 4096, 16384}, K = 5120, N in {5120, 13824} (per-token int8 activations,
     per-channel int8 weights, int32 accumulation, bf16 out), and the row quantiser;
   * fused Q5_K / Q6_K dequant + bf16 GEMM over the linears of one Wan-2.1-14B block at 4096 tokens, next to the
@@ -20,7 +22,7 @@ Other rows of the workload list are reported under "also":
     streamed forward with half the blocks read from the file on every step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--only-headline] [--legs LEGS]
---legs (comma list of headline, lora, int8, fused, streaming, ssd; default all) runs only those legs, for profiling one
+--legs (comma list of headline, formats, lora, int8, fused, streaming, ssd; default all) runs only those legs, for profiling one
 kernel family; without the headline leg the printed line holds the legs' figures only.
 """
 import argparse
@@ -34,6 +36,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 PKG = "comfyui-weightferry_amd"
 HBM_PEAK_GBS = 8000.0
 ROTATE = 4
+ROTATE_BYTES = 1_200_000_000
 
 
 def _args():
@@ -43,10 +46,11 @@ def _args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true", help="leave out the CPU baseline leg")
     ap.add_argument("--only-headline", action="store_true", help="the Q4_K dequant leg only")
-    ap.add_argument("--legs", default="all", help="comma list: headline, lora, int8, fused, streaming, ssd")
+    ap.add_argument("--legs", default="all", help="comma list: headline, formats, lora, int8, fused, streaming, ssd")
     a = ap.parse_args()
     a.legs = {"headline"} if a.only_headline else (
-        {"headline", "lora", "int8", "fused", "streaming", "ssd"} if a.legs == "all" else set(a.legs.split(",")))
+        {"headline", "formats", "lora", "int8", "fused", "streaming", "ssd"} if a.legs == "all"
+        else set(a.legs.split(",")))
     return a
 
 
@@ -267,15 +271,18 @@ def lora_leg(torch, native, raw, shape, steps=20):
 def dequant_leg(torch, native, raws, shapes, qtype, mid, out_dt, steps, warmup):
     """Time `steps` steps of dequantising every matrix once, launched back to back on torch's current stream with
     events at both ends of the timed region on that stream. Returns (ms per step, mean ms per launch, bytes/step);
-    the launches are all of one kernel, so the mean per launch is that kernel's average duration."""
+    the launches are all of one kernel, so the mean per launch is that kernel's average duration. Steps cycle over
+    at least ROTATE copies of inputs and outputs and at least ROTATE_BYTES in all, so the last-level cache (256 MB)
+    cannot serve one step's bytes to a later one."""
     lib = native.lib()
     dev = torch.device("cuda:0")
     stream = native.stream_of(dev)
     out_torch = {0: torch.float16, 1: torch.bfloat16, 2: torch.float32}[out_dt]
-    ins = [[torch.from_numpy(r).to(dev) for r in raws] for _ in range(ROTATE)]
-    outs = [[torch.empty(s, dtype=out_torch, device=dev) for s in shapes] for _ in range(ROTATE)]
     nvals = [s[0] * s[1] for s in shapes]
-    algo = sum(r.size for r in raws) + sum(n * outs[0][0].element_size() for n in nvals)
+    algo = sum(r.size for r in raws) + sum(n * torch.empty((), dtype=out_torch).element_size() for n in nvals)
+    rot = max(ROTATE, -(-ROTATE_BYTES // algo))
+    ins = [[torch.from_numpy(r).to(dev) for r in raws] for _ in range(rot)]
+    outs = [[torch.empty(s, dtype=out_torch, device=dev) for s in shapes] for _ in range(rot)]
 
     def launch(r, m):
         rc = lib.wf_dequant(ins[r][m].data_ptr(), ins[r][m].numel(), qtype, mid, out_dt, outs[r][m].data_ptr(),
@@ -285,19 +292,40 @@ def dequant_leg(torch, native, raws, shapes, qtype, mid, out_dt, steps, warmup):
 
     for i in range(warmup):
         for m in range(len(shapes)):
-            launch(i % ROTATE, m)
+            launch(i % rot, m)
     torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record()
     for i in range(steps):
         for m in range(len(shapes)):
-            launch(i % ROTATE, m)
+            launch(i % rot, m)
     t1.record()
     torch.cuda.synchronize()
     ms_step = t0.elapsed_time(t1) / steps
     del ins, outs
     torch.cuda.empty_cache()
     return ms_step, ms_step / len(shapes), algo
+
+
+FORMATS = ((2, "q4_0"), (3, "q4_1"), (6, "q5_0"), (7, "q5_1"), (13, "q5_k"), (14, "q6_k"), (10, "q2_k"),
+           (11, "q3_k"))
+
+
+def formats_leg(torch, native, encode, steps, warmup):
+    """Dequantisation of one 5120 x 5120 weight in each remaining GGML format -> bf16 (MID float16): GB/s of the
+    algorithmic bytes (blocks in + bf16 out) over the mean launch, and the fraction of the HBM peak."""
+    shape = (5120, 5120)
+    w = encode.weights(shape, seed=1234)
+    res = {}
+    for qt, name in FORMATS:
+        if qt in encode.ENCODERS:
+            raw = encode.encode(w, qt)
+        else:
+            raw = encode.random_blocks(qt, shape[0] * shape[1] // encode.PER_BLOCK[qt], seed=1234)
+        _, k, a = dequant_leg(torch, native, [raw], [shape], qt, 0, 1, steps, warmup)
+        res[name] = {"GB/s": round(a / (k / 1e3) / 1e9, 1), "kernel_us": round(k * 1e3, 2),
+                     "frac": round(a / (k / 1e3) / 1e9 / HBM_PEAK_GBS, 3), "bytes": a}
+    return res
 
 
 def cpu_baseline_dequant(torch, raw, qtype, rows, cols, budget_s=12.0):
@@ -364,6 +392,8 @@ def main():
         raws = [encode.encode_q4_k(encode.weights(s, seed=1234 + i)) for i, s in enumerate(shapes)]
         _log(f"encoded Q4_K pair in {time.perf_counter() - t:.1f} s")
     if "headline" not in args.legs:
+        if "formats" in args.legs:
+            also["dequant_formats_5120sq"] = formats_leg(torch, native, encode, args.steps, args.warmup)
         if "lora" in args.legs:
             also["lora_add_q4_k_13824x5120"] = lora_leg(torch, native, raws[0], shapes[0])
         if "int8" in args.legs:
@@ -407,6 +437,9 @@ def main():
         ms8, k8, a8 = dequant_leg(torch, native, q8, [(5120, 5120)], 8, mid, 1, args.steps, args.warmup)
         also[name] = {"GB/s": round(a8 / (k8 / 1e3) / 1e9, 1), "kernel_us": round(k8 * 1e3, 2),
                       "frac": round(a8 / (k8 / 1e3) / 1e9 / HBM_PEAK_GBS, 3), "bytes": a8}
+    if "formats" in args.legs:
+        also["dequant_formats_5120sq"] = formats_leg(torch, native, encode, args.steps, args.warmup)
+        _log("formats leg done")
     if "lora" in args.legs:
         also["lora_add_q4_k_13824x5120"] = lora_leg(torch, native, raws[0], shapes[0])
         _log("lora leg done")

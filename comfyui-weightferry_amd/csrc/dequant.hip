@@ -354,68 +354,238 @@ struct Q6_K {
     }
 };
 
-// ----------------------------------------------------------------------------- other formats (byte gathers)
-// The legacy formats Q4_0 / Q4_1 / Q5_0 / Q5_1 and the K-quants Q2_K / Q3_K: one lane per 8 values, the
-// reference's per-value formulas with byte loads (enhancers/gguf_dequant.py:136-167,225-249).
+// ------------------------------------------------------------------------------------ format constants
+// Legacy formats: block bytes TS, quant bytes at QS, high bits at QH (Q5_x), min at 2 (HAS_M), quant offset SUB
+// (enhancers/gguf_dequant.py:52-56).
 template <int QT>
 struct Fmt;
 template <> struct Fmt<2> { static constexpr int TS = 18, PER = 32, HAS_M = 0, QH = -1, QS = 2, SUB = 8; };
 template <> struct Fmt<3> { static constexpr int TS = 20, PER = 32, HAS_M = 1, QH = -1, QS = 4, SUB = 0; };
 template <> struct Fmt<6> { static constexpr int TS = 22, PER = 32, HAS_M = 0, QH = 2, QS = 6, SUB = 16; };
 template <> struct Fmt<7> { static constexpr int TS = 24, PER = 32, HAS_M = 1, QH = 4, QS = 8, SUB = 0; };
-template <> struct Fmt<10> { static constexpr int TS = 84, PER = 256; };
-template <> struct Fmt<11> { static constexpr int TS = 110, PER = 256; };
 
-__device__ __forceinline__ float ld_f16(const uint8_t* p) {
-    return f16_bits_to_f32((uint32_t)p[0] | ((uint32_t)p[1] << 8));
-}
-
-template <int QT, int MID>
-__device__ __forceinline__ float deq_value(const uint8_t* b, int v) {
-    if constexpr (QT == 2 || QT == 3 || QT == 6 || QT == 7) {
-        using F = Fmt<QT>;
-        const float d = round_to<MID>(ld_f16(b));
-        int nib = (b[F::QS + (v & 15)] >> ((v >> 4) * 4)) & 0xF;
-        if constexpr (F::QH >= 0) nib |= ((b[F::QH + (v >> 3)] >> (v & 7)) & 1) << 4;
-        float x = round_to<MID>(d * (float)(nib - F::SUB));
-        if constexpr (F::HAS_M) x = round_to<MID>(x + round_to<MID>(ld_f16(b + 2)));
-        return x;
-    } else if constexpr (QT == 11) {
-        const int i = v >> 4;
-        const int ls = (b[96 + (i & 7)] >> ((i >> 3) * 4)) & 0xF;
-        const int hs = (b[104 + (i & 3)] >> ((i >> 2) * 2)) & 3;
-        const int sc = (ls | (hs << 4)) - 32;
-        const float d = round_to<MID>(round_to<MID>(ld_f16(b + 108)) * (float)sc);
-        const int r = v & 127;
-        const int ql = (b[32 + (v >> 7) * 32 + (r & 31)] >> ((r >> 5) * 2)) & 3;
-        const int hb = ((b[v & 31] >> (v >> 5)) & 1) ^ 1;
-        return round_to<MID>(d * (float)(ql - (hb << 2)));
-    } else {  // Q2_K
-        const int sb = b[v >> 4];
-        const float dl = round_to<MID>(round_to<MID>(ld_f16(b + 80)) * (float)(sb & 0xF));
-        const float ml = round_to<MID>(round_to<MID>(ld_f16(b + 82)) * (float)(sb >> 4));
-        const int r = v & 127;
-        const int q = (b[16 + (v >> 7) * 32 + (r & 31)] >> ((r >> 5) * 2)) & 3;
-        return round_to<MID>(round_to<MID>(dl * (float)q) - ml);
+// ------------------------------------------------------------------------- Q4_0 / Q4_1 / Q5_0 / Q5_1 (tiled)
+// Q4_0 (18 B): d @0, qs[16] @2. Q4_1 (20 B): d @0, m @2, qs @4. Q5_0 (22 B): d @0, qh[4] @2, qs @6. Q5_1 (24 B):
+// d @0, m @2, qh[4] @4, qs @8. Value v of a block is nibble v / 16 of qs[v % 16]; Q5_x adds bit v of qh (read as a
+// little-endian dword) as bit 4; q = nib - SUB (Q4_0: 8, Q5_0: 16, else 0). x = MID(MID(d) * q), then
+// x = MID(x + MID(m)) for Q4_1 / Q5_1 (enhancers/gguf_dequant.py:145-160). Lane-item c (4 per block) writes values
+// [8c, 8c + 8): nibble c / 2 of qs bytes [8(c % 2), +8) and the high bits of qh byte c, so a wave's store is 16 whole
+// blocks of output (1 KiB for a 2-byte OUT). Blocks of 18 and 22 bytes are only 2-byte aligned: their quants are
+// read as aligned dwords and funnel-shifted (load8_a2); Q4_1's are dword-aligned and Q5_1's 8-byte aligned.
+template <int QT, int MID, int OUT>
+struct Legacy {
+    using F = Fmt<QT>;
+    static constexpr int LANES_PER_BLOCK = 4, TS = F::TS, PER = 32, OUT_BYTES = OUT == WF_F32 ? 4 : 2;
+    struct Raw { uint32_t dm, qh; uint2 q; };
+    static __device__ __forceinline__ Raw load(const uint8_t* src, uint32_t t) {
+        const uint32_t blk = t >> 2, c = t & 3;
+        const uint32_t b = blk * TS;
+        const uint32_t o = b + F::QS + 8 * (c & 1);
+        Raw r;
+        if constexpr (F::HAS_M) r.dm = *reinterpret_cast<const uint32_t*>(src + b);     // TS 20 / 24: aligned
+        else r.dm = *reinterpret_cast<const uint16_t*>(src + b);
+        if constexpr (F::QH >= 0) r.qh = src[b + F::QH + c];
+        else r.qh = 0;
+        if constexpr (TS % 8 == 0) {
+            r.q = *reinterpret_cast<const uint2*>(src + o);
+        } else if constexpr (TS % 4 == 0) {
+            const uint32_t* p = reinterpret_cast<const uint32_t*>(src + o);
+            r.q = make_uint2(p[0], p[1]);
+        } else {
+            r.q = load8_a2(src, o);
+        }
+        return r;
     }
-}
-
-template <int QT, int MID, int OUT, bool ADD>
-__global__ __launch_bounds__(256) void deq_gather(const uint8_t* __restrict__ src, void* __restrict__ out,
-                                                  int64_t nlanes, const float* __restrict__ diff, float sa) {
-    constexpr int TS = Fmt<QT>::TS, PER = Fmt<QT>::PER, LPB = PER / 8;
-    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < nlanes;
-         t += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t blk = t / LPB;
-        const int v0 = (int)(t % LPB) * 8;
-        const uint8_t* b = src + blk * TS;
-        float v[8];
+    template <class S>
+    static __device__ __forceinline__ void emit(const S& o, uint32_t t, const Raw& r) {
+        const uint32_t c = t & 3;
+        const uint32_t ns = 4u * (c >> 1);
+        uint32_t n[2];
+        n[0] = (r.q.x >> ns) & 0x0f0f0f0fu;
+        n[1] = (r.q.y >> ns) & 0x0f0f0f0fu;
+        if constexpr (F::QH >= 0) {
+            // bit i of the qh byte -> bit 4 of byte i: the four shifted copies of a 4-bit value x in
+            // x * (1 + 2^7 + 2^14 + 2^21) do not overlap, so bit i lands alone on bit 8i
+            n[0] |= (((r.qh & 0xfu) * 0x00204081u) & 0x01010101u) << 4;
+            n[1] |= (((r.qh >> 4) * 0x00204081u) & 0x01010101u) << 4;
+        }
+        const uint32_t e0 = t * 8;
+        if constexpr (MID == WF_F16) {
+            const uint32_t dbits = r.dm & 0xffffu;
+            const h2 d2 = as_h2(dbits | (dbits << 16));
+            const h2 bias = h2s(-1024.0f - (float)F::SUB);
+            h2 v[4];
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = deq_value<QT, MID>(b, v0 + i);
-        if constexpr (ADD) AddDiff{out, diff, sa}.template put<OUT>(t * 8, v);
-        else store8<OUT>(out, t * 8, v);
+            for (int w = 0; w < 2; w++) {
+                v[2 * w] = d2 * (biased_lo(n[w]) + bias);
+                v[2 * w + 1] = d2 * (biased_hi(n[w]) + bias);
+            }
+            if constexpr (F::HAS_M) {
+                const uint32_t mbits = r.dm >> 16;
+                const h2 m2 = as_h2(mbits | (mbits << 16));
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] = v[i] + m2;
+            }
+            o.template puth<OUT>(e0, v);
+        } else {
+            const float d = round_to<MID>(f16_bits_to_f32(r.dm & 0xffffu));
+            float v[8];
+#pragma unroll
+            for (int w = 0; w < 2; w++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    v[4 * w + i] = round_to<MID>(d * (float)((int)byte_of(n[w], i) - F::SUB));
+            if constexpr (F::HAS_M) {
+                const float m = round_to<MID>(f16_bits_to_f32(r.dm >> 16));
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] = round_to<MID>(v[i] + m);
+            }
+            o.template put<OUT>(e0, v);
+        }
     }
-}
+};
+
+// ------------------------------------------------------------------------------------------------- Q2_K
+// 84 B: scales[16] @0 (low nibble: scale, high nibble: min of 16-value sub-block i), qs[64] @16, d @80, dmin @82.
+// Value v: q = (qs[32(v / 128) + v % 32] >> 2((v % 128) / 32)) & 3, dl = MID(MID(d) * (s[v / 16] & 15)),
+// ml = MID(MID(dmin) * (s[v / 16] >> 4)), x = MID(MID(dl * q) - ml) (enhancers/gguf_dequant.py:237-246).
+// Lane-item j (16 per super-block) writes values [8j, 8j + 8) and [128 + 8j, +8): qs bytes [8(j % 4), +8) and
+// [32 + 8(j % 4), +8) at shift 2(j / 4), scale bytes j / 2 and 8 + j / 2.
+template <int MID, int OUT>
+struct Q2_K {
+    static constexpr int LANES_PER_BLOCK = 16, TS = 84, PER = 256, OUT_BYTES = OUT == WF_F32 ? 4 : 2;
+    struct Raw { uint2 q1, q2; uint32_t dd, s1, s2; };
+    static __device__ __forceinline__ Raw load(const uint8_t* src, uint32_t t) {
+        const uint32_t sb = t >> 4, j = t & 15;
+        const uint32_t b0 = sb * 84;                           // dword-aligned
+        const uint32_t* q = reinterpret_cast<const uint32_t*>(src + b0 + 16 + 8 * (j & 3));
+        Raw r;
+        r.q1 = make_uint2(q[0], q[1]);
+        r.q2 = make_uint2(q[8], q[9]);
+        r.dd = *reinterpret_cast<const uint32_t*>(src + b0 + 80);
+        r.s1 = src[b0 + (j >> 1)];
+        r.s2 = src[b0 + 8 + (j >> 1)];
+        return r;
+    }
+    template <class S>
+    static __device__ __forceinline__ void emit(const S& o, uint32_t t, const Raw& r) {
+        const uint32_t sb = t >> 4, j = t & 15;
+        const uint32_t sh = 2u * (j >> 2);
+        uint32_t n1[2], n2[2];
+        n1[0] = (r.q1.x >> sh) & 0x03030303u; n1[1] = (r.q1.y >> sh) & 0x03030303u;
+        n2[0] = (r.q2.x >> sh) & 0x03030303u; n2[1] = (r.q2.y >> sh) & 0x03030303u;
+        const uint32_t e1 = sb * 256 + 8 * j, e2 = e1 + 128;
+        if constexpr (MID == WF_F16) {
+            const h2 dd = as_h2(r.dd);                          // (d, dmin)
+            const h2 off = h2s(-1024.0f);
+            // (scale, min) as float16 pairs through the exponent trick, then (d * scale, dmin * min) rounded to f16
+            const h2 p1 = dd * (as_h2((r.s1 & 15u) | ((r.s1 >> 4) << 16) | 0x64006400u) + off);
+            const h2 p2 = dd * (as_h2((r.s2 & 15u) | ((r.s2 >> 4) << 16) | 0x64006400u) + off);
+            const h2 dl1 = lo2(p1), ml1 = hi2(p1), dl2 = lo2(p2), ml2 = hi2(p2);
+            h2 v1[4], v2[4];
+#pragma unroll
+            for (int w = 0; w < 2; w++) {
+                v1[2 * w] = dl1 * (biased_lo(n1[w]) + off) - ml1;
+                v1[2 * w + 1] = dl1 * (biased_hi(n1[w]) + off) - ml1;
+                v2[2 * w] = dl2 * (biased_lo(n2[w]) + off) - ml2;
+                v2[2 * w + 1] = dl2 * (biased_hi(n2[w]) + off) - ml2;
+            }
+            o.template puth<OUT>(e1, v1);
+            o.template puth<OUT>(e2, v2);
+        } else {
+            const float d = round_to<MID>(f16_bits_to_f32(r.dd & 0xffffu));
+            const float dmin = round_to<MID>(f16_bits_to_f32(r.dd >> 16));
+            const float dl1 = round_to<MID>(d * (float)(r.s1 & 15u)), ml1 = round_to<MID>(dmin * (float)(r.s1 >> 4));
+            const float dl2 = round_to<MID>(d * (float)(r.s2 & 15u)), ml2 = round_to<MID>(dmin * (float)(r.s2 >> 4));
+            float v1[8], v2[8];
+#pragma unroll
+            for (int w = 0; w < 2; w++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    v1[4 * w + i] = round_to<MID>(round_to<MID>(dl1 * (float)byte_of(n1[w], i)) - ml1);
+                    v2[4 * w + i] = round_to<MID>(round_to<MID>(dl2 * (float)byte_of(n2[w], i)) - ml2);
+                }
+            o.template put<OUT>(e1, v1);
+            o.template put<OUT>(e2, v2);
+        }
+    }
+};
+
+// ------------------------------------------------------------------------------------------------- Q3_K
+// 110 B: hmask[32] @0, qs[64] @32, scales[12] @96, d @108. Value v, sub-block i = v / 16: sc = (low 4 bits from
+// scale byte i % 8 at nibble i / 8) | (2 high bits from byte 8 + i % 4 at shift 2(i / 4)) << 4, minus 32;
+// d' = MID(MID(d) * sc); q = ((qs[32(v / 128) + v % 32] >> 2((v % 128) / 32)) & 3) - 4 * (1 - bit v / 32 of
+// hmask[v % 32]); x = MID(d' * q) (enhancers/gguf_dequant.py:225-236). Lane-item j (16 per super-block) writes values
+// [8j, 8j + 8) and [128 + 8j, +8): hmask and qs bytes [8(j % 4), +8) (qs also [32 + 8(j % 4), +8)) at shift
+// 2(j / 4) (hmask bits j / 4 and 4 + j / 4), sub-blocks j / 2 and 8 + j / 2. The 3-bit code (ql | hbit << 2) enters
+// float16 as 1024 + code, and 1028 is subtracted.
+template <int MID, int OUT>
+struct Q3_K {
+    static constexpr int LANES_PER_BLOCK = 16, TS = 110, PER = 256, OUT_BYTES = OUT == WF_F32 ? 4 : 2;
+    struct Raw { uint2 hm, q1, q2; uint32_t ls, hs, d; };
+    static __device__ __forceinline__ Raw load(const uint8_t* src, uint32_t t) {
+        const uint32_t sb = t >> 4, j = t & 15;
+        const uint32_t b0 = sb * 110;                          // 2-byte aligned
+        const uint32_t c = 8 * (j & 3);
+        Raw r;
+        r.hm = load8_a2(src, b0 + c);
+        r.q1 = load8_a2(src, b0 + 32 + c);
+        r.q2 = load8_a2(src, b0 + 64 + c);
+        r.ls = src[b0 + 96 + (j >> 1)];
+        r.hs = src[b0 + 104 + ((j >> 1) & 3)];
+        r.d = *reinterpret_cast<const uint16_t*>(src + b0 + 108);
+        return r;
+    }
+    template <class S>
+    static __device__ __forceinline__ void emit(const S& o, uint32_t t, const Raw& r) {
+        const uint32_t sb = t >> 4, j = t & 15;
+        const uint32_t sh = 2u * (j >> 2), hb = j >> 2;
+        const uint32_t hsh = 2u * ((j >> 1) >> 2);             // 2 * (sub-block / 4) for sub-block j / 2
+        // sub-block j / 2: low nibble of ls, bits hsh of hs; sub-block 8 + j / 2: high nibble, bits hsh + 4
+        const int sc1 = (int)((r.ls & 15u) | (((r.hs >> hsh) & 3u) << 4)) - 32;
+        const int sc2 = (int)((r.ls >> 4) | (((r.hs >> (hsh + 4)) & 3u) << 4)) - 32;
+        uint32_t c1[2], c2[2];
+#pragma unroll
+        for (int w = 0; w < 2; w++) {
+            const uint32_t hm = w ? r.hm.y : r.hm.x;
+            const uint32_t qa = w ? r.q1.y : r.q1.x, qb = w ? r.q2.y : r.q2.x;
+            c1[w] = ((qa >> sh) & 0x03030303u) | (((hm >> hb) & 0x01010101u) << 2);
+            c2[w] = ((qb >> sh) & 0x03030303u) | (((hm >> (hb + 4)) & 0x01010101u) << 2);
+        }
+        const uint32_t e1 = sb * 256 + 8 * j, e2 = e1 + 128;
+        if constexpr (MID == WF_F16) {
+            const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)r.d);
+            h2 dd; dd[0] = d; dd[1] = d;
+            h2 sc; sc[0] = (_Float16)(float)sc1; sc[1] = (_Float16)(float)sc2;
+            const h2 pd = dd * sc;                               // (d * sc1, d * sc2), rounded to f16
+            const h2 dA = lo2(pd), dB = hi2(pd);
+            const h2 bias = h2s(-1028.0f);                       // 1024 + 4
+            h2 v1[4], v2[4];
+#pragma unroll
+            for (int w = 0; w < 2; w++) {
+                v1[2 * w] = dA * (biased_lo(c1[w]) + bias);
+                v1[2 * w + 1] = dA * (biased_hi(c1[w]) + bias);
+                v2[2 * w] = dB * (biased_lo(c2[w]) + bias);
+                v2[2 * w + 1] = dB * (biased_hi(c2[w]) + bias);
+            }
+            o.template puth<OUT>(e1, v1);
+            o.template puth<OUT>(e2, v2);
+        } else {
+            const float d = round_to<MID>(f16_bits_to_f32(r.d));
+            const float dA = round_to<MID>(d * (float)sc1), dB = round_to<MID>(d * (float)sc2);
+            float v1[8], v2[8];
+#pragma unroll
+            for (int w = 0; w < 2; w++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    v1[4 * w + i] = round_to<MID>(dA * (float)((int)byte_of(c1[w], i) - 4));
+                    v2[4 * w + i] = round_to<MID>(dB * (float)((int)byte_of(c2[w], i) - 4));
+                }
+            o.template put<OUT>(e1, v1);
+            o.template put<OUT>(e2, v2);
+        }
+    }
+};
 
 // out = OUT(out + OUT(diff * sa)) on n values already in out: the reference's _deq_add with DEQ off (a K-quant
 // dequantised by its own kernel first, or the second and later LoRAs, enhancers/gguf_dequant.py:387-409). Lane t
@@ -468,7 +638,7 @@ struct Launch {
     dim3 grid;
 };
 
-// grid of the byte-gather kernels (grid-stride loops: at most 2^20 workgroups)
+// grid of the grid-stride add kernel (at most 2^20 workgroups)
 static Launch plan(int64_t nlanes) {
     int64_t wgs = (nlanes + 255) / 256;
     if (wgs > (1 << 20)) wgs = 1 << 20;
@@ -485,12 +655,6 @@ static void launch_items(const uint8_t* src, void* out, int64_t nblocks, const f
     deq_items<F, ADD><<<dim3((unsigned)wgs), 256, 0, s>>>(src, out, nlanes, diff, sa);
 }
 
-template <int QT, int MID, int OUT, bool ADD>
-static void launch_gather(const uint8_t* src, void* out, int64_t nblocks, const float* diff, float sa, hipStream_t s) {
-    const Launch L = plan(nblocks * (Fmt<QT>::PER / 8));
-    deq_gather<QT, MID, OUT, ADD><<<L.grid, 256, 0, s>>>(src, out, L.nlanes, diff, sa);
-}
-
 template <int MID, int OUT, bool ADD>
 static void launch_fmt(int qtype, const uint8_t* src, void* out, int64_t nblocks, const float* diff, float sa,
                        hipStream_t s) {
@@ -499,12 +663,12 @@ static void launch_fmt(int qtype, const uint8_t* src, void* out, int64_t nblocks
     case 12: launch_items<Q45_K<12, MID, OUT>, ADD>(src, out, nblocks, diff, sa, s); break;
     case 13: launch_items<Q45_K<13, MID, OUT>, ADD>(src, out, nblocks, diff, sa, s); break;
     case 14: launch_items<Q6_K<MID, OUT>, ADD>(src, out, nblocks, diff, sa, s); break;
-    case 2: launch_gather<2, MID, OUT, ADD>(src, out, nblocks, diff, sa, s); break;
-    case 3: launch_gather<3, MID, OUT, ADD>(src, out, nblocks, diff, sa, s); break;
-    case 6: launch_gather<6, MID, OUT, ADD>(src, out, nblocks, diff, sa, s); break;
-    case 7: launch_gather<7, MID, OUT, ADD>(src, out, nblocks, diff, sa, s); break;
-    case 10: launch_gather<10, MID, OUT, ADD>(src, out, nblocks, diff, sa, s); break;
-    case 11: launch_gather<11, MID, OUT, ADD>(src, out, nblocks, diff, sa, s); break;
+    case 2: launch_items<Legacy<2, MID, OUT>, ADD>(src, out, nblocks, diff, sa, s); break;
+    case 3: launch_items<Legacy<3, MID, OUT>, ADD>(src, out, nblocks, diff, sa, s); break;
+    case 6: launch_items<Legacy<6, MID, OUT>, ADD>(src, out, nblocks, diff, sa, s); break;
+    case 7: launch_items<Legacy<7, MID, OUT>, ADD>(src, out, nblocks, diff, sa, s); break;
+    case 10: launch_items<Q2_K<MID, OUT>, ADD>(src, out, nblocks, diff, sa, s); break;
+    case 11: launch_items<Q3_K<MID, OUT>, ADD>(src, out, nblocks, diff, sa, s); break;
     default: break;
     }
 }

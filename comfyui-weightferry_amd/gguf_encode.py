@@ -124,7 +124,64 @@ def encode_q6_k(w):
     return out.ravel()
 
 
-ENCODERS = {8: encode_q8_0, 12: encode_q4_k, 13: encode_q5_k, 14: encode_q6_k}
+def _legacy(w, qtype):
+    """Q4_0 / Q5_0 (symmetric: d = f16(v / -2^(bits-1)) where v is the block's value of largest magnitude, q in
+    [0, 2^bits) with x ~ d * (q - 2^(bits-1))) and Q4_1 / Q5_1 (d = f16((max - min) / (2^bits - 1)), m = f16(min),
+    x ~ d * q + m), the blocks laid out as the decoder reads them (enhancers/gguf_dequant.py:145-160): nibble v / 16 of
+    qs[v % 16], bit v of qh."""
+    x = np.asarray(w, dtype=np.float32).reshape(-1, 32)
+    nb = x.shape[0]
+    bits = 5 if qtype in (6, 7) else 4
+    top = (1 << bits) - 1
+    if qtype in (2, 6):
+        idx = np.abs(x).argmax(axis=1)
+        v = x[np.arange(nb), idx]
+        d16 = _f16(v / -float(1 << (bits - 1)))
+        d = d16.astype(np.float32)
+        q = np.clip(np.rint(_safe_div(x, d[:, None])) + (1 << (bits - 1)), 0, top).astype(np.int32)
+        m16 = None
+    else:
+        lo, hi = x.min(axis=1), x.max(axis=1)
+        d16 = _f16((hi - lo) / float(top))
+        m16 = _f16(lo)
+        d, m = d16.astype(np.float32), m16.astype(np.float32)
+        q = np.clip(np.rint(_safe_div(x - m[:, None], d[:, None])), 0, top).astype(np.int32)
+    ts = TYPE_SIZE[qtype]
+    out = np.zeros((nb, ts), dtype=np.uint8)
+    out[:, 0:2] = d16.view(np.uint8).reshape(-1, 2)
+    o = 2
+    if m16 is not None:
+        out[:, 2:4] = m16.view(np.uint8).reshape(-1, 2)
+        o = 4
+    if bits == 5:
+        qh = np.zeros(nb, dtype=np.uint64)
+        for v in range(32):
+            qh |= ((q[:, v] >> 4) & 1).astype(np.uint64) << np.uint64(v)
+        out[:, o:o + 4] = qh.astype(np.uint32).view(np.uint8).reshape(-1, 4)
+        o += 4
+    qn = q & 0xF
+    out[:, o:o + 16] = (qn[:, 0:16] | (qn[:, 16:32] << 4)).astype(np.uint8)
+    return out.ravel()
+
+
+def encode_q4_0(w):
+    return _legacy(w, 2)
+
+
+def encode_q4_1(w):
+    return _legacy(w, 3)
+
+
+def encode_q5_0(w):
+    return _legacy(w, 6)
+
+
+def encode_q5_1(w):
+    return _legacy(w, 7)
+
+
+ENCODERS = {2: encode_q4_0, 3: encode_q4_1, 6: encode_q5_0, 7: encode_q5_1, 8: encode_q8_0, 12: encode_q4_k,
+            13: encode_q5_k, 14: encode_q6_k}
 
 
 def encode(w, qtype):

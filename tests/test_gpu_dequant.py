@@ -83,6 +83,19 @@ def test_full_size_ffn_weight_q4_k(native):
     assert np.array_equal(got, ref)
 
 
+@pytest.mark.parametrize("qtype", [2, 3, 6, 7, 10, 11, 13, 14])
+def test_large_weight_every_format(native, qtype):
+    """One 3072 x 5120 weight per format (encoded from N(0, 0.02) weights; Q2_K / Q3_K as random blocks): several
+    thousand workgroups of the tiled kernels, MID float16 -> bfloat16, value by value."""
+    shape = (3072, 5120)
+    if qtype in encode.ENCODERS:
+        raw = encode.encode(encode.weights(shape, seed=77), qtype)
+    else:
+        raw = encode.random_blocks(qtype, shape[0] * shape[1] // 256, seed=77)
+    got = _bits(gpu_dequant(native, torch.from_numpy(raw).cuda(), qtype, F16, BF16, shape[0] * shape[1]), BF16)
+    assert np.array_equal(got, lib.dequant(raw, qtype, F16, BF16, shape[0] * shape[1]))
+
+
 def test_dequantize_entry_point(native):
     gd = sub("enhancers.gguf_dequant")
     raw = encode.random_blocks(12, 64, seed=3)

@@ -5,7 +5,8 @@
   reference's flat-index formulas, the numpy restatement in GGML's block-loop form, and (hot formats) the
   torch-CPU op chain of ComfyUI-GGUF.
 * Q8_0 against its closed form on all 65536 float16 scales x 256 quants, rounded by numpy / torch.
-* Hand-computed known answers for Q8_0, Q4_K, Q5_K and Q6_K blocks (index layout of each format).
+* Hand-computed known answers for Q8_0, Q4_K, Q5_K, Q6_K and the legacy Q4_0 / Q4_1 / Q5_0 / Q5_1 blocks (index
+  layout of each format).
 * The 6-bit scale / min packing round trip for all 64 x 64 pairs of every sub-block.
 * encode -> decode stays within the quantisation step of the source weights (a dropped or sign-flipped term fails).
 """
@@ -172,14 +173,15 @@ def test_scale_min_roundtrip_all_pairs():
             assert (sc_out.value, m_out.value) == (sc_val, m_val)
 
 
-@pytest.mark.parametrize("qtype", [8, 12, 13, 14])
+@pytest.mark.parametrize("qtype", [2, 3, 6, 7, 8, 12, 13, 14])
 def test_encode_decode_within_step(qtype):
     w = encode.weights((64, 512), seed=3)
     raw = encode.encode(w, qtype)
     got = np_oracle.bits_to_f32(lib.dequant(raw, qtype, F32, F32, w.size), F32).reshape(w.shape)
     err = np.abs(got - w)
     amax = np.abs(w).max()
-    bound = {8: amax / 127, 12: amax * 2 / 15, 13: amax * 2 / 31, 14: amax / 31}[qtype]
+    bound = {2: amax / 8, 3: amax * 2 / 15, 6: amax / 16, 7: amax * 2 / 31, 8: amax / 127, 12: amax * 2 / 15,
+             13: amax * 2 / 31, 14: amax / 31}[qtype]
     assert err.max() <= bound, (qtype, err.max(), bound)
     assert np.abs(got - w).mean() < 0.3 * bound
 
@@ -190,3 +192,74 @@ def test_rejects_mismatched_sizes():
         lib.dequant(raw, 12, F16, BF16, 4 * 256 + 1)
     with pytest.raises(ValueError):
         lib.dequant(raw[:-1], 12, F16, BF16, 4 * 256)
+
+
+@pytest.mark.parametrize("qtype", [2, 3, 6, 7])
+def test_kat_legacy(qtype):
+    """Q4_0 / Q4_1 / Q5_0 / Q5_1 blocks built by hand: d = 0.5, m = -3 (Q4_1 / Q5_1), quant byte k = k | ((15 - k) <<
+    4), qh = 0xA5C3F00F (Q5_x). Value v: nibble v // 16 of qs[v % 16] (the low nibbles are values 0..15), bit v of qh
+    as bit 4; q - 8 (Q4_0) or q - 16 (Q5_0)."""
+    qs = np.array([k | ((15 - k) << 4) for k in range(16)], dtype=np.uint8)
+    qh = np.array([0xA5C3F00F], dtype="<u4").view(np.uint8)
+    head = [_f16b(0.5)]
+    if qtype in (3, 7):
+        head.append(_f16b(-3.0))
+    if qtype in (6, 7):
+        head.append(qh)
+    blk = np.concatenate(head + [qs])
+    assert blk.size == encode.TYPE_SIZE[qtype]
+    expect = np.empty(32, dtype=np.float32)
+    for v in range(32):
+        nib = int(qs[v % 16]) & 0xF if v < 16 else int(qs[v % 16]) >> 4
+        if qtype in (6, 7):
+            nib |= ((0xA5C3F00F >> v) & 1) << 4
+        sub = {2: 8, 6: 16}.get(qtype, 0)
+        expect[v] = 0.5 * (nib - sub) + (-3.0 if qtype in (3, 7) else 0.0)   # exact in every dtype
+    for mid in (F16, BF16, F32):
+        got = np_oracle.bits_to_f32(lib.dequant(blk, qtype, mid, F32, 32), F32)
+        assert np.array_equal(got, expect), (qtype, mid)
+
+
+def test_kat_q2_k():
+    """A Q2_K super-block packed the way GGML writes it: value v = 128n + 32s + l sits at bits 2s of qs[32n + l],
+    sub-block v // 16 has (scale, min) in the low / high nibble of scale byte v // 16; d = 0.5, dmin = 0.25. The
+    expected values 0.5 * scale * q - 0.25 * min are exact in every dtype."""
+    rng = np.random.default_rng(21)
+    q = rng.integers(0, 4, size=256)
+    sc, mn = rng.integers(0, 16, size=16), rng.integers(0, 16, size=16)
+    qs = np.zeros(64, dtype=np.int64)
+    for v in range(256):
+        n, s, l = v // 128, (v % 128) // 32, v % 32
+        qs[32 * n + l] |= q[v] << (2 * s)
+    blk = np.concatenate([(sc | (mn << 4)).astype(np.uint8), qs.astype(np.uint8), _f16b(0.5), _f16b(0.25)])
+    assert blk.size == 84
+    expect = np.array([0.5 * sc[v // 16] * q[v] - 0.25 * mn[v // 16] for v in range(256)], dtype=np.float32)
+    for mid in (F16, BF16, F32):
+        got = np_oracle.bits_to_f32(lib.dequant(blk, 10, mid, F32, 256), F32)
+        assert np.array_equal(got, expect), mid
+
+
+def test_kat_q3_k():
+    """A Q3_K super-block packed the way GGML writes it: value v = 128n + 32s + l has its 2 low bits at bits 2s of
+    qs[32n + l] and its high bit (set for q >= 0) at bit 4n + s of hmask[l]; sub-block i = v // 16 has a 6-bit
+    scale whose low nibble is nibble i // 8 of byte i % 8 and whose 2 high bits sit at bits 2(i // 4) of byte
+    8 + i % 4 of the 12 scale bytes, minus 32; d = 0.5. The expected values 0.5 * (scale - 32) * q are exact."""
+    rng = np.random.default_rng(22)
+    q = rng.integers(-4, 4, size=256)
+    sc = rng.integers(0, 64, size=16)
+    qs = np.zeros(64, dtype=np.int64)
+    hm = np.zeros(32, dtype=np.int64)
+    for v in range(256):
+        n, s, l = v // 128, (v % 128) // 32, v % 32
+        qs[32 * n + l] |= (q[v] & 3) << (2 * s)
+        hm[l] |= int(q[v] >= 0) << (4 * n + s)
+    scb = np.zeros(12, dtype=np.int64)
+    for i in range(16):
+        scb[i % 8] |= (sc[i] & 0xF) << (4 * (i // 8))
+        scb[8 + i % 4] |= (sc[i] >> 4) << (2 * (i // 4))
+    blk = np.concatenate([hm.astype(np.uint8), qs.astype(np.uint8), scb.astype(np.uint8), _f16b(0.5)])
+    assert blk.size == 110
+    expect = np.array([0.5 * (sc[v // 16] - 32) * q[v] for v in range(256)], dtype=np.float32)
+    for mid in (F16, BF16, F32):
+        got = np_oracle.bits_to_f32(lib.dequant(blk, 11, mid, F32, 256), F32)
+        assert np.array_equal(got, expect), mid
