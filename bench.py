@@ -13,7 +13,8 @@ Other rows of the workload list are reported under "also":
   * the int8 W8A8 linear at M in {1024, 4096, 16384}, K = 5120, N in {5120, 13824} (per-token int8 activations,
     per-channel int8 weights, int32 accumulation, bf16 out), and the row quantiser;
   * fused Q5_K / Q6_K dequant + bf16 GEMM over the linears of one Wan-2.1-14B block at 4096 tokens, next to the
-    two-step flow (wf_dequant, then torch's bf16 GEMM);
+    two-step flow (wf_dequant, then torch's bf16 GEMM), and the same linears at 32 tokens (Q4_K / Q5_K / Q6_K, the
+    fused kernel's few-rows form);
   * the LoRA add on a Q4_K 13824 x 5120 weight: the first LoRA fused into the dequantisation and a later LoRA
     onto the bf16 weight (float32 difference of n values each);
   * 40 streamed Wan-14B blocks of Q4_K from pinned host memory through 2 GPU slots, 4096 tokens (ms/step, H2D
@@ -139,6 +140,29 @@ def fused_leg(torch, native):
                      "fused_frac_of_2500": round(flops / tf / 1e9 / 2500, 3),
                      "two_step_ms": round(tu, 3), "two_step_TFLOPS": round(flops / tu / 1e9, 1),
                      "flop": flops, "weight_bytes": wbytes}
+    # few activation rows (32 tokens): the fused kernel's few-rows form streams each weight once; bound by HBM
+    for qt, name in ((12, "q4_k"), (13, "q5_k"), (14, "q6_k")):
+        tf = tu = 0.0
+        wbytes = 0
+        for lname, N, K in WAN_LINEARS:
+            raw = torch.from_numpy(encode.encode(encode.weights((N, K), seed=N + K), qt)).to(dev)
+            x = torch.randn((32, K), device=dev).to(torch.bfloat16)
+            y = torch.empty((32, N), dtype=torch.bfloat16, device=dev)
+            w = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+
+            def fused():
+                lib.wf_linear_gguf(x.data_ptr(), 32, K, raw.data_ptr(), raw.numel(), qt, N, None, y.data_ptr(), 0, st)
+
+            def two_step():
+                lib.wf_dequant(raw.data_ptr(), raw.numel(), qt, 0, 1, w.data_ptr(), N * K, st)
+                torch.matmul(x, w.t(), out=y)
+            tf += _timed(torch, fused, 20, 3)
+            tu += _timed(torch, two_step, 20, 3)
+            wbytes += raw.numel()
+            del raw, x, y, w
+        res[f"{name}_32_tokens"] = {"fused_us": round(tf * 1e3, 1), "two_step_us": round(tu * 1e3, 1),
+                                    "fused_weight_GBps": round(wbytes / (tf / 1e3) / 1e9, 1),
+                                    "weight_bytes": wbytes}
     torch.cuda.empty_cache()
     return res
 
@@ -150,7 +174,7 @@ def streaming_leg(torch, native, n_blocks=40, steps=10):
     prof_mod = importlib.import_module(PKG + ".streaming.profiler")
     dev = torch.device("cuda:0")
     t = time.perf_counter()
-    model = syn.WanLikeStack(n_blocks=n_blocks, qtype=12, mode="dequant")
+    model = syn.WanLikeStack(n_blocks=n_blocks, qtype=12, mode="auto")
     model.fill_random(1234)
     sm = dn.apply_streaming(model, device=dev, prefetch_slots=2, profile=False)
     _log(f"streaming: {n_blocks} blocks captured into pinned memory in {time.perf_counter() - t:.1f} s")
@@ -172,7 +196,7 @@ def streaming_leg(torch, native, n_blocks=40, steps=10):
             "h2d_GBps_effective": round(flat * n_blocks / (ms / 1e3) / 1e9, 2),
             "profiled": {"forward_ms": prof["forward_ms"], "dma_ms": prof["dma_ms"], "stall_ms": prof["stall_ms"],
                          "hidden_fraction": prof["overlap_ratio"], "dma_gbps": prof["dma_gbps"]},
-            "linears": "wf_dequant + torch bf16 GEMM"}
+            "linears": "GGUFLinear mode auto: wf_dequant + torch bf16 GEMM at 4096 and 512 rows"}
 
 
 def ssd_leg(torch, native, n_blocks=40, ram_blocks=20, steps=3):

@@ -472,6 +472,214 @@ __global__ __launch_bounds__(512) void gemm_gguf_dl(const uint16_t* __restrict__
     }
 }
 
+// ------------------------------------------------------------------------- few activation rows (M <= 16 MT)
+// With few rows of activations the product is bound by reading the weight, so the layout streams the quantised
+// weight through the whole chip exactly once: workgroup b takes the 16 weight rows [16 b, 16 b + 16) over all of
+// K, its 8 waves taking super-blocks w, w + 8, w + 16, ..., each with the raw bytes of its next two super-blocks in
+// flight (two register sets). Lane l dequantises the 8 values [8 (l / 16), +8) of each
+// 32-value stage of weight row 16 b + l % 16 straight into its B fragment of v_mfma_f32_16x16x32_bf16 (lane l:
+// column l % 16, K offset 8 (l / 16)); its A fragment is the 8 activations of row 16 mt + l % 16 at the same K
+// offset, read from global memory (a few rows: they stay in the L2). Result layout: lane l, register i -> row
+// 4 (l / 16) + i, column l % 16. The waves' partial sums meet in LDS and are added in wave order 0, 1, ..., 7. Rows
+// past M or N read the last valid row and are not stored.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int QT>
+struct SkRaw;
+template <> struct SkRaw<12> { uint4 hdr; uint2 q[4]; };
+template <> struct SkRaw<13> { uint4 hdr; uint2 q[4]; uint2 qh; };
+template <> struct SkRaw<14> { uint2 ql[4], qh[2]; uint32_t sc[4]; uint32_t d; };
+
+// bytes [o, o + 8) of the block stream at p (o even): aligned dwords funnel-shifted, inside [o - 2, o + 8)
+__device__ __forceinline__ uint2 ld8_even(const uint8_t* p, uint32_t o) {
+    const uint32_t a = o & ~3u, sh = (o & 3u) * 8u;
+    const uint32_t* wp = reinterpret_cast<const uint32_t*>(p + a);
+    const uint32_t w2 = *reinterpret_cast<const uint16_t*>(p + a + (sh ? 8 : 6));
+    return funnel8(wp[0], wp[1], w2, sh);
+}
+
+// raw bytes of K-quarter kq (values 8 kq .. of every stage) of the super-block at b (b: block start, 16-byte aligned
+// for Q4_K / Q5_K, 2-byte aligned for Q6_K)
+template <int QT>
+__device__ __forceinline__ void sk_load(const uint8_t* b, int kq, SkRaw<QT>& w) {
+    if constexpr (QT == 12 || QT == 13) {
+        constexpr int QS = QT == 12 ? 16 : 48;
+        w.hdr = *reinterpret_cast<const uint4*>(b);
+#pragma unroll
+        for (int p = 0; p < 4; p++) w.q[p] = *reinterpret_cast<const uint2*>(b + QS + 32 * p + 8 * kq);
+        if constexpr (QT == 13) w.qh = *reinterpret_cast<const uint2*>(b + 16 + 8 * kq);
+    } else {
+        // ql[64 h + 32 gp + 8 kq ..] for stages g with g / 4 = h, g % 2 = gp (nibble (g % 4) / 2); qh[128 + 32 h + 8 kq
+        // ..] (bits 2 (g % 4)); the scale of stage g is byte 192 + 2 g + kq / 2, read as the 16 bit-pairs at 192 + 4 i
+        const uint32_t o = (uint32_t)(uintptr_t)b & 3u;          // 0 or 2
+        const uint8_t* a = b - o;                                // dword-aligned
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int gp = 0; gp < 2; gp++) w.ql[2 * h + gp] = ld8_even(a, o + 64 * h + 32 * gp + 8 * kq);
+#pragma unroll
+        for (int h = 0; h < 2; h++) w.qh[h] = ld8_even(a, o + 128 + 32 * h + 8 * kq);
+        const uint2 s0 = ld8_even(a, o + 192), s1 = ld8_even(a, o + 200);
+        w.sc[0] = s0.x; w.sc[1] = s0.y; w.sc[2] = s1.x; w.sc[3] = s1.y;
+        w.d = *reinterpret_cast<const uint16_t*>(b + 208);
+    }
+}
+
+// the 8 values of stage g as a bf16x8 B fragment, the reference's rounding chain in MID
+template <int QT, int MID, int g>
+__device__ __forceinline__ bf16x8 sk_dequant(const SkRaw<QT>& w, int kq) {
+    uint32_t code[2];
+    uint32_t o[4];
+    if constexpr (QT == 12 || QT == 13) {
+        const uint2 qq = w.q[g >> 1];
+        code[0] = (qq.x >> (4 * (g & 1))) & 0x0f0f0f0fu;
+        code[1] = (qq.y >> (4 * (g & 1))) & 0x0f0f0f0fu;
+        if constexpr (QT == 13) {
+            code[0] |= ((w.qh.x >> g) & 0x01010101u) << 4;
+            code[1] |= ((w.qh.y >> g) & 0x01010101u) << 4;
+        }
+        uint32_t sc, m;
+        scale_min(w.hdr.y, w.hdr.z, w.hdr.w, g, sc, m);
+        if constexpr (MID == WF_F16) {
+            const h2 off = h2s(-1024.0f);
+            const h2 pr = as_h2(w.hdr.x) * (as_h2(sc | (m << 16) | 0x64006400u) + off);   // (d * sc, dmin * m)
+            const h2 ds = lo2(pr), dm = hi2(pr);
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const h2 v0 = ds * (biased_lo(code[i]) + off) - dm, v1 = ds * (biased_hi(code[i]) + off) - dm;
+                o[2 * i] = pack_bf16((float)v0[0], (float)v0[1]);
+                o[2 * i + 1] = pack_bf16((float)v1[0], (float)v1[1]);
+            }
+        } else {
+            const float d = round_to<MID>(f16_bits_to_f32(w.hdr.x & 0xffffu));
+            const float dmin = round_to<MID>(f16_bits_to_f32(w.hdr.x >> 16));
+            const float ds = round_to<MID>(d * (float)sc), dm = round_to<MID>(dmin * (float)m);
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] = round_to<MID>(round_to<MID>(ds * (float)byte_of(code[i], e)) - dm);
+                o[2 * i] = pack_bf16(v[0], v[1]);
+                o[2 * i + 1] = pack_bf16(v[2], v[3]);
+            }
+        }
+    } else {
+        constexpr int h = g >> 2, gp = g & 1, ns = 4 * ((g & 3) >> 1), hs = 2 * (g & 3);
+        const uint2 ql = w.ql[2 * h + gp], qh = w.qh[h];
+        code[0] = ((ql.x >> ns) & 0x0f0f0f0fu) | (((qh.x >> hs) & 0x03030303u) << 4);
+        code[1] = ((ql.y >> ns) & 0x0f0f0f0fu) | (((qh.y >> hs) & 0x03030303u) << 4);
+        // scale byte 2 g + kq / 2 of the 16: dword (2 g + kq / 2) / 4 = g / 2, byte (2 g + kq / 2) % 4
+        const int sbyte = 2 * (g & 1) + (kq >> 1);
+        const int sc = (int8_t)((w.sc[g >> 1] >> (8 * sbyte)) & 0xffu);
+        if constexpr (MID == WF_F16) {
+            const _Float16 ds1 = __builtin_bit_cast(_Float16, (uint16_t)(w.d & 0xffffu)) * (_Float16)(float)sc;
+            h2 ds;
+            ds[0] = ds1;
+            ds[1] = ds1;
+            const h2 off = h2s(-1056.0f);
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const h2 v0 = ds * (biased_lo(code[i]) + off), v1 = ds * (biased_hi(code[i]) + off);
+                o[2 * i] = pack_bf16((float)v0[0], (float)v0[1]);
+                o[2 * i + 1] = pack_bf16((float)v1[0], (float)v1[1]);
+            }
+        } else {
+            const float ds = round_to<MID>(round_to<MID>(f16_bits_to_f32(w.d & 0xffffu)) * (float)sc);
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] = round_to<MID>(ds * (float)((int)byte_of(code[i], e) - 32));
+                o[2 * i] = pack_bf16(v[0], v[1]);
+                o[2 * i + 1] = pack_bf16(v[2], v[3]);
+            }
+        }
+    }
+    return __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
+}
+
+constexpr int kSkWaves = 8;
+
+template <int QT, int MID, bool BIAS, int MT>
+__global__ __launch_bounds__(64 * kSkWaves) void gemm_gguf_skinny(const uint16_t* __restrict__ X,
+                                                                  const uint8_t* __restrict__ W,
+                                                                  const uint16_t* __restrict__ bias,
+                                                                  uint16_t* __restrict__ Y, int M, int N, int K) {
+    constexpr int TS = GGUFTs<QT>::TS, NW = kSkWaves;
+    __shared__ f32x4 red[NW][MT][64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 15, kq = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int64_t row_bytes = (int64_t)(K / 256) * TS;
+    const uint8_t* wrow = W + (int64_t)min(n0 + r, N - 1) * row_bytes;
+    const uint16_t* xrow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) xrow[mt] = X + (int64_t)min(16 * mt + r, M - 1) * K + 8 * kq;
+    f32x4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int nsb = K / 256;
+    auto stage = [&](auto G, const SkRaw<QT>& w, int sb) {
+        constexpr int g = decltype(G)::value;
+        const bf16x8 bw = sk_dequant<QT, MID, g>(w, kq);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const bf16x8 ax = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(xrow[mt] + sb * 256 + 32 * g));
+            acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bw, acc[mt], 0, 0, 0);
+        }
+    };
+    auto superblock = [&](const SkRaw<QT>& w, int sb) {
+        stage(std::integral_constant<int, 0>{}, w, sb);
+        stage(std::integral_constant<int, 1>{}, w, sb);
+        stage(std::integral_constant<int, 2>{}, w, sb);
+        stage(std::integral_constant<int, 3>{}, w, sb);
+        stage(std::integral_constant<int, 4>{}, w, sb);
+        stage(std::integral_constant<int, 5>{}, w, sb);
+        stage(std::integral_constant<int, 6>{}, w, sb);
+        stage(std::integral_constant<int, 7>{}, w, sb);
+    };
+    // super-blocks wave, wave + NW, ...: two raw register sets, each refilled two super-blocks ahead
+    SkRaw<QT> wa, wb;
+    int sb = wave;
+    if (sb < nsb) sk_load<QT>(wrow + (int64_t)sb * TS, kq, wa);
+    if (sb + NW < nsb) sk_load<QT>(wrow + (int64_t)(sb + NW) * TS, kq, wb);
+    while (sb < nsb) {
+        superblock(wa, sb);
+        if (sb + 2 * NW < nsb) sk_load<QT>(wrow + (int64_t)(sb + 2 * NW) * TS, kq, wa);
+        sb += NW;
+        if (sb >= nsb) break;
+        superblock(wb, sb);
+        if (sb + 2 * NW < nsb) sk_load<QT>(wrow + (int64_t)(sb + 2 * NW) * TS, kq, wb);
+        sb += NW;
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) red[wave][mt][lane] = acc[mt];
+    __syncthreads();
+    const int n = n0 + r;
+    const float bn = BIAS && n < N ? __uint_as_float((uint32_t)bias[n] << 16) : 0.0f;
+    for (int mt = wave; mt < MT; mt += NW) {
+        f32x4 t = red[0][mt][lane];
+#pragma unroll
+        for (int v = 1; v < NW; v++) t = t + red[v][mt][lane];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = 16 * mt + 4 * kq + i;
+            float y = t[i];
+            if (BIAS) y = y + bn;
+            if (m < M && n < N) Y[(int64_t)m * N + n] = __builtin_bit_cast(uint16_t, (__bf16)y);
+        }
+    }
+}
+
+template <int QT, int MID, int MT>
+static void launch_skinny(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
+                          hipStream_t s) {
+    const dim3 grid((unsigned)((N + 15) / 16));
+    if (bias) gemm_gguf_skinny<QT, MID, true, MT><<<grid, 64 * kSkWaves, 0, s>>>(X, W, bias, Y, M, N, K);
+    else gemm_gguf_skinny<QT, MID, false, MT><<<grid, 64 * kSkWaves, 0, s>>>(X, W, bias, Y, M, N, K);
+}
+
 template <int QT, int MID, int VM, int VN, int WM, int WN>
 static void launch_shape(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
                          hipStream_t s) {
@@ -486,6 +694,9 @@ static void launch_shape(const uint16_t* X, const uint8_t* W, const uint16_t* bi
 template <int QT, int MID>
 static void launch(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
                    hipStream_t s) {
+    if (M <= 16) { launch_skinny<QT, MID, 1>(X, W, bias, Y, M, N, K, s); return; }
+    if (M <= 32) { launch_skinny<QT, MID, 2>(X, W, bias, Y, M, N, K, s); return; }
+    if (M <= 64) { launch_skinny<QT, MID, 4>(X, W, bias, Y, M, N, K, s); return; }
     auto cost = [&](int bn) {
         const int64_t tiles = (int64_t)((M + 255) / 256) * ((N + bn - 1) / bn);
         return (tiles + 255) / 256 * bn;

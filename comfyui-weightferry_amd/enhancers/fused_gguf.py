@@ -3,9 +3,10 @@
 The reference dequantises the weight (enhancers/gguf_dequant.py:296-326, one kernel into a bf16 weight in HBM)
 and ComfyUI-GGUF then runs torch.nn.functional.linear on it. ``linear`` does both in one kernel launch for bf16
 activations and a Q4_K / Q5_K / Q6_K weight, with the same dequantised values (dequant dtype MID, then the layer
-dtype) and float32 accumulation; mode="dequant" keeps the reference's two-step flow (wf_dequant, then F.linear).
-Anything else -- other formats, dtypes, CPU tensors -- returns None from ``fused_linear`` and ``linear`` takes
-the two-step flow."""
+dtype) and float32 accumulation; mode="dequant" keeps the reference's two-step flow (wf_dequant, then F.linear);
+mode="auto" (the default of GGUFLinear) picks whichever measured faster on MI355X for the layer's shape
+(``prefer_fused``). Anything else -- other formats, dtypes, CPU tensors -- returns None from ``fused_linear`` and
+``linear`` takes the two-step flow."""
 import torch
 
 from .. import _native
@@ -41,9 +42,29 @@ def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
     return y.reshape(*x.shape[:-1], n_out)
 
 
-def linear(x, data, qtype, oshape, bias=None, mid_dtype=None, mode="fused"):
-    """The layer's forward: the fused kernel when it takes the case (mode "fused"), else the reference's flow --
-    the weight dequantised to x's dtype (wf_dequant), then torch.nn.functional.linear."""
+# Rows of activations up to which the fused kernel (its few-rows form: the weight streamed through the chip once)
+# beats the two-step flow, and from which its tiled form does for Q4_K / Q5_K weights no wider than they are deep.
+# Measured on MI355X (Wan-14B shapes 5120 x 5120, 13824 x 5120, 5120 x 13824): at 32 rows 24-61 us fused against
+# 39-67 us two-step; from 128 to 4096 rows the two-step flow (one dequantisation, then hipBLASLt) is faster; at 8192
+# rows the fused kernel takes 5120 x 5120 and 5120 x 13824 (Q4_K / Q5_K) 5-20 % faster, 13824 x 5120 and Q6_K not.
+FEW_ROWS = 64
+MANY_ROWS = 8192
+
+
+def prefer_fused(rows, qtype, n_out, k):
+    """mode "auto": True when the fused kernel is the faster way to compute this layer on MI355X."""
+    if rows <= FEW_ROWS:
+        return True
+    return rows >= MANY_ROWS and int(qtype) in (12, 13) and n_out <= k
+
+
+def linear(x, data, qtype, oshape, bias=None, mid_dtype=None, mode="auto"):
+    """The layer's forward: the fused kernel when it takes the case (mode "fused", or "auto" where it is the faster
+    one), else the reference's flow -- the weight dequantised to x's dtype (wf_dequant), then
+    torch.nn.functional.linear."""
+    if mode == "auto":
+        rows = x.numel() // x.shape[-1] if x.dim() else 0
+        mode = "fused" if prefer_fused(rows, qtype, oshape[0], oshape[1]) else "dequant"
     if mode == "fused":
         y = fused_linear(x, data, qtype, oshape, bias, mid_dtype)
         if y is not None:
@@ -58,7 +79,7 @@ class GGUFLinear(torch.nn.Module):
     """A linear layer with a GGUF-quantised weight held as raw uint8 blocks (the form ComfyUI-GGUF keeps), so that
     block streaming moves the quantised bytes."""
 
-    def __init__(self, in_features, out_features, qtype=12, bias=True, mode="fused", mid_dtype=None):
+    def __init__(self, in_features, out_features, qtype=12, bias=True, mode="auto", mid_dtype=None):
         super().__init__()
         q = int(qtype)
         ts = _FUSED_TYPES.get(q) or gguf_dequant._FORMATS.get(q, (None, None))[1]

@@ -26,7 +26,7 @@ def random_gguf_bytes(n_out, n_in, qtype, seed, d=2.0e-5, dmin=4.0e-5):
 
 
 class WanLikeBlock(torch.nn.Module):
-    def __init__(self, dim=5120, heads=40, ffn=13824, qtype=12, mode="fused"):
+    def __init__(self, dim=5120, heads=40, ffn=13824, qtype=12, mode="auto"):
         super().__init__()
         self.dim, self.heads = dim, heads
         L = lambda i, o: GGUFLinear(i, o, qtype, bias=True, mode=mode)  # noqa: E731
@@ -85,7 +85,7 @@ def write_gguf_model(model, path, alignment=256):
 
 
 class WanLikeStack(torch.nn.Module):
-    def __init__(self, n_blocks=40, dim=5120, heads=40, ffn=13824, qtype=12, mode="fused"):
+    def __init__(self, n_blocks=40, dim=5120, heads=40, ffn=13824, qtype=12, mode="auto"):
         super().__init__()
         self.blocks = torch.nn.ModuleList(WanLikeBlock(dim, heads, ffn, qtype, mode) for _ in range(n_blocks))
 

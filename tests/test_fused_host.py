@@ -1,0 +1,45 @@
+"""Host logic of the GGUF linear drop-in (enhancers/fused_gguf.py): the mode "auto" choice between the fused kernel
+and the two-step flow (measured crossover on MI355X), and its routing -- no GPU needed (the kernels are stubbed)."""
+import torch
+
+from conftest import sub
+
+fg = sub("enhancers.fused_gguf")
+
+
+def test_prefer_fused_rule():
+    # few activation rows: the fused kernel streams the weight once
+    for rows in (1, 16, 32, 64):
+        assert fg.prefer_fused(rows, 12, 5120, 5120)
+        assert fg.prefer_fused(rows, 14, 13824, 5120)
+    # between the two thresholds the two-step flow is faster for every format and shape
+    for rows in (65, 512, 4096, 8191):
+        for q in (12, 13, 14):
+            assert not fg.prefer_fused(rows, q, 5120, 5120)
+    # many rows: Q4_K / Q5_K weights no wider than deep take the fused kernel, the rest the two-step flow
+    assert fg.prefer_fused(8192, 12, 5120, 5120) and fg.prefer_fused(32768, 13, 5120, 13824)
+    assert not fg.prefer_fused(8192, 12, 13824, 5120)
+    assert not fg.prefer_fused(8192, 14, 5120, 5120)
+
+
+def test_auto_routes_by_rows(monkeypatch):
+    calls = []
+
+    def fake_fused(x, data, qtype, oshape, bias=None, mid_dtype=None):
+        calls.append("fused")
+        return torch.zeros(*x.shape[:-1], oshape[0])
+
+    def fake_dequant(data, qtype, oshape, mid_dtype=None, out_dtype=None):
+        calls.append("dequant")
+        return torch.zeros(oshape, dtype=out_dtype)
+
+    monkeypatch.setattr(fg, "fused_linear", fake_fused)
+    monkeypatch.setattr(fg.gguf_dequant, "dequantize", fake_dequant)
+    data = torch.zeros(16, dtype=torch.uint8)
+    fg.linear(torch.zeros(2, 8, 256, dtype=torch.bfloat16), data, 12, (32, 256))           # 16 rows
+    fg.linear(torch.zeros(1, 512, 256, dtype=torch.bfloat16), data, 12, (32, 256))         # 512 rows
+    fg.linear(torch.zeros(1, 512, 256, dtype=torch.bfloat16), data, 12, (32, 256), mode="fused")
+    fg.linear(torch.zeros(4, 256, dtype=torch.bfloat16), data, 12, (32, 256), mode="dequant")
+    assert calls == ["fused", "dequant", "fused", "dequant"]
+    layer = fg.GGUFLinear(256, 32, 12, bias=False)
+    assert layer.mode == "auto"

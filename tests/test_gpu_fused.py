@@ -95,6 +95,24 @@ def test_wan_block_shapes_sampled_rows(native, qtype, N, K):
     check(y, x, weight_bf16(raw, qtype, 0, N, K), rows=rows)
 
 
+@pytest.mark.parametrize("qtype", [12, 13, 14])
+@pytest.mark.parametrize("mid", [0, 2])
+@pytest.mark.parametrize("M,N,K,with_bias", [(1, 300, 256, True), (5, 5120, 5120, False), (16, 61, 512, True),
+                                             (17, 1000, 1024, False), (33, 300, 2048, True), (64, 5120, 512, False),
+                                             (48, 777, 1280, True), (65, 256, 768, False)])
+def test_few_rows_whole_output(native, qtype, mid, M, N, K, with_bias):
+    # up to 64 activation rows take the few-rows kernel (16 weight rows per workgroup, K split over its 8 waves,
+    # 1 to 4 row tiles of 16; K = 256 and 512 leave waves with no super-block); 65 rows the tiled kernel: ragged M
+    # and N, every output element checked
+    raw = encode.random_blocks(qtype, N * K // 256, seed=qtype * 7 + M, family="normal")
+    g = torch.Generator().manual_seed(M * 31 + N)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16) if with_bias else None
+    y = fused(native, x.cuda(), torch.from_numpy(raw).cuda(), qtype, N, bias=bias.cuda() if with_bias else None,
+              mid=mid)
+    check(y, x, weight_bf16(raw, qtype, mid, N, K), bias=bias)
+
+
 def test_rejects_what_it_does_not_handle(native):
     lib_ = native.lib()
     assert lib_.wf_linear_gguf(None, 4, 300, None, 0, 12, 4, None, None, 0, None) == native.EUNSUPPORTED   # K
