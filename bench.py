@@ -379,6 +379,78 @@ def cpu_baseline_dequant(torch, raw, qtype, rows, cols, budget_s=12.0):
                       f"first {rows} rows of the 13824x5120 weight, median of {len(times)} runs"}
 
 
+def _cpu_median(fn, budget_s, runs=10):
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < runs and time.perf_counter() < t_end:
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_baselines(torch, encode):
+    """The reference's CPU path beside every other workload row, each on a bounded sample (a few seconds): ComfyUI-
+    GGUF's torch op chain (oracle/torch_chain.py) for the dequantisation, torch's bf16 F.linear after it, and
+    torch._int_mm with the scale epilogue for the int8 linear; the streamed forward has no CPU path in the reference,
+    so its baseline is the CPU dequantisation + linear of one Wan block, extrapolated to 4096 tokens x 40 blocks."""
+    from oracle import torch_chain
+    cores = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(cores)
+    res = {}
+    # Q8_0, first 512 rows of the 5120 x 5120 weight
+    raw = encode.encode_q8_0(encode.weights((512, 5120), seed=1234))
+    t8 = torch.from_numpy(raw)
+    med, n = _cpu_median(lambda: torch_chain.dequantize(t8, 8, (512, 5120), torch.float16, torch.bfloat16), 6.0)
+    res["q8_0_dequant"] = {"value": round((raw.size + 512 * 5120 * 2) / med / 1e9, 3), "unit": "GB/s", "cores": cores,
+                           "kind": "port", "sample": f"Q8_0 -> bf16 (MID f16), 512 rows x 5120, median of {n}"}
+    # fused-GEMM row: Q5_K dequantisation of one 5120 x 5120 layer + bf16 F.linear at 64 tokens
+    raw5 = torch.from_numpy(encode.random_blocks(13, 5120 * 5120 // 256, seed=1234))
+    x = torch.randn((64, 5120)).to(torch.bfloat16)
+
+    def layer():
+        w = torch_chain.dequantize(raw5, 13, (5120, 5120), torch.float16, torch.bfloat16)
+        return torch_chain.linear_bf16(x, w)
+    med, n = _cpu_median(layer, 8.0, 5)
+    res["q5_k_dequant_plus_linear"] = {"value": round(2 * 64 * 5120 * 5120 / med / 1e12, 4), "unit": "TFLOPS",
+                                       "cores": cores, "kind": "port", "ms_per_layer": round(med * 1e3, 1),
+                                       "sample": f"Q5_K 5120x5120 dequant + bf16 linear, 64 tokens, median of {n}"}
+    # int8 W8A8 row: torch._int_mm + (acc * xs) * ws epilogue, 256 x 5120 by 5120 x 5120
+    xq = torch.randint(-127, 128, (256, 5120), dtype=torch.int8)
+    wq = torch.randint(-127, 128, (5120, 5120), dtype=torch.int8)
+    wqt = wq.t().contiguous()
+    xs, ws = torch.rand(256) * 0.01, torch.rand(5120) * 0.01
+
+    def i8():
+        acc = torch._int_mm(xq, wqt)
+        return ((acc.float() * xs[:, None]) * ws[None, :]).to(torch.bfloat16)
+    med, n = _cpu_median(i8, 6.0)
+    res["int8_linear"] = {"value": round(2 * 256 * 5120 * 5120 / med / 1e12, 4), "unit": "TOPS", "cores": cores,
+                          "kind": "port", "sample": f"torch._int_mm 256x5120 by 5120x5120 + scale epilogue, median of {n}"}
+    # streamed row: one Wan block's linears (Q4_K) on the CPU at 64 tokens -- eight 5120 x 5120 layers and two of
+    # 13824 x 5120 elements (ffn up / down), timed once per shape on random blocks; the dequantisations (per call,
+    # not per token) counted once, the GEMMs scaled to 4096 tokens; x 40 blocks
+    t_deq = t_mm = 0.0
+    for (N, K), count in (((5120, 5120), 8), ((13824, 5120), 2)):
+        r = torch.from_numpy(encode.random_blocks(12, N * K // 256, seed=N))
+        xb = torch.randn((64, K)).to(torch.bfloat16)
+        dq, _ = _cpu_median(lambda: torch_chain.dequantize(r, 12, (N, K), torch.float16, torch.bfloat16), 2.0, 3)
+        w = torch_chain.dequantize(r, 12, (N, K), torch.float16, torch.bfloat16)
+        mm, _ = _cpu_median(lambda: torch_chain.linear_bf16(xb, w), 2.0, 3)
+        t_deq += count * dq
+        t_mm += count * mm
+    block_s = t_deq + t_mm * 4096 / 64
+    res["streamed_block_linears"] = {"value": round(40 * block_s * 1e3, 0), "unit": "ms/step (extrapolated)",
+                                     "cores": cores, "kind": "port",
+                                     "sample": "one Wan block's 10 Q4_K linears on the CPU: dequantisation "
+                                               f"{t_deq * 1e3:.0f} ms + bf16 GEMMs at 64 tokens {t_mm * 1e3:.0f} ms "
+                                               "scaled to 4096 tokens, x 40 blocks (linears only; attention "
+                                               "excluded)"}
+    return res
+
+
 def _traffic():
     """HBM bytes per launch of the headline kernel from the committed rocprofv3 counter summary (FETCH_SIZE +
     WRITE_SIZE scaled by the plain-copy calibration), or None when the summary is absent."""
@@ -483,6 +555,8 @@ def main():
     if not args.skip_cpu:
         cpu = cpu_baseline_dequant(torch, raws[0], 12, 512, 5120)
         _log(f"cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
+        also["cpu_baselines"] = cpu_baselines(torch, encode)
+        _log("cpu baselines of the other rows done")
 
     line = {
         "metric": "dequant HBM GB/s (% peak); int8/bf16 GEMM TFLOPS; streamed-block ms/step",
