@@ -189,13 +189,27 @@ def streaming_leg(torch, native, n_blocks=40, steps=10):
     torch.cuda.synchronize()
     prof = sm.profile_summary()["mean_excluding_first_forward"]
     flat = sm.state.flat_bytes
+    # the link's own rate: block 0's pinned host flat into slot 0, five copies alone on the copy stream
+    st = sm.state
+    a, b = native.Event(timing=True), native.Event(timing=True)
+    a.record(st.prefetch_stream.handle)
+    for _ in range(5):
+        native.call("wf_h2d_async", st.slot_flats[0].data_ptr(), st.host_flats[0].data_ptr(), flat,
+                    st.prefetch_stream.handle)
+    b.record(st.prefetch_stream.handle)
+    b.synchronize()
+    raw_ms = a.elapsed_ms(b) / 5
     sm.teardown(device="cpu")
     del model, sm
     torch.cuda.empty_cache()
     return {"ms_per_step": round(ms, 2), "blocks": n_blocks, "slots": 2, "bytes_per_block": flat,
             "h2d_GBps_effective": round(flat * n_blocks / (ms / 1e3) / 1e9, 2),
+            "raw_h2d_GBps": round(flat / (raw_ms / 1e3) / 1e9, 2),
+            "copy_floor_ms_per_step": round(n_blocks * raw_ms, 1),
             "profiled": {"forward_ms": prof["forward_ms"], "dma_ms": prof["dma_ms"], "stall_ms": prof["stall_ms"],
-                         "hidden_fraction": prof["overlap_ratio"], "dma_gbps": prof["dma_gbps"]},
+                         "compute_ms": prof["streamed_compute_ms"],
+                         "hidden_fraction": prof["overlap_ratio"], "dma_gbps": prof["dma_gbps"],
+                         "hidden_fraction_bound": round(min(1.0, prof["streamed_compute_ms"] / prof["dma_ms"]), 4)},
             "linears": "GGUFLinear mode auto: wf_dequant + torch bf16 GEMM at 4096 and 512 rows"}
 
 

@@ -173,8 +173,11 @@ def _install_block_stream_hooks(dit, state, owner):
             slot_idx = state.slot_of(cur_s)
             state.computed_events[slot_idx].record(compute)
             next_s = cur_s + state.num_slots
-            if next_s < state.num_stream and not state.issued[next_s]:
-                state.issue_prefetch(next_s)
+            if next_s < state.num_stream:
+                if not state.issued[next_s]:
+                    state.issue_prefetch(next_s)
+            else:
+                state.wrap_prefetch(slot_idx)    # the slot's last block of this forward: the next forward's block
             if prof is not None:
                 prof.add_cpu(time.perf_counter() - t0)
         return stream_post_hook

@@ -21,6 +21,7 @@ class _StreamProfiler:
         self.no_staging = no_staging
         self.forwards = []
         self.cur = None
+        self.pending = {}     # events of the next forward's blocks, recorded during this one (wrap-around copies)
         # an idle stream: an event recorded on it completes when the CPU reaches it (CPU marks on the GPU timeline)
         self.marker_stream = _native.Stream()
 
@@ -38,7 +39,8 @@ class _StreamProfiler:
         if len(self.forwards) >= self.MAX_FORWARDS:
             self.cur = None
             return
-        self.cur = {"start": self._event(stream), "blocks": {}, "cpu_hook_s": 0.0}
+        self.cur = {"start": self._event(stream), "blocks": self.pending, "cpu_hook_s": 0.0}
+        self.pending = {}
         self.forwards.append(self.cur)
 
     def end_forward(self, stream):
@@ -46,8 +48,10 @@ class _StreamProfiler:
             self.cur["end"] = self._event(stream)
             self.cur = None
 
-    def record(self, s_idx, name, stream):
-        if self.cur is not None:
+    def record(self, s_idx, name, stream, next_forward=False):
+        if next_forward:
+            self.pending.setdefault(s_idx, {})[name] = self._event(stream)
+        elif self.cur is not None:
             self.cur["blocks"].setdefault(s_idx, {})[name] = self._event(stream)
 
     def add_cpu(self, seconds):

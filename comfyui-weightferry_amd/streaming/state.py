@@ -46,6 +46,10 @@ class _StreamState:
         for ev in self.computed_events:
             ev.record(compute)
         self.issued = [False] * self.num_stream
+        # end of the previous forward on the compute stream: the next forward is enqueued only once it has run
+        self.forward_done = _native.Event()
+        self.next_issued = set()          # the next forward's blocks already copied (wrap_prefetch)
+        self.forward_pending = False
         self.slot_ptrs = {v.data_ptr() for views in slot_views for v in views}
         self.copies = 0
         # SSD tier: stream index -> position in the ring's block order
@@ -61,19 +65,19 @@ class _StreamState:
     def slot_of(self, s_idx):
         return s_idx % self.num_slots
 
-    def materialize(self, s_idx, slot_idx, stream):
+    def materialize(self, s_idx, slot_idx, stream, next_forward=False):
         """Copy block s_idx's host flat into slot slot_idx on ``stream`` (streaming/state.py:133-149)."""
         prof = self.profiler
         src = self.host_flats[s_idx]
         dst = self.slot_flats[slot_idx]
         n = min(src.numel(), dst.numel())
         if prof is not None:
-            prof.record(s_idx, "dma0", stream)
+            prof.record(s_idx, "dma0", stream, next_forward)
         _native.call("wf_h2d_async", dst.data_ptr(), src.data_ptr(), n, stream)
         self.copies += 1
         if prof is not None:
-            prof.record(s_idx, "dma1", stream)
-            prof.record(s_idx, "ready", stream)
+            prof.record(s_idx, "dma1", stream, next_forward)
+            prof.record(s_idx, "ready", stream, next_forward)
 
     def issue_prefetch(self, s_idx):
         """Async copy of block s_idx into its slot, after that slot's last reader finished."""
@@ -96,18 +100,44 @@ class _StreamState:
         self.transferred_events[s_idx].query()        # forces submission without blocking the CPU
         self.issued[s_idx] = True
 
+    def wrap_prefetch(self, slot_idx):
+        """At the post-hook of the last block of this forward in slot slot_idx: copy the next forward's block
+        slot_idx (the first block that slot serves) into it, so that the next forward starts with its first blocks
+        on the GPU instead of waiting for their copies. The captured weights are the same for every forward. Blocks
+        of the SSD tier are left to the next forward (the ring serves its blocks in one cycle per forward)."""
+        k = slot_idx
+        if k >= self.num_stream or k in self.disk_index or self.host_flats[k] is None:
+            return
+        stream = self.prefetch_stream.handle
+        _native.stream_wait(stream, self.computed_events[slot_idx])
+        self.materialize(k, slot_idx, stream, next_forward=True)
+        self.transferred_events[k].record(stream)
+        self.transferred_events[k].query()
+        self.next_issued.add(k)
+
     def wait_transfer(self, s_idx):
         """Host side of the pre-hook for an SSD-tier block: its copy is on the copy stream (the event recorded)."""
         if s_idx in self.disk_index:
             self.ring.wait(self.tickets.pop(s_idx))
 
     def begin_forward(self):
-        self.issued = [False] * self.num_stream
+        """Start of a forward. The host waits until the previous forward has run on the GPU before enqueuing this
+        one: measured on MI355X with 40 Wan blocks, a host left to queue forward after forward runs the steps at
+        165-171 ms, one forward at a time at 147-148 ms (the block copies then hold 57 GB/s; queued several forwards
+        deep, many ran at 28-40 GB/s)."""
+        if self.forward_pending:
+            self.forward_done.synchronize()
+            self.forward_pending = False
+        self.issued = [s in self.next_issued for s in range(self.num_stream)]
+        self.next_issued = set()
         self.ssd_submitted = 0
 
     def end_forward(self):
-        """After a forward: when it stopped part way through the SSD tier, let the submitted copies finish and restart
-        the ring's cycle at block 0 (DiskRing.restart_if_needed, core/tiers/sources.py:318-335)."""
+        """After a forward: mark its end on the compute stream; when it stopped part way through the SSD tier, let the
+        submitted copies finish and restart the ring's cycle at block 0 (DiskRing.restart_if_needed,
+        core/tiers/sources.py:318-335)."""
+        self.forward_done.record(self.compute_stream())
+        self.forward_pending = True
         if self.ring is None:
             return
         pending = list(self.tickets.values())

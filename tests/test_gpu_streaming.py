@@ -1,8 +1,9 @@
 """GPU block streaming through the library's pinned buffers, copies and events.
 
 * A streamed forward of a small GGUF DiT stack is bit-identical to the same stack resident on the GPU (the
-  reference's own criterion, tests/test_streaming.py:222, torch.equal), with 2 and 3 slots, twice in a row, and with
-  a block skipped (the prefetch chain repaired in the pre-hook).
+  reference's own criterion, tests/test_streaming.py:222, torch.equal), with 2 and 3 slots, twice in a row (the
+  second forward starting from the first blocks the first one's tail copied ahead), and with a block skipped (the
+  prefetch chain repaired in the pre-hook).
 * After a copy, a slot holds exactly its block's host bytes.
 * The profiler's summary is consistent (overlap in [0, 1], a positive copy rate).
 * PinnedHost allocates page-locked memory of the exact size.
@@ -65,24 +66,46 @@ def test_streamed_forward_equals_resident(native, slots, mode):
         summ = sm.profile_summary()
         f = summ["per_forward"][-1]
         assert f["streamed_blocks"] == 6 and 0.0 <= f["overlap_ratio"] <= 1.0 and f["dma_gbps"] > 0
-        assert sm.state.copies == 12
+        # 6 blocks per forward; the last `slots` blocks of each forward also copy the next forward's first blocks
+        assert sm.state.copies == 12 + slots
     finally:
         sm.teardown()
 
 
-def test_skipped_block_repairs_the_prefetch_chain(native):
+@pytest.mark.parametrize("mode", ["fused", "dequant"])
+def test_skipped_block_repairs_the_prefetch_chain(native, mode):
     dn = sub("streaming.dit_node")
     x, ctx = _inputs()
-    resident = Skipping(_small_stack().cuda(), skip=(2,))
+    resident = Skipping(_small_stack(mode=mode).cuda(), skip=(2,))
     with torch.no_grad():
         ref = resident(x, ctx)
-    streamed = Skipping(_small_stack(), skip=(2,))
+    streamed = Skipping(_small_stack(mode=mode), skip=(2,))
     sm = dn.apply_streaming(streamed, device="cuda", prefetch_slots=2, profile=False)
     try:
         with torch.no_grad():
             y = sm(x, ctx)
         torch.cuda.synchronize()
         assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+    finally:
+        sm.teardown()
+
+
+def test_auto_mode_equals_resident(native):
+    # mode "auto": the 256-token linears take the two-step flow, the 64-token cross-attention k / v the fused
+    # few-rows kernel; three forwards in a row bit-identical to the resident stack
+    dn = sub("streaming.dit_node")
+    x, ctx = _inputs()
+    resident = _small_stack(mode="auto").cuda()
+    with torch.no_grad():
+        ref = resident(x, ctx)
+    streamed = _small_stack(mode="auto")
+    sm = dn.apply_streaming(streamed, device="cuda", prefetch_slots=2, profile=False)
+    try:
+        for _ in range(3):
+            with torch.no_grad():
+                y = sm(x, ctx)
+            assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+        torch.cuda.synchronize()
     finally:
         sm.teardown()
 

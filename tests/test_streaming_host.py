@@ -105,7 +105,7 @@ class FakeNative:
                         self.L.recorded.add((op[1], op[2]))
                     elif op[0] == "copy":
                         ctypes.memmove(op[1], op[2], op[3])
-                        self.L.log.append(("copy", op[1]))
+                        self.L.log.append(("copy", op[1], op[2]))
 
 
 class Tagged(torch.nn.Module):
@@ -189,8 +189,11 @@ def test_every_copy_waits_for_the_slots_last_reader(fake):
     sm(torch.zeros(1))
     fake.run_all()
     copies = [op for op in fake.L.log if op[0] == "copy"]
-    assert len(copies) == 6
+    # the 6 blocks, then the next forward's blocks 0 and 1 copied by the last block of each slot (wrap_prefetch)
+    assert len(copies) == 8
     st = sm.state
+    assert st.next_issued == {0, 1}
+    assert [op[2] for op in copies[-2:]] == [st.host_flats[0].data_ptr(), st.host_flats[1].data_ptr()]
     slot_of_ptr = {f.data_ptr(): i for i, f in enumerate(st.slot_flats)}
     copy_stream = st.prefetch_stream.handle
     ops = [op for op in fake.L.issued if op[0] == copy_stream]
@@ -201,6 +204,10 @@ def test_every_copy_waits_for_the_slots_last_reader(fake):
     # the compute stream waits for each block's transfer event before the block runs
     waits = [op[2] for op in fake.L.issued if op[0] == 1 and op[1] == "wait"]
     assert waits == [e.handle for e in st.transferred_events]
+    # a second forward starts from the copies made ahead: only blocks 2..5 are copied in it (and again 0, 1 ahead)
+    sm(torch.zeros(1))
+    fake.run_all()
+    assert len([op for op in fake.L.log if op[0] == "copy"]) == 8 + 6
 
 
 def test_flag_overrides_slot_count(monkeypatch):
