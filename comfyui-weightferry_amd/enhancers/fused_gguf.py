@@ -63,7 +63,7 @@ def linear(x, data, qtype, oshape, bias=None, mid_dtype=None, mode="auto"):
     one), else the reference's flow -- the weight dequantised to x's dtype (wf_dequant), then
     torch.nn.functional.linear."""
     if mode == "auto":
-        rows = x.numel() // x.shape[-1] if x.dim() else 0
+        rows = x.numel() // max(1, x.shape[-1]) if x.dim() else 0
         mode = "fused" if prefer_fused(rows, qtype, oshape[0], oshape[1]) else "dequant"
     if mode == "fused":
         y = fused_linear(x, data, qtype, oshape, bias, mid_dtype)
