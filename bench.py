@@ -7,7 +7,7 @@ the timed region; each step works on the next of four copies of inputs and outpu
 256 MB last-level cache cannot serve one step's bytes to the next.
 
 Other rows of the workload list are reported under "also":
-  * Q8_0 dequantisation of a 5120 x 5120 weight (MID float16 and float32);
+  * Q8_0 dequantisation of a 5120 x 5120 weight (MID float16 and float32) and of the FFN pair;
   * every other GGML format at 5120 x 5120 -> bf16 (MID float16): Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q5_K / Q6_K encoded
     from the same N(0, 0.02) weights, Q2_K / Q3_K as random blocks with typical float16 scales;
   * the int8 W8A8 linear at M in {1024, 4096, 16384}, K = 5120, N in {5120, 13824} (per-token int8 activations,
@@ -541,12 +541,17 @@ def main():
     ms32, k32, _ = dequant_leg(torch, native, raws, shapes, 12, 2, 1, max(5, args.steps // 2), 3)
     also["q4_k_pair_mid_f32"] = {"GB/s": round(algo / (ms32 / 1e3) / 1e9, 1),
                                  "kernel_us": round(k32 * 1e3, 2)}
-    # Q8_0 5120 x 5120 (MID float16 and float32 -> bf16)
+    # Q8_0 5120 x 5120 (MID float16 and float32 -> bf16), and the 14B-DiT FFN pair in Q8_0
     q8 = [encode.encode_q8_0(encode.weights((5120, 5120), seed=1234))]
     for mid, name in ((0, "q8_0_5120sq_mid_f16"), (2, "q8_0_5120sq_mid_f32")):
         ms8, k8, a8 = dequant_leg(torch, native, q8, [(5120, 5120)], 8, mid, 1, args.steps, args.warmup)
         also[name] = {"GB/s": round(a8 / (k8 / 1e3) / 1e9, 1), "kernel_us": round(k8 * 1e3, 2),
                       "frac": round(a8 / (k8 / 1e3) / 1e9 / HBM_PEAK_GBS, 3), "bytes": a8}
+    q8p = [encode.encode_q8_0(encode.weights(sh, seed=1234 + i)) for i, sh in enumerate(shapes)]
+    ms8, k8, a8 = dequant_leg(torch, native, q8p, shapes, 8, 0, 1, args.steps, args.warmup)
+    also["q8_0_ffn_pair_mid_f16"] = {"GB/s": round(a8 / (ms8 / 1e3) / 1e9, 1), "kernel_us": round(k8 * 1e3, 2),
+                                     "frac": round(a8 / (ms8 / 1e3) / 1e9 / HBM_PEAK_GBS, 3), "bytes": a8}
+    del q8p
     if "formats" in args.legs:
         also["dequant_formats_5120sq"] = formats_leg(torch, native, encode, args.steps, args.warmup)
         _log("formats leg done")
