@@ -8,6 +8,9 @@ the timed region; each step works on the next of four copies of inputs and outpu
 
 Other rows of the workload list are reported under "also":
   * Q8_0 dequantisation of a 5120 x 5120 weight (MID float16 and float32) and of the FFN pair;
+  * what HBM delivers, with the same rotation, to a kernel that only moves the bytes of a dequantisation launch
+    (the Q4_K 13824 x 5120 launch, Q8_0 / Q4_0 / Q6_K 5120 x 5120) in the nearest read:write mix (1:2 or 2:7), and
+    the Q4_K / Q8_0 launches as a fraction of it;
   * every other GGML format at 5120 x 5120 -> bf16 (MID float16): Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q5_K / Q6_K encoded
     from the same N(0, 0.02) weights, Q2_K / Q3_K as random blocks with typical float16 scales;
   * the int8 W8A8 linear at M in {1024, 4096, 16384}, K = 5120, N in {5120, 13824} (per-token int8 activations,
@@ -23,8 +26,8 @@ Other rows of the workload list are reported under "also":
     streamed forward with half the blocks read from the file on every step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--only-headline] [--legs LEGS]
---legs (comma list of headline, formats, lora, int8, fused, streaming, ssd; default all) runs only those legs, for profiling one
-kernel family; without the headline leg the printed line holds the legs' figures only.
+--legs (comma list of headline, ceiling, formats, lora, int8, fused, streaming, ssd; default all) runs only those
+legs, for profiling one kernel family; without the headline leg the printed line holds the legs' figures only.
 """
 import argparse
 import importlib
@@ -47,10 +50,11 @@ def _args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true", help="leave out the CPU baseline leg")
     ap.add_argument("--only-headline", action="store_true", help="the Q4_K dequant leg only")
-    ap.add_argument("--legs", default="all", help="comma list: headline, formats, lora, int8, fused, streaming, ssd")
+    ap.add_argument("--legs", default="all",
+                    help="comma list: headline, ceiling, formats, lora, int8, fused, streaming, ssd")
     a = ap.parse_args()
     a.legs = {"headline"} if a.only_headline else (
-        {"headline", "formats", "lora", "int8", "fused", "streaming", "ssd"} if a.legs == "all"
+        {"headline", "ceiling", "formats", "lora", "int8", "fused", "streaming", "ssd"} if a.legs == "all"
         else set(a.legs.split(",")))
     return a
 
@@ -345,6 +349,55 @@ def dequant_leg(torch, native, raws, shapes, qtype, mid, out_dt, steps, warmup):
     return ms_step, ms_step / len(shapes), algo
 
 
+def hbm_stream_leg(torch, native, nbytes, reads, writes, steps, warmup):
+    """What HBM delivers to a kernel that only moves bytes (wf_hbm_stream: reads:writes 16-byte chunks per thread,
+    non-temporal stores) for about `nbytes` per launch, with the dequant legs' rotation over ROTATE_BYTES. Returns
+    (bytes per launch, mean us per launch)."""
+    lib = native.lib()
+    dev = torch.device("cuda:0")
+    stream = native.stream_of(dev)
+    items = nbytes // (16 * (reads + writes))
+    per = 16 * items * (reads + writes)
+    rot = max(ROTATE, -(-ROTATE_BYTES // per))
+    ins = [torch.empty(max(16, 16 * items * reads), dtype=torch.uint8, device=dev) for _ in range(rot)]
+    outs = [torch.empty(max(16, 16 * items * writes), dtype=torch.uint8, device=dev) for _ in range(rot)]
+    for t in ins:
+        t.fill_(1)
+
+    def launch(r):
+        rc = lib.wf_hbm_stream(ins[r].data_ptr(), outs[r].data_ptr(), items, reads, writes, stream)
+        if rc != 0:
+            raise RuntimeError(native.last_error())
+
+    for i in range(warmup):
+        launch(i % rot)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(steps):
+        launch(i % rot)
+    t1.record()
+    torch.cuda.synchronize()
+    us = t0.elapsed_time(t1) * 1e3 / steps
+    del ins, outs
+    torch.cuda.empty_cache()
+    return per, us
+
+
+# the dequantisation launches set beside a byte-moving kernel of the same size and nearest read:write mix
+CEILINGS = (("q4_k_13824x5120_mix_2_7", 181_370_880, 2, 7), ("q8_0_5120sq_mix_1_2", 80_281_600, 1, 2),
+            ("q4_0_5120sq_mix_2_7", 67_174_400, 2, 7), ("q6_k_5120sq_mix_1_2", 73_932_800, 1, 2))
+
+
+def ceiling_leg(torch, native, steps, warmup):
+    res = {}
+    for name, nbytes, r, w in CEILINGS:
+        per, us = hbm_stream_leg(torch, native, nbytes, r, w, steps, warmup)
+        res[name] = {"GB/s": round(per / us / 1e3, 1), "kernel_us": round(us, 2), "bytes": per,
+                     "frac": round(per / us / 1e3 / HBM_PEAK_GBS, 3)}
+    return res
+
+
 FORMATS = ((2, "q4_0"), (3, "q4_1"), (6, "q5_0"), (7, "q5_1"), (13, "q5_k"), (14, "q6_k"), (10, "q2_k"),
            (11, "q3_k"))
 
@@ -502,6 +555,8 @@ def main():
         raws = [encode.encode_q4_k(encode.weights(s, seed=1234 + i)) for i, s in enumerate(shapes)]
         _log(f"encoded Q4_K pair in {time.perf_counter() - t:.1f} s")
     if "headline" not in args.legs:
+        if "ceiling" in args.legs:
+            also["hbm_stream_same_mix"] = ceiling_leg(torch, native, args.steps, args.warmup)
         if "formats" in args.legs:
             also["dequant_formats_5120sq"] = formats_leg(torch, native, encode, args.steps, args.warmup)
         if "lora" in args.legs:
@@ -552,6 +607,13 @@ def main():
     also["q8_0_ffn_pair_mid_f16"] = {"GB/s": round(a8 / (ms8 / 1e3) / 1e9, 1), "kernel_us": round(k8 * 1e3, 2),
                                      "frac": round(a8 / (ms8 / 1e3) / 1e9 / HBM_PEAK_GBS, 3), "bytes": a8}
     del q8p
+    if "ceiling" in args.legs:
+        ceil = ceiling_leg(torch, native, args.steps, args.warmup)
+        also["hbm_stream_same_mix"] = ceil
+        also["q8_0_5120sq_mid_f16"]["of_same_mix_stream"] = round(
+            also["q8_0_5120sq_mid_f16"]["GB/s"] / ceil["q8_0_5120sq_mix_1_2"]["GB/s"], 3)
+        also["q4_k_13824x5120_of_same_mix_stream"] = round(achieved / ceil["q4_k_13824x5120_mix_2_7"]["GB/s"], 3)
+        _log("ceiling leg done")
     if "formats" in args.legs:
         also["dequant_formats_5120sq"] = formats_leg(torch, native, encode, args.steps, args.warmup)
         _log("formats leg done")

@@ -76,3 +76,16 @@ def test_check_maps_codes():
     assert native.check(native.EUNSUPPORTED, "x") is False
     with pytest.raises(native.NativeError):
         native.check(native.EHIP, "x")
+
+
+def test_hbm_stream_argument_checks_without_gpu():
+    native = sub("_native")
+    lib = native.lib()
+    buf = ctypes.create_string_buffer(4096)
+    p16 = (ctypes.addressof(buf) + 15) // 16 * 16
+    assert lib.wf_hbm_stream(p16, p16, 0, 1, 2, None) == native.EINVAL
+    assert lib.wf_hbm_stream(p16, None, 4, 1, 0, None) == native.EINVAL
+    assert lib.wf_hbm_stream(None, p16, 4, 1, 2, None) == native.EINVAL
+    assert lib.wf_hbm_stream(p16 + 4, p16, 4, 1, 2, None) == native.EINVAL
+    assert lib.wf_hbm_stream(p16, p16, 4, 3, 5, None) == native.EUNSUPPORTED
+    assert "3:5" in native.last_error()
