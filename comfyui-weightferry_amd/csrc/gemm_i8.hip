@@ -6,10 +6,10 @@
 // 4 (l / 32) + i % 4, column l % 32 of the 32x32 tile.
 //
 // Two kernels:
-//  * gemm_i8_dl (K % 64 == 0, the workload): 256 x 320, 256 x 256 or 256 x 128 tiles (chosen per shape, see
-//    launch_dl), operands streamed global -> LDS by the load unit (no register staging) through a 4-stage ring of
-//    64-byte K stages, and an epilogue that stages the rounded tile in LDS and stores whole 16-byte runs of output
-//    rows.
+//  * gemm_i8_dl (K % 64 == 0, the workload): 256 x 320, 256 x 256, 256 x 128 or 128 x 160 tiles (chosen per
+//    shape, see launch_dl), operands streamed global -> LDS by the load unit (no register staging) through a
+//    4-stage ring of 64-byte K stages, and an epilogue that stages the rounded tile in LDS and stores whole 16-byte
+//    runs of output rows.
 //  * gemm_i8 (K % 16 == 0 otherwise): 2 x 2 waves, predicated loads staged through registers into a
 //    double-buffered LDS tile of 128-byte K stages. Rows are 8 chunks of 16 bytes; chunk c of row r sits at slot
 //    c ^ (((r >> 1) ^ ((r & 1) << 2)) & 7), conflict-free for stage writes and fragment reads.
@@ -17,6 +17,8 @@
 // Tile order is XCD-aware: workgroup w runs on XCD w % 8, so consecutive tile indices are dealt to one XCD's
 // workgroups and that XCD's L2 sees neighbouring tiles (they share A rows / B rows); within the order, tiles are
 // grouped GROUP_M tile-rows at a time.
+
+#include <algorithm>
 
 #include "lds_ring.h"
 
@@ -395,6 +397,8 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
 //              make exactly 256 tiles.
 //   256 x 256: 8 waves of 4 x 2 MFMA tiles (128 x 64).
 //   256 x 128: 4 waves of 4 x 2 MFMA tiles, one per SIMD: more workgroups for small outputs.
+//   128 x 160: 4 waves of 1 x 5 MFMA tiles: 1024 x 5120 outputs make exactly 256 tiles (1.2 LDS fragment reads per
+//              MFMA against 0.75 for 4 x 2, but every CU busy: 42.7 against 50.9 us for the 256 x 128 tiling).
 template <int VM, int VN, int WM, int WN, int OUT>
 static void launch_dl_shape(const int8_t* A, const int8_t* B, const float* xs, const float* ws, const void* bias,
                             void* out, int M, int N, int K, Residual r, bool resid, hipStream_t s) {
@@ -415,9 +419,11 @@ template <int OUT>
 static void launch_dl(const int8_t* A, const int8_t* B, const float* xs, const float* ws, const void* bias,
                       void* out, int M, int N, int K, Residual r, bool resid, hipStream_t s) {
     const int64_t c320 = dl_cost(M, N, 256, 320, 1030), c256 = dl_cost(M, N, 256, 256, 1000);
-    const int64_t c128 = dl_cost(M, N, 256, 128, 780);
-    if (c128 < c256 && c128 < c320) launch_dl_shape<2, 2, 4, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
-    else if (c256 < c320) launch_dl_shape<2, 4, 4, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
+    const int64_t c128 = dl_cost(M, N, 256, 128, 780), c160 = dl_cost(M, N, 128, 160, 581);
+    const int64_t best = std::min(std::min(c320, c256), std::min(c128, c160));
+    if (c160 == best) launch_dl_shape<4, 1, 1, 5, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
+    else if (c128 == best) launch_dl_shape<2, 2, 4, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
+    else if (c256 == best) launch_dl_shape<2, 4, 4, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
     else launch_dl_shape<4, 2, 2, 5, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
 }
 
