@@ -22,12 +22,13 @@ Other rows of the workload list are reported under "also":
     onto the bf16 weight (float32 difference of n values each);
   * 40 streamed Wan-14B blocks of Q4_K from pinned host memory through 2 GPU slots, 4096 tokens (ms/step, H2D
     GB/s, share of the copy time hidden behind compute);
+  * chunk (sub-block) streaming of the same 40 blocks: 96 MB chunks of a block's linears through 4 GPU slots;
   * the SSD tier: the same 40 blocks as a GGUF file on local disk, the reader ring's O_DIRECT read rate, and the
     streamed forward with half the blocks read from the file on every step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--only-headline] [--legs LEGS]
---legs (comma list of headline, ceiling, formats, lora, int8, fused, streaming, ssd; default all) runs only those
-legs, for profiling one kernel family; without the headline leg the printed line holds the legs' figures only.
+--legs (comma list of headline, ceiling, formats, lora, int8, fused, streaming, chunk, ssd; default all) runs only
+those legs, for profiling one kernel family; without the headline leg the printed line holds the legs' figures only.
 """
 import argparse
 import importlib
@@ -51,10 +52,10 @@ def _args():
     ap.add_argument("--skip-cpu", action="store_true", help="leave out the CPU baseline leg")
     ap.add_argument("--only-headline", action="store_true", help="the Q4_K dequant leg only")
     ap.add_argument("--legs", default="all",
-                    help="comma list: headline, ceiling, formats, lora, int8, fused, streaming, ssd")
+                    help="comma list: headline, ceiling, formats, lora, int8, fused, streaming, chunk, ssd")
     a = ap.parse_args()
     a.legs = {"headline"} if a.only_headline else (
-        {"headline", "ceiling", "formats", "lora", "int8", "fused", "streaming", "ssd"} if a.legs == "all"
+        {"headline", "ceiling", "formats", "lora", "int8", "fused", "streaming", "chunk", "ssd"} if a.legs == "all"
         else set(a.legs.split(",")))
     return a
 
@@ -215,6 +216,38 @@ def streaming_leg(torch, native, n_blocks=40, steps=10):
                          "hidden_fraction": prof["overlap_ratio"], "dma_gbps": prof["dma_gbps"],
                          "hidden_fraction_bound": round(min(1.0, prof["streamed_compute_ms"] / prof["dma_ms"]), 4)},
             "linears": "GGUFLinear mode auto: wf_dequant + torch bf16 GEMM at 4096 and 512 rows"}
+
+
+def chunk_leg(torch, native, n_blocks=40, steps=5, chunk_mb=96, slots=4):
+    """Chunk (sub-block) streaming of the same 40 blocks: the GPU holds ``slots`` chunks of at most ``chunk_mb`` MB of
+    a block's linears (plus a spare) instead of two whole blocks. The first forward learns the call order (each
+    linear copied on the compute stream just before it runs); the timed forwards stream chunk units."""
+    syn = importlib.import_module(PKG + ".streaming.synthetic")
+    dn = importlib.import_module(PKG + ".streaming.dit_node")
+    dev = torch.device("cuda:0")
+    model = syn.WanLikeStack(n_blocks=n_blocks, qtype=12, mode="auto")
+    model.fill_random(1234)
+    sm = dn.apply_streaming(model, device=dev, chunk=True, chunk_bytes=chunk_mb * 1024 ** 2, chunk_slots=slots)
+    g = torch.Generator().manual_seed(99)
+    x = torch.randn((1, 4096, 5120), generator=g).to(torch.bfloat16).to(dev)
+    ctx = torch.randn((1, 512, 5120), generator=g).to(torch.bfloat16).to(dev)
+    with torch.no_grad():
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        sm(x, ctx)
+        torch.cuda.synchronize()
+        calib_ms = (time.perf_counter() - t) * 1e3
+        ms = _timed(torch, lambda: sm(x, ctx), steps, 1)
+    st = sm.state
+    res = {"ms_per_step": round(ms, 2), "calibration_forward_ms": round(calib_ms, 1), "blocks": n_blocks,
+           "chunk_mb": chunk_mb, "slots": slots, "chunks_per_block": st.n_types,
+           "chunk_slot_bytes": st.slot_bytes, "gpu_weight_bytes": st.slot_bytes * (slots + len(st.spares)),
+           "block_mode_gpu_weight_bytes": 2 * st.flat_bytes, "spare_uses": st.spare_uses,
+           "h2d_GBps_effective": round(st.flat_bytes * n_blocks / (ms / 1e3) / 1e9, 2)}
+    sm.teardown(device="cpu")
+    del model, sm
+    torch.cuda.empty_cache()
+    return res
 
 
 def ssd_leg(torch, native, n_blocks=40, ram_blocks=20, steps=3):
@@ -567,6 +600,8 @@ def main():
             also["fused_dequant_gemm_wan_block"] = fused_leg(torch, native)
         if "streaming" in args.legs:
             also["streamed_40_blocks_q4_k"] = streaming_leg(torch, native)
+        if "chunk" in args.legs:
+            also["chunk_streamed_40_blocks_q4_k"] = chunk_leg(torch, native)
         if "ssd" in args.legs:
             also["ssd_tier_40_blocks_q4_k"] = ssd_leg(torch, native)
         print(json.dumps({"legs": sorted(args.legs), "also": also}), flush=True)
@@ -629,6 +664,9 @@ def main():
     if "streaming" in args.legs:
         also["streamed_40_blocks_q4_k"] = streaming_leg(torch, native)
         _log("streaming leg done")
+    if "chunk" in args.legs:
+        also["chunk_streamed_40_blocks_q4_k"] = chunk_leg(torch, native)
+        _log("chunk leg done")
     if "ssd" in args.legs:
         also["ssd_tier_40_blocks_q4_k"] = ssd_leg(torch, native)
         _log("ssd leg done")

@@ -20,6 +20,14 @@ DEFAULTS = {
     "WEIGHTFERRY_MODEL_FILE": None,        # the GGUF file the SSD tier reads blocks from (else a cache file)
     "WEIGHTFERRY_CACHE_DIR": None,         # directory of the SSD tier's cache files (default: temp directory)
     "WEIGHTFERRY_RAM_MARGIN_GB": "6",      # RAM kept free besides the RAM tier when its budget is automatic
+    # chunk (sub-block) streaming
+    "WEIGHTFERRY_CHUNK": None,             # "1": the node streams chunks of blocks; "0" / unset: whole blocks
+    "WEIGHTFERRY_CHUNK_MB": "96",          # bytes of layers per chunk
+    "WEIGHTFERRY_CHUNK_SLOTS": "4",        # rotating chunk slots on the GPU (plus a spare)
+    "WEIGHTFERRY_CHUNK_BLOCK0": "1",       # "0": block 0 stays resident in chunk mode
+    "WEIGHTFERRY_CHUNK_RECALIBRATE": None,  # "1": learn the call order again on every load
+    "WEIGHTFERRY_CHUNK_LOG": None,         # "1": a log line per chunked forward
+    "WEIGHTFERRY_OUTSIDE_LEAF": "1",       # "0": a layer called before any block starts the chunk pipeline
 }
 
 

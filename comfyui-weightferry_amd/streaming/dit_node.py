@@ -8,7 +8,8 @@ installs the hooks, ``StreamedModel.__call__`` runs one forward with streaming a
 import torch
 
 from .common import _ACTIVE_ATTR, _STATE_ATTR, _blocks
-from .load_steps import _build_state, _install_block_stream_hooks, _install_first_block_hook
+from .load_steps import (_build_chunk_state, _build_state, _install_block_stream_hooks, _install_chunk_hooks,
+                         _install_first_block_hook)
 
 
 class StreamedModel:
@@ -66,7 +67,8 @@ class StreamedModel:
 
 def apply_streaming(dit, device="cuda", resident_blocks=0, prefetch_slots=2, pin_memory=True, profile=None,
                     model_file=None, ram_blocks=None, ssd_layout=None, ring_depth=2, ring_threads=1, direct_io=True,
-                    tensor_name=None, double_buffer=True, ssd_dir=None):
+                    tensor_name=None, double_buffer=True, ssd_dir=None, chunk=False, chunk_bytes=None,
+                    chunk_slots=None, order_cache=None):
     """Stream all but the first ``resident_blocks`` blocks of ``dit`` (which stay where they are, on ``device``)
     through ``prefetch_slots`` (>= 2) GPU slots. The reference keeps block 0 resident by default
     (streaming/dit_node.py:237-267); here resident_blocks = 0 streams every block.
@@ -77,7 +79,11 @@ def apply_streaming(dit, device="cuda", resident_blocks=0, prefetch_slots=2, pin
     straight from a GGUF ``model_file`` holding the blocks' tensors, or else from a cache file the capture writes
     into ``ssd_dir`` (default WEIGHTFERRY_CACHE_DIR / the temp directory). ``tensor_name(block_index,
     param_name)`` gives a parameter's tensor name in the model file (default "<block list>.<index>.<param name>",
-    ComfyUI-GGUF's naming of a DiT's state dict)."""
+    ComfyUI-GGUF's naming of a DiT's state dict).
+
+    ``chunk``: sub-block streaming (streaming.chunk_state): the GPU holds ``chunk_slots`` chunks of at most
+    ``chunk_bytes`` of a block's layers instead of whole blocks; the first forward learns the blocks' call order,
+    kept in ``order_cache`` (a dict) when one is given. RAM tier and double buffering only."""
     blocks = list(_blocks(dit))
     if not blocks:
         raise ValueError("the model has no block list (blocks / transformer_blocks / layers / block)")
@@ -89,6 +95,17 @@ def apply_streaming(dit, device="cuda", resident_blocks=0, prefetch_slots=2, pin
     for i in resident_idx:
         blocks[i].to(device)
     owner = object()
+    if chunk:
+        if ram_blocks is not None and ram_blocks < len(stream_idx):
+            raise ValueError("chunk streaming keeps every streamed block in RAM (no SSD tier)")
+        if not double_buffer:
+            raise ValueError("chunk streaming is double-buffered")
+        state = _build_chunk_state(owner, device, [blocks[i] for i in stream_idx], chunk_bytes, chunk_slots,
+                                   pin_memory, order_cache)
+        _install_first_block_hook(dit, blocks[0], state, owner)
+        _install_chunk_hooks(dit, state, owner)
+        setattr(dit, _STATE_ATTR, state)
+        return StreamedModel(dit, state, resident_idx, stream_idx, owner)
     ssd = None
     if model_file is None and ram_blocks is not None and ram_blocks < len(stream_idx):
         from ..core.tiers.plan import ssd_positions

@@ -115,6 +115,63 @@ def _build_state(owner, device, blocks, prefetch_slots=2, pin_memory=True, profi
     return state
 
 
+def _build_chunk_state(owner, device, blocks, chunk_bytes=None, num_slots=None, pin_memory=True, order_cache=None):
+    """Capture + chunk streaming state (streaming/load_steps.py:736-753 of the reference): the blocks' host flats as
+    for block streaming; the GPU holds ``num_slots`` chunk slots (WEIGHTFERRY_CHUNK_SLOTS, default 4) of at most
+    ``chunk_bytes`` of layers each (WEIGHTFERRY_CHUNK_MB, default 96 MB) plus a spare, sized once the first forward
+    has shown the blocks' call order."""
+    from .chunk_state import _ChunkState
+    specs = _check_block_layouts(blocks)
+    offsets, flat_bytes = _flat_layout(specs)
+    holders, host_flats, host_views = _capture_streamed_blocks(blocks, specs, offsets, flat_bytes, pin_memory)
+    rest = []
+    for blk, views in zip(blocks, host_views):
+        for p, v in zip(blk.parameters(), views):
+            p.data = v
+        rest.append(views)
+    if chunk_bytes is None:
+        chunk_bytes = int(float(_env.get("WEIGHTFERRY_CHUNK_MB")) * 1024 ** 2)
+    if num_slots is None:
+        num_slots = int(_env.get("WEIGHTFERRY_CHUNK_SLOTS"))
+    state = _ChunkState(owner, device, list(blocks), host_flats, host_views, rest, specs, offsets, chunk_bytes,
+                        num_slots, order_cache)
+    state.holders = holders
+    state.flat_bytes = flat_bytes
+    state.disk_store = None
+    return state
+
+
+def _install_chunk_hooks(dit, state, owner):
+    """Chunk streaming: pre / post hooks on every streamed block and on each of its leaf modules
+    (streaming/load_steps.py:359-397); block hooks first, so a block that owns parameters itself starts before its
+    own leaf hook runs."""
+    def make_block_hooks(cur_s):
+        def block_pre(module, args):
+            if getattr(dit, _ACTIVE_ATTR, None) is owner:
+                state.block_pre(cur_s)
+
+        def block_post(module, args, output):
+            if getattr(dit, _ACTIVE_ATTR, None) is owner:
+                state.block_post(cur_s)
+        return block_pre, block_post
+
+    def leaf_pre(module, args):
+        if getattr(dit, _ACTIVE_ATTR, None) is owner:
+            state.leaf_pre(module)
+
+    def leaf_post(module, args, output):
+        if getattr(dit, _ACTIVE_ATTR, None) is owner:
+            state.leaf_post(module)
+
+    for s_idx, blk in enumerate(state.streaming_blocks):
+        pre_h, post_h = make_block_hooks(s_idx)
+        state.handles.append(blk.register_forward_pre_hook(pre_h))
+        state.handles.append(blk.register_forward_hook(post_h))
+        for leaf_mod in state.leaf_modules[s_idx].values():
+            state.handles.append(leaf_mod.register_forward_pre_hook(leaf_pre))
+            state.handles.append(leaf_mod.register_forward_hook(leaf_post))
+
+
 def _install_first_block_hook(dit, first_block, state, owner):
     """Pre-hook of the model's first block: the prefetch of the first slots, only when block 0 really runs."""
     def first_block_pre_hook(module, args):

@@ -10,12 +10,18 @@ registers
     ON_LOAD (a clone switch).
 Block 0 stays resident (resident_blocks >= 1), as in the reference.
 
+WEIGHTFERRY_CHUNK=1 streams chunks of blocks instead of whole blocks (streaming.chunk_state; the reference's
+dit_node.py:215-246): the GPU holds WEIGHTFERRY_CHUNK_SLOTS chunks of WEIGHTFERRY_CHUNK_MB of layers, the call
+order learned at the first load is kept with the node for later loads, and with resident_blocks <= 1 block 0
+streams too (WEIGHTFERRY_CHUNK_BLOCK0=0 keeps it resident). Chunk mode needs Double Buffer and the RAM tier; with
+either missing the node streams whole blocks.
+
 Tiering "Auto" puts the streamed blocks over the RAM budget (``ram_budget_gb``; 0: the available RAM minus
 WEIGHTFERRY_RAM_MARGIN_GB, see core.tiers.plan.plan_tiers) on the SSD tier:
 read straight from the GGUF model file named by WEIGHTFERRY_MODEL_FILE (ComfyUI-GGUF's loaded tensors do not carry
 their file's path), or else from a cache file of their captured bytes (WEIGHTFERRY_CACHE_DIR). Options of the reference that belong to other paths -- SageAttention, fp8 storage format,
-self-managed residents, auto-configuration, the VRAM budget, chunk streaming -- are accepted and logged as not
-applied; the node then streams as with their defaults."""
+self-managed residents, auto-configuration, the VRAM budget -- are accepted and logged as not applied; the node
+then streams as with their defaults."""
 import math
 
 from ..core import env as _env
@@ -113,21 +119,33 @@ class WeightFerryDiT:
         if len(blocks) == 0:
             log_warn(f"DiT Layer Streaming: no transformer block list on {type(dit).__name__}, skipping.")
             return (patcher,)
-        resident_k = max(1, min(len(blocks), int(resident_blocks)))
+        double = buffer_mode != BUFFER_SINGLE
+        env_tier = _env.get("WEIGHTFERRY_TIERING")
+        tier_auto = (env_tier == "auto") if env_tier else tiering == TIERING_AUTO
+        chunk = _env.get("WEIGHTFERRY_CHUNK") == "1"
+        if chunk and (not double or tier_auto):
+            log_info("DiT Layer Streaming [chunks]: chunk streaming needs Double Buffer and the RAM tier; "
+                     "streaming whole blocks.")
+            chunk = False
+        # chunk mode streams block 0 as well when it has the other blocks' layout (the reference's stream_block0)
+        uniform0 = len(blocks) > 1 and [(tuple(p.shape), p.dtype) for p in blocks[0].parameters()] == \
+            [(tuple(p.shape), p.dtype) for p in blocks[1].parameters()]
+        stream_block0 = (chunk and uniform0 and int(resident_blocks) <= 1
+                         and _env.get("WEIGHTFERRY_CHUNK_BLOCK0") != "0")
+        resident_k = 0 if stream_block0 else max(1, min(len(blocks), int(resident_blocks)))
         num_stream = len(blocks) - resident_k
         if num_stream <= 0:
             log_info("DiT Layer Streaming: All blocks resident, no streaming offload registered.")
             return (patcher,)
-        double = buffer_mode != BUFFER_SINGLE
-        env_tier = _env.get("WEIGHTFERRY_TIERING")
-        tier_auto = (env_tier == "auto") if env_tier else tiering == TIERING_AUTO
+        order_cache = {}                      # the learned chunk call order, kept with this node for later loads
         env_budget = _env.get("WEIGHTFERRY_RAM_BUDGET_GB")
         budget = float(env_budget) if env_budget else float(ram_budget_gb)
         model_file = _env.get("WEIGHTFERRY_MODEL_FILE") if tier_auto else None
         owner = object()
         log_info(f"DiT Layer Streaming: Registering Late Offload ({resident_k}/{len(blocks)} resident, {num_stream} "
                  f"streaming blocks, pin_memory={pin_memory}, double_buffer={double}, "
-                 f"prefetch_slots={prefetch_slots if double else 1}, tiering={'auto' if tier_auto else 'ram'})...")
+                 f"prefetch_slots={prefetch_slots if double else 1}, tiering={'auto' if tier_auto else 'ram'}"
+                 f"{', chunks' if chunk else ''})...")
 
         def on_load(p, device_to, lowvram_model_memory, force_patch_weights, full_load):
             dev = device_to if device_to is not None else p.load_device
@@ -135,6 +153,14 @@ class WeightFerryDiT:
                 return
             _teardown(dit)                    # a previous capture of this model (or another config's)
             ram_blocks, depth = None, 2
+            if chunk:
+                sm = dit_node.apply_streaming(dit, device=dev, resident_blocks=resident_k, pin_memory=pin_memory,
+                                              chunk=True, order_cache=order_cache)
+                sm.owner_node = owner
+                setattr(dit, _NODE_ATTR, sm)
+                log_info(f"DiT Layer Streaming [Late Offload]: {num_stream} blocks offloaded to pinned RAM, "
+                         f"streamed in chunks.")
+                return
             if tier_auto:
                 from ..core.tiers.plan import plan_tiers
                 per = sum(q.numel() * q.element_size() for q in blocks[resident_k].parameters())

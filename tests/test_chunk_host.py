@@ -1,0 +1,214 @@
+"""Chunk (sub-block) streaming on the CPU (no GPU), driven through the recording stand-in for the library's streams,
+events and copies of test_streaming_host (a copy runs when its stream runs; a stream runs only past waits whose
+events have been recorded, so a missing fence shows up as a layer computing with the wrong bytes). The protocol is
+the reference's streaming/chunk_state.py:124-392: the first forward learns the call order, later forwards copy
+chunk units into rotating slots behind slot-free events; layers out of order go through a spare."""
+import pytest
+import torch
+
+from conftest import sub
+from test_streaming_host import FakeNative
+
+
+class Leaf(torch.nn.Module):
+    """A layer whose forward records the first and last value of its weight (its tag when the bytes are right)."""
+
+    def __init__(self, tag, n, seen):
+        super().__init__()
+        self.tag, self.seen = tag, seen
+        self.w = torch.nn.Parameter(torch.full((n,), float(tag)), requires_grad=False)
+
+    def forward(self, x):
+        self.seen.append((self.tag, float(self.w[0]), float(self.w[-1])))
+        return x + 1
+
+
+class Blk(torch.nn.Module):
+    """Four layers registered a, b, c, d and called in ``order`` (the Cosmos blocks' registration and call orders
+    differ too)."""
+
+    def __init__(self, i, seen, order, n=64):
+        super().__init__()
+        self.a, self.b = Leaf(10 * (i + 1) + 1, n, seen), Leaf(10 * (i + 1) + 2, n, seen)
+        self.c, self.d = Leaf(10 * (i + 1) + 3, n, seen), Leaf(10 * (i + 1) + 4, n, seen)
+        self.order = order
+
+    def forward(self, x):
+        for name in self.order:
+            x = getattr(self, name)(x)
+        return x
+
+
+class Model(torch.nn.Module):
+    def __init__(self, n, seen, order="cadb", odd=None, outside=False, skip=()):
+        super().__init__()
+        self.blocks = torch.nn.ModuleList(Blk(i, seen, odd[1] if odd and i == odd[0] else order) for i in range(n))
+        self.outside, self.skip = outside, set(skip)
+
+    def forward(self, x):
+        if self.outside:
+            x = self.blocks[0].c(x)          # a layer of block 0 called before any block runs
+        for i, b in enumerate(self.blocks):
+            if i not in self.skip:
+                x = b(x)
+        return x
+
+
+@pytest.fixture
+def fake(monkeypatch):
+    fn = FakeNative()
+    state_mod = sub("streaming.state")
+    chunk_mod = sub("streaming.chunk_state")
+    monkeypatch.setattr(state_mod, "_native", fn)
+    monkeypatch.setattr(chunk_mod, "_native", fn)
+    monkeypatch.setattr(state_mod._StreamState, "compute_stream", lambda self: 1)
+    fn.L.queues[1] = []
+    ls_mod = sub("streaming.load_steps")
+    dn = sub("streaming.dit_node")
+    orig = ls_mod._install_chunk_hooks
+
+    def install(dit, state, owner):
+        orig(dit, state, owner)
+        # the compute stream runs its queue whenever a layer is about to compute
+        for mods in state.leaf_modules:
+            for m in mods.values():
+                m.register_forward_pre_hook(lambda mod, a: fn.run_all())
+    monkeypatch.setattr(dn, "_install_chunk_hooks", install)
+    return fn
+
+
+def _check(seen, expect_tags):
+    assert [s[0] for s in seen] == expect_tags
+    for tag, w0, w1 in seen:
+        assert (w0, w1) == (tag, tag), seen
+
+
+def _tags(n, order, skip=(), outside=False, odd=None):
+    idx = {"a": 1, "b": 2, "c": 3, "d": 4}
+    out = [13] if outside else []
+    for i in range(n):
+        if i in skip:
+            continue
+        o = odd[1] if odd and i == odd[0] else order
+        out += [10 * (i + 1) + idx[ch] for ch in o]
+    return out
+
+
+@pytest.mark.parametrize("slots", [2, 3])
+def test_learns_call_order_and_binds_the_right_bytes(fake, slots):
+    dn = sub("streaming.dit_node")
+    seen = []
+    model = Model(5, seen)
+    cache = {}
+    sm = dn.apply_streaming(model, device="cpu", pin_memory=False, chunk=True, chunk_bytes=512, chunk_slots=slots,
+                            order_cache=cache)
+    st = sm.state
+    assert st.calibrating
+    for fwd in range(3):
+        seen.clear()
+        sm(torch.zeros(1))
+        fake.run_all()
+        _check(seen, _tags(5, "cadb"))
+        # after the forward every parameter is bound to its host view again
+        for blk, views in zip(model.blocks, st.host_views):
+            assert all(p.data.data_ptr() == v.data_ptr() for p, v in zip(blk.parameters(), views))
+        if fwd == 0:
+            assert not st.calibrating
+            assert st.order == ["c", "a", "d", "b"] and cache["order"] == st.order
+            assert st.types == [["c", "a"], ["d", "b"]]
+            assert len(st.chunk_slots) == slots and len(st.spares) == 1
+    assert st.spare_uses == 0
+    # parameters a..d are indices 0..3: unit [c, a] is two runs ({0}, {2}), so two copies per unit
+    assert [len(plan[0]) for plan in st.type_plan] == [2, 2]
+
+
+def test_every_copy_waits_for_its_slots_previous_unit(fake):
+    dn = sub("streaming.dit_node")
+    seen = []
+    model = Model(4, seen, order="abcd")
+    sm = dn.apply_streaming(model, device="cpu", pin_memory=False, chunk=True, chunk_bytes=512, chunk_slots=2)
+    sm(torch.zeros(1))                        # calibration
+    fake.run_all()
+    st = sm.state
+    # registration order = call order: each unit is one run, one copy
+    assert [len(plan[0]) for plan in st.type_plan] == [1, 1]
+    fake.L.issued.clear()
+    seen.clear()
+    sm(torch.zeros(1))
+    fake.run_all()
+    _check(seen, _tags(4, "abcd"))
+    copy_stream = st.prefetch_stream.handle
+    ops = [op for op in fake.L.issued if op[0] == copy_stream]
+    slot_of = {b.data_ptr(): k for k, b in enumerate(st.chunk_slots)}
+    copies = [i for i, op in enumerate(ops) if op[1] == "copy"]
+    assert len(copies) == 4 * 2               # 4 blocks x 2 units, one run each
+    for i in copies:
+        k = slot_of[ops[i][2]]
+        assert ops[i - 1][1] == "wait" and ops[i - 1][2] == st.slot_free_events[k].handle
+    # the compute stream waits for each unit's copy before its first layer
+    waits = [op[2] for op in fake.L.issued if op[0] == 1 and op[1] == "wait"]
+    assert waits == [e.handle for e in st.unit_events]
+
+
+def test_out_of_order_layers_use_a_spare(fake):
+    dn = sub("streaming.dit_node")
+    seen = []
+    # one layer per unit, two slots: block 2 calls d first, while the rotating slots still hold its c and a units
+    model = Model(5, seen, order="cadb", odd=(2, "dcab"))
+    sm = dn.apply_streaming(model, device="cpu", pin_memory=False, chunk=True, chunk_bytes=256, chunk_slots=2)
+    for _ in range(3):
+        seen.clear()
+        sm(torch.zeros(1))
+        fake.run_all()
+        _check(seen, _tags(5, "cadb", odd=(2, "dcab")))
+    assert sm.state.types == [["c"], ["a"], ["d"], ["b"]]
+    assert sm.state.spare_uses == 2             # once in each chunked forward
+
+
+def test_skipped_block_and_outside_layer(fake):
+    dn = sub("streaming.dit_node")
+    seen = []
+    model = Model(6, seen, outside=True, skip=(3,))
+    sm = dn.apply_streaming(model, device="cpu", pin_memory=False, chunk=True, chunk_bytes=512, chunk_slots=2)
+    for _ in range(3):
+        seen.clear()
+        sm(torch.zeros(1))
+        fake.run_all()
+        _check(seen, _tags(6, "cadb", skip=(3,), outside=True))
+
+
+def test_order_cache_skips_calibration(fake, monkeypatch):
+    dn = sub("streaming.dit_node")
+    seen = []
+    cache = {"order": ["c", "a", "d", "b"]}
+    sm = dn.apply_streaming(Model(3, seen), device="cpu", pin_memory=False, chunk=True, chunk_bytes=512,
+                            chunk_slots=2, order_cache=cache)
+    assert not sm.state.calibrating and sm.state.types == [["c", "a"], ["d", "b"]]
+    sm(torch.zeros(1))
+    fake.run_all()
+    _check(seen, _tags(3, "cadb"))
+    # a stale order (unknown layer names) or the recalibrate flag: learned again
+    sm2 = dn.apply_streaming(Model(3, []), device="cpu", pin_memory=False, chunk=True, chunk_bytes=512,
+                             chunk_slots=2, order_cache={"order": ["x"]})
+    assert sm2.state.calibrating
+    monkeypatch.setenv("WEIGHTFERRY_CHUNK_RECALIBRATE", "1")
+    sm3 = dn.apply_streaming(Model(3, []), device="cpu", pin_memory=False, chunk=True, chunk_bytes=512,
+                             chunk_slots=2, order_cache=dict(cache))
+    assert sm3.state.calibrating
+
+
+def test_chunk_types_cut_by_bytes():
+    chunk = sub("streaming.chunk_state")
+    specs = [((64,), torch.float32)] * 3 + [((1000,), torch.float32)]
+    offsets = [0, 256, 512, 768]
+    runs, where, total = chunk._runs([3, 0, 1], specs, offsets)
+    # indices 0, 1 are one run (their padding included), 3 another, placed at the next 256-byte boundary
+    assert runs == [(0, 0, 512), (768, 512, 4000)] and where == {0: 0, 1: 256, 3: 512} and total == 4608
+
+
+def test_chunk_mode_rejects_ssd_and_single_buffer():
+    dn = sub("streaming.dit_node")
+    with pytest.raises(ValueError):
+        dn.apply_streaming(Model(3, []), device="cpu", pin_memory=False, chunk=True, ram_blocks=1)
+    with pytest.raises(ValueError):
+        dn.apply_streaming(Model(3, []), device="cpu", pin_memory=False, chunk=True, double_buffer=False)

@@ -1,8 +1,9 @@
 """The WeightFerryDiT node on the GPU through a stand-in ModelPatcher (ON_LOAD / ON_DETACH callbacks and the
 DIFFUSION_MODEL wrapper, as ComfyUI calls them): every forward is bit-identical to the same stack resident on the GPU
 (the reference's criterion, tests/test_streaming.py:222) -- after a load, twice; when ComfyUI skipped ON_LOAD (lazy
-capture in the wrapper); with Single Buffer; after a re-load; and with tiering Auto putting blocks over the RAM
-budget on the SSD tier (read from the GGUF file). A detach gives the weights back on the CPU."""
+capture in the wrapper); with Single Buffer; after a re-load; with tiering Auto putting blocks over the RAM
+budget on the SSD tier (read from the GGUF file); and in chunk mode (WEIGHTFERRY_CHUNK=1, block 0 streamed too, the
+learned call order reused by a re-load). A detach gives the weights back on the CPU."""
 import pytest
 import torch
 
@@ -129,3 +130,22 @@ def test_tiering_auto_without_a_model_file_uses_a_cache_file(native, comfy, tmp_
     assert len(sm.state.disk_index) == 8 and sm.state.disk_store is not None     # ring of 4 and 1 block in RAM
     _check(mp, x, ctx, ref, times=2)
     mp.detach()
+
+
+def test_chunk_mode_streams_block0_and_reuses_the_order(native, comfy, reference, monkeypatch):
+    x, ctx, ref = reference
+    node = sub("streaming.node")
+    monkeypatch.setenv("WEIGHTFERRY_CHUNK", "1")
+    monkeypatch.setenv("WEIGHTFERRY_CHUNK_MB", "0.3")
+    model = _stack()
+    mp = node.WeightFerryDiT().apply_streaming(fake_comfy.FakeModelPatcher(model), resident_blocks=1)[0]
+    mp.load()
+    sm = getattr(model, node._NODE_ATTR)
+    assert len(sm.stream_idx) == 6 and sm.state.chunk_mode and sm.state.calibrating
+    _check(mp, x, ctx, ref, times=3)
+    mp.load()                                   # a re-load: chunked from its first forward
+    sm = getattr(model, node._NODE_ATTR)
+    assert not sm.state.calibrating and sm.state.n_types >= 3
+    _check(mp, x, ctx, ref, times=2)
+    mp.detach()
+    assert all(p.device.type == "cpu" for b in model.blocks for p in b.parameters())

@@ -161,3 +161,56 @@ def test_gguf_linear_fused_matches_dequant_flow(native):
         assert err <= 1e-2
         # not the fused kernel's case: float32 activations go through the two-step flow
         assert fg.fused_linear(x.float(), lin.weight, qtype, (768, 512)) is None
+
+
+@pytest.mark.parametrize("slots,chunk_kb", [(2, 300), (4, 300), (2, 160)])
+def test_chunk_streamed_forward_equals_resident(native, slots, chunk_kb):
+    # chunk (sub-block) streaming: the first forward learns the call order (copies on the compute stream), the
+    # next two stream chunk units through `slots` rotating slots; every forward bit-identical to the resident stack
+    dn = sub("streaming.dit_node")
+    x, ctx = _inputs()
+    resident = _small_stack(mode="auto").cuda()
+    with torch.no_grad():
+        ref = resident(x, ctx)
+    streamed = _small_stack(mode="auto")
+    cache = {}
+    sm = dn.apply_streaming(streamed, device="cuda", chunk=True, chunk_bytes=chunk_kb * 1024, chunk_slots=slots,
+                            order_cache=cache)
+    try:
+        for _ in range(3):
+            with torch.no_grad():
+                y = sm(x, ctx)
+            torch.cuda.synchronize()
+            assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+            for blk in streamed.blocks:
+                assert all(p.device.type == "cpu" for p in blk.parameters())
+        st = sm.state
+        assert cache["order"] == ["q", "k", "v", "o", "cq", "ck", "cv", "co", "up", "down"]
+        assert st.n_types >= 3 and len(st.chunk_slots) == slots and st.spare_uses == 0
+        # registration order = call order: one copy per unit
+        assert all(len(plan[0]) == 1 for plan in st.type_plan)
+    finally:
+        sm.teardown()
+
+
+def test_chunk_streaming_skipped_block_and_learned_order_reused(native):
+    dn = sub("streaming.dit_node")
+    x, ctx = _inputs()
+    resident = Skipping(_small_stack(mode="auto").cuda(), skip=(2,))
+    with torch.no_grad():
+        ref = resident(x, ctx)
+    cache = {}
+    for load in range(2):
+        streamed = Skipping(_small_stack(mode="auto"), skip=(2,))
+        sm = dn.apply_streaming(streamed, device="cuda", chunk=True, chunk_bytes=300 * 1024, chunk_slots=2,
+                                order_cache=cache)
+        try:
+            # the second load starts chunked: the order the first one learned is reused
+            assert sm.state.calibrating == (load == 0)
+            for _ in range(2):
+                with torch.no_grad():
+                    y = sm(x, ctx)
+                torch.cuda.synchronize()
+                assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+        finally:
+            sm.teardown()
