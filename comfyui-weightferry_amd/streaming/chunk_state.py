@@ -63,6 +63,8 @@ class _ChunkState(_StreamState):
         self.chunk_bytes = int(chunk_bytes)
         self.n_chunk_slots = max(2, int(num_slots))
         names = [n for n, _ in streaming_blocks[0].named_parameters()]
+        if not names:
+            raise ValueError("chunk streaming needs blocks with parameters")
         self.leaf_params = {}
         for j, n in enumerate(names):
             self.leaf_params.setdefault(n.rpartition(".")[0], []).append(j)
