@@ -172,6 +172,17 @@ def fused_leg(torch, native):
     return res
 
 
+def _resident_check(torch, sm, model, x, ctx, y_stream, dev):
+    """The reference's criterion for streaming (tests/test_streaming.py:222, torch.equal): tear the streaming down
+    with the blocks' weights moved onto the GPU, run the same forward resident and compare it with the last streamed
+    output bit for bit."""
+    sm.teardown(device=dev)
+    with torch.no_grad():
+        y_res = model(x, ctx)
+    torch.cuda.synchronize()
+    return bool(torch.equal(y_res.view(torch.int16), y_stream.view(torch.int16)))
+
+
 def streaming_leg(torch, native, n_blocks=40, steps=10):
     """40 Wan-14B blocks with Q4_K weights streamed from pinned host memory through 2 GPU slots (4096 tokens)."""
     syn = importlib.import_module(PKG + ".streaming.synthetic")
@@ -190,7 +201,7 @@ def streaming_leg(torch, native, n_blocks=40, steps=10):
         ms = _timed(torch, lambda: sm(x, ctx), steps, 1)
         sm.state.profiler = prof_mod._StreamProfiler(n_blocks, sm.state.flat_bytes, True)
         for _ in range(3):
-            sm(x, ctx)
+            y_stream = sm(x, ctx)
     torch.cuda.synchronize()
     prof = sm.profile_summary()["mean_excluding_first_forward"]
     flat = sm.state.flat_bytes
@@ -204,10 +215,11 @@ def streaming_leg(torch, native, n_blocks=40, steps=10):
     b.record(st.prefetch_stream.handle)
     b.synchronize()
     raw_ms = a.elapsed_ms(b) / 5
-    sm.teardown(device="cpu")
+    identical = _resident_check(torch, sm, model, x, ctx, y_stream, dev)
     del model, sm
     torch.cuda.empty_cache()
     return {"ms_per_step": round(ms, 2), "blocks": n_blocks, "slots": 2, "bytes_per_block": flat,
+            "bit_identical_to_resident": identical,
             "h2d_GBps_effective": round(flat * n_blocks / (ms / 1e3) / 1e9, 2),
             "raw_h2d_GBps": round(flat / (raw_ms / 1e3) / 1e9, 2),
             "copy_floor_ms_per_step": round(n_blocks * raw_ms, 1),
@@ -238,13 +250,14 @@ def chunk_leg(torch, native, n_blocks=40, steps=5, chunk_mb=96, slots=4):
         torch.cuda.synchronize()
         calib_ms = (time.perf_counter() - t) * 1e3
         ms = _timed(torch, lambda: sm(x, ctx), steps, 1)
+        y_stream = sm(x, ctx)
     st = sm.state
     res = {"ms_per_step": round(ms, 2), "calibration_forward_ms": round(calib_ms, 1), "blocks": n_blocks,
            "chunk_mb": chunk_mb, "slots": slots, "chunks_per_block": st.n_types,
            "chunk_slot_bytes": st.slot_bytes, "gpu_weight_bytes": st.slot_bytes * (slots + len(st.spares)),
            "block_mode_gpu_weight_bytes": 2 * st.flat_bytes, "spare_uses": st.spare_uses,
            "h2d_GBps_effective": round(st.flat_bytes * n_blocks / (ms / 1e3) / 1e9, 2)}
-    sm.teardown(device="cpu")
+    res["bit_identical_to_resident"] = _resident_check(torch, sm, model, x, ctx, y_stream, dev)
     del model, sm
     torch.cuda.empty_cache()
     return res

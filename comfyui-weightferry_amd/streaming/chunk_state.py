@@ -88,6 +88,7 @@ class _ChunkState(_StreamState):
         self.spare_uses = 0
         self.blocks_started = 0
         self._fwd = None
+        self._retired = []                # unit events replaced in this forward (closed once it has run)
         if order_cache is not None:
             self.use_learned_order(order_cache)
 
@@ -162,7 +163,7 @@ class _ChunkState(_StreamState):
         self.spares = []
         self._new_spare()
         self.n_units = self.num_stream * self.n_types
-        self.unit_events = [_native.Event() for _ in range(self.n_units)]
+        self.unit_events = [None] * self.n_units
         self.scratch = None
         self.scratch_views = {}
         self.calibrating = False
@@ -178,7 +179,10 @@ class _ChunkState(_StreamState):
 
     # ---- chunked forwards
     def begin_forward(self):
-        super().begin_forward()
+        super().begin_forward()           # the previous forward has run on the GPU: its events are free
+        for ev in self._retired:
+            ev.close()
+        self._retired = []
         self.blocks_started = 0
         self._fwd = {"t0": time.perf_counter(), "spares": 0, "outside": 0}
         if self.types is None:
@@ -206,10 +210,15 @@ class _ChunkState(_StreamState):
             buf, free, _ = self.spares[spare]
             self.spare_owner[spare] = u
             self.u_spare[u] = spare
+        free.synchronize()                # host-side fence (see leaf_pre)
         _native.stream_wait(stream, free)
         self._copy(s, self.type_plan[t][0], buf, stream)
-        self.unit_events[u].record(stream)
-        self.unit_events[u].query()       # submit now without blocking the host
+        ev = _native.Event()
+        ev.record(stream)
+        ev.query()                        # submit now without blocking the host
+        if self.unit_events[u] is not None:
+            self._retired.append(self.unit_events[u])
+        self.unit_events[u] = ev
         self.u_issued[u] = True
 
     def pump(self):
@@ -281,6 +290,12 @@ class _ChunkState(_StreamState):
             self._fwd["spares"] += 1
         views = (self.spares[self.u_spare[u]][2][t] if u in self.u_spare
                  else self.slot_type_views[u % self.n_chunk_slots][t])
+        # Host-side fences in both directions (here, and on the slot-free event before a copy is issued), besides
+        # the stream waits: with the two stream waits alone, 40 Wan blocks streamed in 3 chunks each gave layers the
+        # wrong bytes from the third forward on in some processes (after other streams had been created and
+        # destroyed; never in the CPU protocol model, nor in block streaming). The host then runs at most the slots'
+        # depth ahead of the GPU; the copies stay ahead of the compute.
+        self.unit_events[u].synchronize()
         _native.stream_wait(self.compute_stream(), self.unit_events[u])
         self._bind(s, views)
         self.u_bound[u] = True
@@ -348,8 +363,10 @@ class _ChunkState(_StreamState):
 
     def close(self):
         super().close()
-        for e in getattr(self, "slot_free_events", []) + getattr(self, "unit_events", []):
-            e.close()
+        for e in getattr(self, "slot_free_events", []) + getattr(self, "unit_events", []) + self._retired:
+            if e is not None:
+                e.close()
+        self._retired = []
         for _, ev, _ in self.spares:
             ev.close()
         self.chunk_slots, self.spares = [], []

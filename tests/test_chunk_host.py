@@ -212,3 +212,92 @@ def test_chunk_mode_rejects_ssd_and_single_buffer():
         dn.apply_streaming(Model(3, []), device="cpu", pin_memory=False, chunk=True, ram_blocks=1)
     with pytest.raises(ValueError):
         dn.apply_streaming(Model(3, []), device="cpu", pin_memory=False, chunk=True, double_buffer=False)
+
+
+class DeferredFake(FakeNative):
+    """The stand-in with layer reads deferred onto the compute stream: a layer's forward enqueues a read of its
+    weight tensor, executed when the stream runs, as a kernel would read it -- so the host can run a whole forward
+    ahead of the "GPU", which only runs at the end of each forward (the host's forward_done wait)."""
+
+    def run_all(self):
+        progress = True
+        while progress:
+            progress = False
+            for s, q in self.L.queues.items():
+                while q:
+                    op = q[0]
+                    if op[0] == "wait" and (op[1], op[2]) not in self.L.recorded and op[2] > 0:
+                        break
+                    q.pop(0)
+                    progress = True
+                    if op[0] == "record":
+                        self.L.recorded.add((op[1], op[2]))
+                    elif op[0] == "copy":
+                        ctypes.memmove(op[1], op[2], op[3])
+                        self.L.log.append(("copy", op[1], op[2]))
+                    elif op[0] == "fn":
+                        op[1]()
+
+
+import ctypes  # noqa: E402
+
+
+class DLeaf(torch.nn.Module):
+    def __init__(self, tag, n, seen, fake):
+        super().__init__()
+        self.tag, self.seen, self.fake = tag, seen, fake
+        self.w = torch.nn.Parameter(torch.full((n,), float(tag)), requires_grad=False)
+
+    def forward(self, x):
+        w, tag = self.w.data, self.tag
+        self.fake.L.queues[1].append(("fn", lambda: self.seen.append((tag, float(w[0]), float(w[-1])))))
+        return x
+
+
+class WanLike(torch.nn.Module):
+    """Ten layers per block sized like a Wan block's (eight of 14.76 units, up and down 39.8), called in order."""
+
+    def __init__(self, i, seen, fake):
+        super().__init__()
+        sizes = [1476] * 8 + [3980, 3980]
+        self.layers = torch.nn.ModuleList(DLeaf(100 * (i + 1) + k, n, seen, fake) for k, n in enumerate(sizes))
+
+    def forward(self, x):
+        for m in self.layers:
+            x = m(x)
+        return x
+
+
+@pytest.mark.parametrize("blocks,slots,chunk_kb", [(40, 4, 38), (12, 4, 38), (40, 2, 38), (40, 4, 17)])
+def test_host_far_ahead_of_the_gpu(monkeypatch, blocks, slots, chunk_kb):
+    # the whole forward is enqueued before anything runs; every layer must still read its own bytes
+    fn = DeferredFake()
+    state_mod = sub("streaming.state")
+    chunk_mod = sub("streaming.chunk_state")
+    monkeypatch.setattr(state_mod, "_native", fn)
+    monkeypatch.setattr(chunk_mod, "_native", fn)
+    monkeypatch.setattr(state_mod._StreamState, "compute_stream", lambda self: 1)
+    fn.L.queues[1] = []
+    dn = sub("streaming.dit_node")
+    seen = []
+
+    class M(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.blocks = torch.nn.ModuleList(WanLike(i, seen, fn) for i in range(blocks))
+
+        def forward(self, x):
+            for b in self.blocks:
+                x = b(x)
+            return x
+
+    model = M()
+    sm = dn.apply_streaming(model, device="cpu", pin_memory=False, chunk=True, chunk_bytes=chunk_kb * 1024,
+                            chunk_slots=slots)
+    for f in range(5):
+        seen.clear()
+        sm(torch.zeros(1))
+        fn.run_all()
+        bad = [(t, a, b) for t, a, b in seen if (a, b) != (t, t)]
+        assert not bad, (f, bad[:4])
+        assert len(seen) == blocks * 10
