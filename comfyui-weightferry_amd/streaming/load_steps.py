@@ -201,7 +201,9 @@ def _install_block_stream_hooks(dit, state, owner):
                     state.issue_prefetch(cur_s)      # the prefetch chain was broken (a block was skipped)
                 state.wait_transfer(cur_s)
                 if prof is not None:
-                    prof.record(cur_s, "wait0", compute)
+                    prof.record(cur_s, "wait0", compute)   # before the host fence: the GPU's idle time counts as stall
+                if state.host_fence:
+                    state.transferred_events[cur_s].synchronize()
                 from .. import _native
                 _native.stream_wait(compute, state.transferred_events[cur_s])
             else:
