@@ -580,7 +580,7 @@ def _traffic():
 def main():
     args = _args()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+        print(f"bench.py: runs on one GPU; --gpus {args.gpus} is not supported "
               "(the one-GPU throughput is the reported value)", file=sys.stderr)
         sys.exit(2)
     sys.path.insert(0, ROOT)

@@ -730,7 +730,7 @@ static int check_blocks(const char* who, const void* src, int64_t src_bytes, int
         return WF_EUNSUPPORTED;
     }
     if (n_values > (int64_t)1 << 40) {   // keeps every tiled launch under 2^31 workgroups
-        set_error("%s: %lld values is beyond this build's limit of 2^40", who, (long long)n_values);
+        set_error("%s: %lld values is beyond the kernels' limit of 2^40", who, (long long)n_values);
         return WF_EUNSUPPORTED;
     }
     if (n_values && (!src || !out)) { set_error("%s: null pointer", who); return WF_EINVAL; }

@@ -498,7 +498,7 @@ extern "C" int wf_linear_i8(const int8_t* xq, const int8_t* wq, const float* xs,
         return WF_EUNSUPPORTED;
     }
     if (M >= (1LL << 31) || N >= (1LL << 31) || K >= (1LL << 31) || M * N >= (1LL << 62)) {
-        set_error("wf_linear_i8: sizes beyond this build's 32-bit tile indices");
+        set_error("wf_linear_i8: sizes beyond the kernels' 32-bit tile indices");
         return WF_EUNSUPPORTED;
     }
     // int32 accumulation is exact when K * 128 * 128 < 2^31

@@ -104,7 +104,7 @@ class WeightFerryDiT:
             ("resident_mode=self-managed", resident_mode == RESIDENT_MODE_SELF), ("auto_config", auto_config),
             ("vram_budget_gb", bool(vram_budget_gb)), ("text encoder streaming", _text_encoder)) if on]
         if not_applied:
-            log_info(f"DiT Layer Streaming: not part of this build, not applied: {', '.join(not_applied)}.")
+            log_info(f"DiT Layer Streaming: not part of this package, not applied: {', '.join(not_applied)}.")
         if _text_encoder:
             return (model,)
         patcher = model.clone()

@@ -11,7 +11,7 @@
  *   - LoRA add (_deq_add)         enhancers/gguf_dequant.py:99-133,387-409
  *   - int8 row quantiser          enhancers/fused_kernels.py:44-49,65-81,137-174
  *   - quantiser operations (PRE)  enhancers/fused_kernels.py:14-18,84-136,143-163; enhancers/fused_int8.py:28-39,94-105
- *   - int8 linear epilogue        enhancers/fused_int8.py:191-206 (order of the epilogue fixed by this build)
+ *   - int8 linear epilogue        enhancers/fused_int8.py:191-206 (the epilogue order is defined here)
  *
  * Build: gcc -O2 -fPIC -shared -ffp-contract=off -fno-fast-math (see oracle/Makefile). No FMA contraction: every
  * product and sum is rounded on its own, as the reference's kernels launched with enable_fp_fusion=False.
@@ -304,7 +304,8 @@ int wfo_linear_i8(const int8_t* xq, const int8_t* wq, const float* xs, const flo
 
 /* out = R_OUT(f32(resid) + f32(gate[n]) * ((f32(acc) * xs[m]) * ws[n])), the role of kitchen's
  * cutlass_int8_dequant_residual (enhancers/fused_int8.py:212-268; x_res + gate * linear(x) per group of
- * rows_per_group rows, gate [groups, N]). Epilogue order: this build's definition. bf16 operands only. */
+ * rows_per_group rows, gate [groups, N]). Epilogue order: (f32(acc) * xs[m]) * ws[n], then the residual. bf16
+ * operands only. */
 int wfo_linear_i8_residual(const int8_t* xq, const int8_t* wq, const float* xs, const float* ws,
                            const uint16_t* gate, const uint16_t* resid, uint16_t* out,
                            int64_t M, int64_t N, int64_t K, int64_t rows_per_group) {
