@@ -1,6 +1,6 @@
 """ORACLE -- test infrastructure only, never the product.
 
-CPU restatements of WeightFerry's quantized-weight hot path, used as the checker:
+CPU restatements of WeightFerry's quantized-weight hot path, against which the tests hold the GPU kernels:
 
 * ``lib``         -- ctypes binding of ``wf_oracle.c`` (scalar C restatement; the reference's flat-index formulas,
                      enhancers/gguf_dequant.py:72-256, enhancers/fused_kernels.py:84-174).
