@@ -308,13 +308,15 @@ def ssd_leg(torch, native, n_blocks=40, ram_blocks=20, steps=3):
         n_disk = len(sm.state.disk_index)
         with torch.no_grad():
             ms = _timed(torch, lambda: sm(x, ctx), steps, 1)
+            y_stream = sm(x, ctx)
         st = sm.state.ring.stats()
-        sm.teardown(device="cpu")
+        identical = _resident_check(torch, sm, model, x, ctx, y_stream, dev)
     finally:
         os.remove(path)
     del model
     torch.cuda.empty_cache()
     return {"file_GB": round(size / 1e9, 3), "ring_raw_read": reads, "ms_per_step": round(ms, 1),
+            "bit_identical_to_resident": identical,
             "blocks": n_blocks, "ram_tier_blocks": n_blocks - n_disk, "ssd_tier_blocks": n_disk,
             "ssd_bytes_per_step": block_bytes * n_disk,
             "ssd_GBps_per_step": round(block_bytes * n_disk / (ms / 1e3) / 1e9, 2),
