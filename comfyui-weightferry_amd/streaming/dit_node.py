@@ -9,7 +9,7 @@ import torch
 
 from .common import _ACTIVE_ATTR, _STATE_ATTR, _blocks
 from .load_steps import (_build_chunk_state, _build_state, _install_block_stream_hooks, _install_chunk_hooks,
-                         _install_first_block_hook)
+                         _install_first_block_hook, _install_resident_profile_hooks)
 
 
 class StreamedModel:
@@ -133,5 +133,6 @@ def apply_streaming(dit, device="cuda", resident_blocks=0, prefetch_slots=2, pin
                          double_buffer)
     _install_first_block_hook(dit, blocks[0], state, owner)
     _install_block_stream_hooks(dit, state, owner)
+    _install_resident_profile_hooks(dit, blocks, resident_idx, state, owner)
     setattr(dit, _STATE_ATTR, state)
     return StreamedModel(dit, state, resident_idx, stream_idx, owner)

@@ -244,3 +244,23 @@ def _install_block_stream_hooks(dit, state, owner):
     for s_idx, blk in enumerate(state.streaming_blocks):
         state.handles.append(blk.register_forward_pre_hook(make_pre_hook(s_idx)))
         state.handles.append(blk.register_forward_hook(make_post_hook(s_idx)))
+
+
+def _install_resident_profile_hooks(dit, blocks, resident_idx, state, owner):
+    """Blocks kept on the GPU (not streamed): r_start / r_end events on the compute stream when the profiler is on,
+    so its summary separates their compute from the streamed blocks' and from idle time (the reference records
+    them in its resident-block hooks, streaming/profiler.py:59-61)."""
+    def make(b_idx):
+        def pre(module, args):
+            if state.profiler is not None and getattr(dit, _ACTIVE_ATTR, None) is owner:
+                state.profiler.record_resident(b_idx, "r_start", state.compute_stream())
+
+        def post(module, args, output):
+            if state.profiler is not None and getattr(dit, _ACTIVE_ATTR, None) is owner:
+                state.profiler.record_resident(b_idx, "r_end", state.compute_stream())
+        return pre, post
+
+    for b_idx in resident_idx:
+        pre, post = make(b_idx)
+        state.handles.append(blocks[b_idx].register_forward_pre_hook(pre))
+        state.handles.append(blocks[b_idx].register_forward_hook(post))

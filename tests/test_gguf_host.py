@@ -78,7 +78,7 @@ def test_kquant_gate(gd):
 
 
 def test_stats_reset(gd):
-    gd._state["stats"]["used"] = 5
+    gd._counts["used"] = 5
     assert gd.stats(reset=True)["used"] == 5
     assert gd.stats() == {"used": 0, "fallback": 0}
 
@@ -121,3 +121,64 @@ def test_get_weight_counts_lora_fallback(gd, fake_gguf):
     assert layer.get_weight(t, torch.bfloat16) == "host-get-weight"
     assert "lora_fallback" not in gd.stats()
     assert layer.get_weight(None, torch.bfloat16) is None
+
+
+def test_version_of_inference_tensor_is_none(gd):
+    # ComfyUI builds its tensors under torch.inference_mode: they have no version counter, and reading it raises
+    with torch.inference_mode():
+        t = torch.zeros(4, 4)
+    with pytest.raises(RuntimeError):
+        t._version
+    assert gd._version(t) is None
+    assert gd._version(torch.zeros(2)) == 0
+
+
+def test_pinned_factor_of_inference_tensor_is_reused_then_released(gd, monkeypatch):
+    # the page-locked copy is keyed by (storage, version, device); an inference-mode factor has version None and
+    # must still be cached and reused, then forgotten when the factor is collected and released on request
+    pinned_calls, emptied = [], []
+    monkeypatch.setattr(torch.Tensor, "pin_memory", lambda self: pinned_calls.append(1) or self.clone())
+    monkeypatch.setattr(torch._C, "_host_emptyCache", lambda: emptied.append(1), raising=False)
+    store = gd._PinnedFactors()
+    store._hooked = True                       # no ComfyUI here: nothing to hook
+    with torch.inference_mode():
+        up = torch.full((8, 4), 0.5, dtype=torch.bfloat16)
+    a = store.upload(up, "cpu")
+    b = store.upload(up, "cpu")
+    assert a.dtype == torch.float32 and torch.equal(a, b) and len(pinned_calls) == 1 and len(store) == 1
+    store.release()
+    assert emptied == []                      # nothing dropped yet
+    del up
+    import gc
+    gc.collect()
+    assert len(store) == 0
+    store.release()
+    store.release()
+    assert emptied == [1]
+
+
+def test_comfy_memory_calls_release_pinned_copies(gd, monkeypatch):
+    import types
+    import sys
+    calls = []
+    mm = types.ModuleType("comfy.model_management")
+    mm.free_memory = lambda *a, **k: calls.append(("free_memory", a, k)) or "freed"
+    mm.unload_all_models = lambda: calls.append(("unload_all_models",))
+    mm.soft_empty_cache = lambda force=False: calls.append(("soft_empty_cache", force))
+    comfy = types.ModuleType("comfy")
+    comfy.model_management = mm
+    monkeypatch.setitem(sys.modules, "comfy", comfy)
+    monkeypatch.setitem(sys.modules, "comfy.model_management", mm)
+    emptied = []
+    monkeypatch.setattr(torch._C, "_host_emptyCache", lambda: emptied.append(1), raising=False)
+    monkeypatch.setattr(gd._PINNED, "_hooked", False)
+    gd._hook_comfy_memory()
+    gd._hook_comfy_memory()                    # once only: no double wrapping
+    assert all(getattr(mm, n)._weightferry_cache for n in ("free_memory", "unload_all_models", "soft_empty_cache"))
+    assert not getattr(mm.free_memory.__wrapped__, "_weightferry_cache", False)
+    monkeypatch.setattr(gd._PINNED, "_freed", True)
+    assert mm.free_memory(3, "cuda", keep=1) == "freed"
+    assert emptied == [1] and calls[-1] == ("free_memory", (3, "cuda"), {"keep": 1})
+    mm.soft_empty_cache(True)
+    mm.unload_all_models()
+    assert emptied == [1] and [c[0] for c in calls] == ["free_memory", "soft_empty_cache", "unload_all_models"]

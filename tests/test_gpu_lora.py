@@ -134,3 +134,33 @@ def test_patched_get_weight_with_lora(native, fake_gguf):
         assert ok, where
     finally:
         gd.uninstall()
+
+
+def test_inference_mode_factors_use_the_kernel(native, fake_gguf):
+    # ComfyUI runs under torch.inference_mode and its LoRA factors are inference tensors (no version counter): the
+    # pinned-factor path must take them (lora_used), reuse their page-locked copies on the next call, and give the
+    # same bits as the oracle's chain
+    gd = sub("enhancers.gguf_dequant")
+    ops = fake_gguf
+    assert gd.install(force=True)
+    try:
+        n_out, n_in = 256, 512
+        raw = encode.encode(encode.weights((n_out, n_in), seed=4), 12)
+        g = torch.Generator().manual_seed(4)
+        with torch.inference_mode():
+            up, down = torch.randn((n_out, 8), generator=g), torch.randn((8, n_in), generator=g)
+            t = ops.GGMLTensor(torch.from_numpy(raw).cuda(), tensor_type=12, tensor_shape=torch.Size((n_out, n_in)),
+                               patches=[([_patch(up, down, 4.0, 0.75)], "key")])
+            gd.stats(reset=True)
+            held_before = len(gd._PINNED)
+            ys = [ops.GGMLLayer().get_weight(t, torch.bfloat16) for _ in range(2)]
+            torch.cuda.synchronize()
+        assert gd.stats().get("lora_used") == 2 and "lora_fallback" not in gd.stats()
+        assert len(gd._PINNED) == held_before + 2          # one page-locked copy per factor, reused by the 2nd call
+        loras = gd.lora_factors([_patch(up, down, 4.0, 0.75)], n_out, n_in)
+        expect = _expected(raw, 12, F16, BF16, n_out, n_in, loras)
+        for y in ys:
+            ok, where = _same(_bits(y, BF16), expect, BF16)
+            assert ok, where
+    finally:
+        gd.uninstall()

@@ -243,11 +243,22 @@ def test_profiler_summary_formulas():
     # two blocks: copies of 2 ms each, the first stalls compute 1 ms, the second not at all
     blocks = {0: {"dma0": E(0), "dma1": E(2), "ready": E(2), "wait0": E(0), "start": E(1), "end": E(4)},
               1: {"dma0": E(2), "dma1": E(4), "ready": E(4), "wait0": E(4), "start": E(4), "end": E(7)}}
-    p.forwards = [{"start": E(0), "end": E(8), "blocks": blocks, "cpu_hook_s": 0.0}]
-    s = p.summary()["per_forward"][0]
+    resident = {0: {"r_start": E(8), "r_end": E(9.5)}}
+    p.forwards = [prof_mod._Forward(start=E(0), end=E(10), blocks=blocks, resident=resident)]
+    summ = p.summary()
+    s = summ["per_forward"][0]
     assert s["dma_ms"] == 4 and s["stall_ms"] == 1 and s["streamed_compute_ms"] == 6
     assert s["overlap_ratio"] == 0.75                      # 1 - stall / transfer
     assert s["dma_gbps"] == round(1e6 * 2 / (4 / 1000) / 1e9, 2)
+    assert s["resident_compute_ms"] == 1.5 and s["compute_idle_ms"] == 10 - 6 - 1.5
+    tl = summ["timeline_one_forward"]
+    assert tl["streamed"]["1"]["start"] == 4 and tl["resident"]["0"]["r_end"] == 9.5 and tl["forward_ms"] == 10
+    # a stall longer than the copy clamps to 0 hidden; no copy at all gives no ratio and no rate
+    blocks[0]["start"] = E(6)
+    assert p.summary()["per_forward"][0]["overlap_ratio"] == 0.0
+    p.forwards = [prof_mod._Forward(start=E(0), end=E(1), blocks={0: {"start": E(0), "end": E(1)}})]
+    s = p.summary()["per_forward"][0]
+    assert s["overlap_ratio"] is None and s["dma_gbps"] is None
 
 
 def test_pinned_host_falls_back_without_gpu():
