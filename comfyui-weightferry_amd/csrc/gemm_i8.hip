@@ -51,8 +51,10 @@ __device__ __forceinline__ void tile_of(int w, int T, int ntm, int ntn, int& tm,
     tn = in / gm;
 }
 
-// Epilogue operands of the residual variant: out = OUT(resid + gate[m / rows_per_group] * t), t the plain epilogue
-// value before rounding (the role of kitchen's cutlass_int8_dequant_residual, enhancers/fused_int8.py:212-268).
+// Epilogue operands of the residual variant: out = bf16(resid + gate[m / rows_per_group] * bf16(t)), t the plain
+// epilogue value: the plain GEMM's bf16 output followed by torch's addcmul on bf16 tensors (the product of two bf16
+// values is exact in float32, the sum rounds once to float32, then to bf16). The reference states the same bits for
+// kitchen's cutlass_int8_dequant_residual (enhancers/fused_int8.py:212-268, enhancers/fused_block.py:24-26).
 struct Residual {
     const uint16_t* gate;    // bf16 [groups, N]
     const uint16_t* resid;   // bf16 [M, N]
@@ -168,7 +170,7 @@ __global__ __launch_bounds__(256) void gemm_i8(const int8_t* __restrict__ A, con
                 if constexpr (RESID) {
                     const float g = __uint_as_float((uint32_t)res.gate[(int64_t)(m / res.rows_per_group) * N + n] << 16);
                     const float r = __uint_as_float((uint32_t)res.resid[o] << 16);
-                    t = r + g * t;
+                    t = r + g * (float)(__bf16)t;
                 }
                 if constexpr (OUT == WF_BF16) {
                     static_cast<__bf16*>(out)[o] = (__bf16)t;
@@ -360,7 +362,7 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
         }
         return;
     }
-    // the residual form keeps float32 until its single rounding: element stores
+    // the residual form: element stores
 #pragma unroll
     for (int j = 0; j < WN; j++) {
         const int n = n0 + wn * WN * 32 + j * 32 + lr;
@@ -379,7 +381,7 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
                 if constexpr (RESID) {
                     const float g = __uint_as_float((uint32_t)res.gate[(int64_t)(m / res.rows_per_group) * N + n] << 16);
                     const float r = __uint_as_float((uint32_t)res.resid[o] << 16);
-                    t = r + g * t;
+                    t = r + g * (float)(__bf16)t;
                 }
                 if constexpr (OUT == WF_BF16) {
                     static_cast<__bf16*>(out)[o] = (__bf16)t;

@@ -9,9 +9,13 @@
 //   amax = min(max |y|, 3.38953139e38); scale = max(amax / 127, 1e-30) (stored as float32);
 //   q = clamp(rint(bf16(bf16(y) / bf16(scale))), -128, 127).
 //
-// One wave per row, the row held in registers. ConvRot: a lane loads 16 consecutive values of a 256-group (the
-// two lowest radix-4 digits), runs stages 1 and 4 on them, exchanges through LDS so that it then holds the 16 values
-// that share its two lowest digits (stride 16), and runs stages 16 and 64. The quotient y / s is computed with a
+// A row is held in registers by one wave (rows up to 6144 values in ConvRot mode, 8192 plain; four rows per
+// 256-thread workgroup) or by the four waves of a workgroup (wider rows, up to 32768 values; the waves' partial
+// maxima meet in LDS -- the maximum does not depend on the order it is taken in, so the bits do not depend on the
+// split). ConvRot: a lane loads 16 consecutive values of a 256-group (the two lowest radix-4 digits), runs stages 1
+// and 4 on them, exchanges through LDS so that it then holds the 16 values that share its two lowest digits
+// (stride 16), and runs stages 16 and 64. Groups are independent until the row maximum, so a wave may take any of
+// them: pass p of wave w of a row takes groups 4 (p W + w) .. 4 (p W + w) + 3, W waves per row. The quotient y / s is computed with a
 // correctly rounded reciprocal of s (one IEEE division per row) and one Markstein correction step -- mul, then two
 // fma -- which is the correctly rounded IEEE quotient for every normal result (subnormal quotients round to 0 in the
 // integer anyway). Built without contraction; the fma calls are explicit.
@@ -52,6 +56,23 @@ __device__ __forceinline__ int8_t quant1(float y, float sb, float rsb) {
     float v = __builtin_rintf(round_bf16(div_rn(round_bf16(y), sb, rsb)));
     v = fminf(fmaxf(v, -128.0f), 127.0f);
     return (int8_t)(int)v;
+}
+
+// the row's maximum over its W waves (W = 1: the wave's own); every lane of the W waves gets it. W > 1 needs the
+// whole workgroup to be one row (no wave leaves early), since it takes a workgroup barrier.
+template <int W>
+__device__ __forceinline__ float row_max(float wave_amax, int wave) {
+    if constexpr (W == 1) {
+        return wave_amax;
+    } else {
+        __shared__ float part[W];
+        if ((threadIdx.x & 63) == 0) part[wave] = wave_amax;
+        __syncthreads();
+        float m = part[0];
+#pragma unroll
+        for (int i = 1; i < W; i++) m = fmaxf(m, part[i]);
+        return m;
+    }
 }
 
 struct RowScale {
@@ -124,41 +145,42 @@ __device__ __forceinline__ void ln_stats(const uint16_t* xr, int K, int lane, fl
 }
 
 // ------------------------------------------------------------------------------------------------ plain rows
-// CPL chunks of 8 values per lane (chunk c of the row at lane + 64 * i): K <= 512 * CPL, K % 8 == 0.
-template <int CPL>
+// W waves per row, CPL chunks of 8 values per lane: chunk c = (i W + w) 64 + lane of the row for wave w, i < CPL.
+// K <= 512 W CPL, K % 8 == 0. W = 1: four rows per workgroup; W = 4: one.
+template <int CPL, int W>
 __global__ __launch_bounds__(256) void quant_plain(const uint16_t* __restrict__ x, int64_t M, int K,
                                                    int8_t* __restrict__ xq, float* __restrict__ xs) {
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= M) return;                       // whole waves leave together; no block barrier below
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, w = wave % W;
+    const int64_t row = (int64_t)blockIdx.x * (4 / W) + wave / W;
+    if (W == 1 && row >= M) return;             // whole waves leave together; W = 1 takes no workgroup barrier
     const uint4* xr = reinterpret_cast<const uint4*>(x + row * K);
     const int nchunks = K >> 3;
     uint4 v[CPL];
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < CPL; i++) {
-        const int c = lane + 64 * i;
+        const int c = (i * W + w) * 64 + lane;
         v[i] = c < nchunks ? xr[c] : make_uint4(0, 0, 0, 0);
-        const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+        const uint32_t u[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
         for (int h = 0; h < 4; h++) {
-            amax = fmaxf(amax, fabsf(bf16_bits_to_f32(w[h] & 0xffffu)));
-            amax = fmaxf(amax, fabsf(bf16_bits_to_f32(w[h] >> 16)));
+            amax = fmaxf(amax, fabsf(bf16_bits_to_f32(u[h] & 0xffffu)));
+            amax = fmaxf(amax, fabsf(bf16_bits_to_f32(u[h] >> 16)));
         }
     }
-    const RowScale rs = row_scale(wave_max(amax));
-    if (lane == 0) xs[row] = rs.scale;
+    const RowScale rs = row_scale(row_max<W>(wave_max(amax), wave));
+    if (lane == 0 && w == 0) xs[row] = rs.scale;
     uint2* qr = reinterpret_cast<uint2*>(xq + row * K);
 #pragma unroll
     for (int i = 0; i < CPL; i++) {
-        const int c = lane + 64 * i;
+        const int c = (i * W + w) * 64 + lane;
         if (c >= nchunks) continue;
-        const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+        const uint32_t u[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
         uint32_t b[2] = {0, 0};
 #pragma unroll
         for (int h = 0; h < 4; h++) {
-            const uint32_t lo = (uint8_t)quant1(bf16_bits_to_f32(w[h] & 0xffffu), rs.sb, rs.rsb);
-            const uint32_t hi = (uint8_t)quant1(bf16_bits_to_f32(w[h] >> 16), rs.sb, rs.rsb);
+            const uint32_t lo = (uint8_t)quant1(bf16_bits_to_f32(u[h] & 0xffffu), rs.sb, rs.rsb);
+            const uint32_t hi = (uint8_t)quant1(bf16_bits_to_f32(u[h] >> 16), rs.sb, rs.rsb);
             b[h >> 1] |= (lo | (hi << 8)) << (16 * (h & 1));
         }
         qr[c] = make_uint2(b[0], b[1]);
@@ -179,16 +201,16 @@ __device__ __forceinline__ void h4(float& a, float& b, float& c, float& d) {
 // for both the contiguous and the stride-16 access)
 __device__ __forceinline__ int slot(int g, int i) { return g * 272 + i + (i >> 4); }
 
-// NP passes of 4 groups (1024 values) per wave: K <= 1024 * NP, K % 256 == 0. Lane t of a pass owns group
-// 4p + t / 16, position tl = t % 16.
-template <int NP, int PRE>
+// W waves per row, NP passes of 4 groups (1024 values) per wave: K <= 1024 W NP, K % 256 == 0. Lane t of pass p
+// of wave w owns group 4 (p W + w) + t / 16, position tl = t % 16. W = 1: four rows per workgroup; W = 4: one.
+template <int NP, int PRE, int W>
 __global__ __launch_bounds__(256) void quant_convrot(const uint16_t* __restrict__ x, int64_t M, int K,
                                                      int8_t* __restrict__ xq, float* __restrict__ xs, PreArgs pa) {
     __shared__ float stage[4][4 * 272];          // per wave: one 4-group window
-    __shared__ uint32_t qbytes[4][NP * 256];     // per wave: the int8 row, 4 bytes a word
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + wave;
-    if (row >= M) return;                        // whole waves leave together; only wave barriers below
+    __shared__ uint32_t qbytes[4][256];          // per wave: the 1024 int8 values of one pass, 4 bytes a word
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, w = wave % W;
+    const int64_t row = (int64_t)blockIdx.x * (4 / W) + wave / W;
+    if (W == 1 && row >= M) return;              // whole waves leave together; W = 1 takes no workgroup barrier
     const int G = K >> 8;                        // groups in the row
     const int gl = lane >> 4, tl = lane & 15;
     float* st = stage[wave];
@@ -203,24 +225,24 @@ __global__ __launch_bounds__(256) void quant_convrot(const uint16_t* __restrict_
     }
 #pragma unroll
     for (int p = 0; p < NP; p++) {
-        const int g = 4 * p + gl;
+        const int g = 4 * (p * W + w) + gl;
         const bool live = g < G;
         // 16 consecutive values [16 tl, 16 tl + 16) of group g: digits k0 (stride 1) and k1 (stride 4)
         float v[16];
         if (live) {
             const uint4* src = reinterpret_cast<const uint4*>(x + row * K + g * 256 + 16 * tl);
             const uint4 a = src[0], b = src[1];
-            const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
             for (int h = 0; h < 8; h++) {
-                v[2 * h] = bf16_bits_to_f32(w[h] & 0xffffu);
-                v[2 * h + 1] = bf16_bits_to_f32(w[h] >> 16);
+                v[2 * h] = bf16_bits_to_f32(u[h] & 0xffffu);
+                v[2 * h + 1] = bf16_bits_to_f32(u[h] >> 16);
             }
             if constexpr (PRE == 1) {
 #pragma unroll
                 for (int h = 0; h < 8; h++) {
-                    v[2 * h] = bf16_bits_to_f32(pa.s[w[h] & 0xffffu]);
-                    v[2 * h + 1] = bf16_bits_to_f32(pa.s[w[h] >> 16]);
+                    v[2 * h] = bf16_bits_to_f32(pa.s[u[h] & 0xffffu]);
+                    v[2 * h + 1] = bf16_bits_to_f32(pa.s[u[h] >> 16]);
                 }
             } else if constexpr (PRE >= 2) {
                 const int64_t o = grp * K + g * 256 + 16 * tl;
@@ -266,46 +288,82 @@ __global__ __launch_bounds__(256) void quant_convrot(const uint16_t* __restrict_
         }
         __builtin_amdgcn_wave_barrier();
     }
-    const RowScale rs = row_scale(wave_max(amax));
-    if (lane == 0) xs[row] = rs.scale;
-    // quantise, put each byte at its row position in LDS, then write the row with 16-byte stores
+    const RowScale rs = row_scale(row_max<W>(wave_max(amax), wave));
+    if (lane == 0 && w == 0) xs[row] = rs.scale;
+    // per pass: quantise into the wave's LDS words at the bytes' row positions, then store the pass's 1024 bytes
+    // (four whole groups, contiguous in the row) with one 16-byte store per lane
     uint8_t* qb = reinterpret_cast<uint8_t*>(qbytes[wave]);
-#pragma unroll
-    for (int p = 0; p < NP; p++) {
-        const int g = 4 * p + gl;
-        if (g >= G) continue;
-#pragma unroll
-        for (int m = 0; m < 16; m++) qb[g * 256 + tl + 16 * m] = (uint8_t)quant1(y[p][m], rs.sb, rs.rsb);
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
     const uint4* qs = reinterpret_cast<const uint4*>(qbytes[wave]);
     uint4* dst = reinterpret_cast<uint4*>(xq + row * K);
-    for (int c = lane; c < (K >> 4); c += 64) dst[c] = qs[c];
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        const int g0 = 4 * (p * W + w);
+        if (g0 >= G) break;                      // the same for the whole wave
+        if (g0 + gl < G) {
+#pragma unroll
+            for (int m = 0; m < 16; m++) qb[gl * 256 + tl + 16 * m] = (uint8_t)quant1(y[p][m], rs.sb, rs.rsb);
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_wave_barrier();
+        if (g0 + (lane >> 4) < G) dst[g0 * 16 + lane] = qs[lane];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_s_waitcnt(0);           // the pass's LDS reads done before the next pass writes
+        __builtin_amdgcn_wave_barrier();
+    }
 }
 
-template <int CPL>
+// widest rows taken: 32768 values (one workgroup of four waves per row)
+constexpr int kMaxRowK = 32768;
+
+template <int CPL, int W>
 static void launch_plain(const uint16_t* x, int64_t M, int K, int8_t* xq, float* xs, hipStream_t s) {
-    quant_plain<CPL><<<dim3((unsigned)((M + 3) / 4)), 256, 0, s>>>(x, M, K, xq, xs);
+    quant_plain<CPL, W><<<dim3((unsigned)((M + 4 / W - 1) / (4 / W))), 256, 0, s>>>(x, M, K, xq, xs);
 }
 
-template <int NP, int PRE>
+static void launch_plain_rows(const uint16_t* x, int64_t M, int K, int8_t* xq, float* xs, hipStream_t s) {
+    if (K <= 8192) {                                   // one wave per row
+        const int cpl = (K + 511) / 512;
+        if (cpl <= 2) launch_plain<2, 1>(x, M, K, xq, xs, s);
+        else if (cpl <= 4) launch_plain<4, 1>(x, M, K, xq, xs, s);
+        else if (cpl <= 8) launch_plain<8, 1>(x, M, K, xq, xs, s);
+        else if (cpl <= 10) launch_plain<10, 1>(x, M, K, xq, xs, s);
+        else launch_plain<16, 1>(x, M, K, xq, xs, s);
+    } else {                                           // four waves per row: 2048 values per chunk step
+        const int cpl = (K + 2047) / 2048;
+        if (cpl <= 6) launch_plain<6, 4>(x, M, K, xq, xs, s);
+        else if (cpl <= 8) launch_plain<8, 4>(x, M, K, xq, xs, s);
+        else if (cpl <= 12) launch_plain<12, 4>(x, M, K, xq, xs, s);
+        else launch_plain<16, 4>(x, M, K, xq, xs, s);
+    }
+}
+
+template <int NP, int PRE, int W>
 static void launch_convrot_pre(const uint16_t* x, int64_t M, int K, int8_t* xq, float* xs, const PreArgs& pa,
                                hipStream_t s) {
-    quant_convrot<NP, PRE><<<dim3((unsigned)((M + 3) / 4)), 256, 0, s>>>(x, M, K, xq, xs, pa);
+    quant_convrot<NP, PRE, W><<<dim3((unsigned)((M + 4 / W - 1) / (4 / W))), 256, 0, s>>>(x, M, K, xq, xs, pa);
 }
 
 template <int PRE>
 static void launch_convrot(const uint16_t* x, int64_t M, int K, int8_t* xq, float* xs, const PreArgs& pa,
                            hipStream_t s) {
-    const int np = (K + 1023) / 1024;
-    if (np <= 1) launch_convrot_pre<1, PRE>(x, M, K, xq, xs, pa, s);
-    else if (np <= 2) launch_convrot_pre<2, PRE>(x, M, K, xq, xs, pa, s);
-    else if (np <= 3) launch_convrot_pre<3, PRE>(x, M, K, xq, xs, pa, s);
-    else if (np <= 4) launch_convrot_pre<4, PRE>(x, M, K, xq, xs, pa, s);
-    else if (np <= 5) launch_convrot_pre<5, PRE>(x, M, K, xq, xs, pa, s);
-    else launch_convrot_pre<6, PRE>(x, M, K, xq, xs, pa, s);
+    if (K <= 6144) {                                   // one wave per row, 1024 values per pass
+        const int np = (K + 1023) / 1024;
+        if (np <= 1) launch_convrot_pre<1, PRE, 1>(x, M, K, xq, xs, pa, s);
+        else if (np <= 2) launch_convrot_pre<2, PRE, 1>(x, M, K, xq, xs, pa, s);
+        else if (np <= 3) launch_convrot_pre<3, PRE, 1>(x, M, K, xq, xs, pa, s);
+        else if (np <= 4) launch_convrot_pre<4, PRE, 1>(x, M, K, xq, xs, pa, s);
+        else if (np <= 5) launch_convrot_pre<5, PRE, 1>(x, M, K, xq, xs, pa, s);
+        else launch_convrot_pre<6, PRE, 1>(x, M, K, xq, xs, pa, s);
+    } else {                                           // four waves per row, 4096 values per pass
+        const int np = (K + 4095) / 4096;
+        if (np <= 2) launch_convrot_pre<2, PRE, 4>(x, M, K, xq, xs, pa, s);
+        else if (np <= 3) launch_convrot_pre<3, PRE, 4>(x, M, K, xq, xs, pa, s);
+        else if (np <= 4) launch_convrot_pre<4, PRE, 4>(x, M, K, xq, xs, pa, s);
+        else if (np <= 5) launch_convrot_pre<5, PRE, 4>(x, M, K, xq, xs, pa, s);
+        else if (np <= 6) launch_convrot_pre<6, PRE, 4>(x, M, K, xq, xs, pa, s);
+        else launch_convrot_pre<8, PRE, 4>(x, M, K, xq, xs, pa, s);
+    }
 }
 
 // the checks both entry points share
@@ -332,19 +390,16 @@ extern "C" int wf_quant_rows_i8(const void* x_bf16, int64_t M, int64_t K, int mo
     const uint16_t* xp = static_cast<const uint16_t*>(x_bf16);
     const int k = (int)K;
     if (mode == 0) {
-        if (K % 16 || K > 8192) {
-            set_error("wf_quant_rows_i8: plain mode needs K %% 16 == 0 and K <= 8192 (K = %lld)", (long long)K);
+        if (K % 16 || K > kMaxRowK) {
+            set_error("wf_quant_rows_i8: plain mode needs K %% 16 == 0 and K <= %d (K = %lld)", kMaxRowK,
+                      (long long)K);
             return WF_EUNSUPPORTED;
         }
-        const int cpl = (k + 511) / 512;
-        if (cpl <= 2) launch_plain<2>(xp, M, k, xq, xs, s);
-        else if (cpl <= 4) launch_plain<4>(xp, M, k, xq, xs, s);
-        else if (cpl <= 8) launch_plain<8>(xp, M, k, xq, xs, s);
-        else if (cpl <= 10) launch_plain<10>(xp, M, k, xq, xs, s);
-        else launch_plain<16>(xp, M, k, xq, xs, s);
+        launch_plain_rows(xp, M, k, xq, xs, s);
     } else if (mode == 1) {
-        if (K % 256 || K > 6144) {
-            set_error("wf_quant_rows_i8: ConvRot mode needs K %% 256 == 0 and K <= 6144 (K = %lld)", (long long)K);
+        if (K % 256 || K > kMaxRowK) {
+            set_error("wf_quant_rows_i8: ConvRot mode needs K %% 256 == 0 and K <= %d (K = %lld)", kMaxRowK,
+                      (long long)K);
             return WF_EUNSUPPORTED;
         }
         launch_convrot<0>(xp, M, k, xq, xs, PreArgs{nullptr, nullptr, 1, 0.0f}, s);
@@ -363,8 +418,9 @@ extern "C" int wf_quant_rows_i8_pre(const void* x_bf16, int64_t M, int64_t K, in
     const int rc = check_rows("wf_quant_rows_i8_pre", x_bf16, M, K, xq, xs);
     if (rc != WF_OK || M == 0) return rc;
     if (pre < 0 || pre > 3) { set_error("wf_quant_rows_i8_pre: operation %d", pre); return WF_EUNSUPPORTED; }
-    if (K % 256 || K > 6144 || (pre == 3 && K % 512)) {
-        set_error("wf_quant_rows_i8_pre: K = %lld (K %% 256 == 0, K <= 6144; LayerNorm K %% 512 == 0)", (long long)K);
+    if (K % 256 || K > kMaxRowK || (pre == 3 && K % 512)) {
+        set_error("wf_quant_rows_i8_pre: K = %lld (K %% 256 == 0, K <= %d; LayerNorm K %% 512 == 0)", (long long)K,
+                  kMaxRowK);
         return WF_EUNSUPPORTED;
     }
     if (pre >= 1 && !s_bf16) { set_error("wf_quant_rows_i8_pre: null pointer"); return WF_EINVAL; }

@@ -1,8 +1,11 @@
-"""Shared state of the int8 linear path: the per-thread pending input / shared quantisation / pending residual, and
-the per-part used / fallback counters (the reference's enhancers/fused_state.py)."""
+"""State shared by the int8 linear path (fused_int8) and its block adapter (int8_block): the installed parts and
+the methods they replaced, the per-thread pending input / shared quantisation / pending residual (``_tls.pre``,
+``_tls.qkv``, ``_tls.res``), and per-part counters of calls served here ("used") or left to ComfyUI ("fallback", with
+the first reason seen). The counters' shape is what ``stats()`` reports (the reference's enhancers/fused_state.py).
+"""
 import threading
 
-_state = {"parts": ("modq",), "orig": None}
+_state = {"parts": (), "orig": None}
 _stats = {}   # part -> {"used": n, "fallback": n, "why": first fallback reason}
 _tls = threading.local()
 

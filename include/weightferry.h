@@ -61,7 +61,7 @@ int wf_dequant_add(const void* src, int64_t src_bytes, int qtype, int mid_dt, in
  * Per-row int8 quantisation of bf16 activations: replaces the Triton `_quant_row` with PRE_NONE
  * (enhancers/fused_kernels.py:137-174, launched at enhancers/fused_int8.py:172-176) and kitchen's
  * quantize_int8_rowwise_convrot64 (enhancers/fused_int8.py:178-181). mode 0: plain per-token (K % 16 == 0,
- * K <= 8192); mode 1: ConvRot 256-groups (K % 256 == 0, K <= 6144). x: bf16 [M, K] row-major; xq: int8 [M, K];
+ * K <= 32768); mode 1: ConvRot 256-groups (K % 256 == 0, K <= 32768). x: bf16 [M, K] row-major; xq: int8 [M, K];
  * xs: float32 [M]. x and xq 16-byte aligned. */
 int wf_quant_rows_i8(const void* x_bf16, int64_t M, int64_t K, int mode, int8_t* xq, float* xs, void* stream);
 
@@ -72,7 +72,7 @@ int wf_quant_rows_i8(const void* x_bf16, int64_t M, int64_t K, int mode, int8_t*
  * bf16 [M / rows_per_group, K], row r using group r / rows_per_group (:28-39); 3 LNMOD: LayerNorm without affine
  * first -- mean and variance by the reference's Welford order (:84-136), rstd = 1 / sqrt(var + eps) correctly rounded
  * where the reference uses the NVIDIA approximation rsqrt.approx.f32 -- rounded to bf16, then MOD. K % 256 == 0,
- * K <= 6144 (LNMOD: K % 512 == 0); s / shift 16-byte aligned for MOD / LNMOD. */
+ * K <= 32768 (LNMOD: K % 512 == 0); s / shift 16-byte aligned for MOD / LNMOD. */
 int wf_quant_rows_i8_pre(const void* x_bf16, int64_t M, int64_t K, int pre, const void* s_bf16, const void* shift_bf16,
                          int64_t rows_per_group, float eps, int8_t* xq, float* xs, void* stream);
 
@@ -83,10 +83,11 @@ int wf_quant_rows_i8_pre(const void* x_bf16, int64_t M, int64_t K, int pre, cons
 int wf_linear_i8(const int8_t* xq, const int8_t* wq, const float* xs, const float* ws, const void* bias, void* out,
                  int out_dt, int64_t M, int64_t N, int64_t K, void* stream);
 
-/* out = bf16(resid + gate[m / rows_per_group] * ((float(acc) * xs[m]) * ws[n])), one product and one sum each
- * rounded in float32, then the single rounding to bf16: replaces kitchen's cutlass_int8_dequant_residual
- * (enhancers/fused_int8.py:212-268: x_res + gate * linear(x) per (batch, frame) group of rows). gate: bf16
- * [M / rows_per_group, N]; resid, out: bf16 [M, N]. */
+/* out = bf16(resid + gate[m / rows_per_group] * bf16((float(acc) * xs[m]) * ws[n])): wf_linear_i8's bf16 output
+ * followed by torch.addcmul(resid, gate, out) on bf16 tensors (the product exact in float32, the sum rounded once
+ * to float32, then to bf16) -- replaces kitchen's cutlass_int8_dequant_residual, which the reference states gives
+ * those bits (enhancers/fused_int8.py:212-268: x_res + gate * linear(x) per (batch, frame) group of rows;
+ * enhancers/fused_block.py:24-26). gate: bf16 [M / rows_per_group, N]; resid, out: bf16 [M, N]. */
 int wf_linear_i8_residual(const int8_t* xq, const int8_t* wq, const float* xs, const float* ws, const void* gate_bf16,
                           const void* resid_bf16, void* out_bf16, int64_t M, int64_t N, int64_t K,
                           int64_t rows_per_group, void* stream);

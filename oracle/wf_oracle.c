@@ -302,10 +302,11 @@ int wfo_linear_i8(const int8_t* xq, const int8_t* wq, const float* xs, const flo
     return 0;
 }
 
-/* out = R_OUT(f32(resid) + f32(gate[n]) * ((f32(acc) * xs[m]) * ws[n])), the role of kitchen's
- * cutlass_int8_dequant_residual (enhancers/fused_int8.py:212-268; x_res + gate * linear(x) per group of
- * rows_per_group rows, gate [groups, N]). Epilogue order: (f32(acc) * xs[m]) * ws[n], then the residual. bf16
- * operands only. */
+/* out = bf16(f32(resid) + f32(gate) * bf16((f32(acc) * xs[m]) * ws[n])): the plain linear's bf16 output, then
+ * torch.addcmul(resid, gate, out) on bf16 tensors (the product of two bf16 values is exact in float32; the sum is
+ * rounded once to float32). The role of kitchen's cutlass_int8_dequant_residual, whose bits the reference states
+ * equal that addcmul (enhancers/fused_int8.py:212-268; enhancers/fused_block.py:24-26); gate [groups, N], row m in
+ * group m / rows_per_group. bf16 operands only. */
 int wfo_linear_i8_residual(const int8_t* xq, const int8_t* wq, const float* xs, const float* ws,
                            const uint16_t* gate, const uint16_t* resid, uint16_t* out,
                            int64_t M, int64_t N, int64_t K, int64_t rows_per_group) {
@@ -316,7 +317,7 @@ int wfo_linear_i8_residual(const int8_t* xq, const int8_t* wq, const float* xs, 
             float t = ((float)(int32_t)acc * xs[m]) * ws[n];
             float g = u2f((uint32_t)gate[(m / rows_per_group) * N + n] << 16);
             float rv = u2f((uint32_t)resid[m * N + n] << 16);
-            float o = rv + g * t;
+            float o = rv + g * u2f(bf16_trick(f2u(t)));     /* addcmul on the bf16 GEMM output */
             out[m * N + n] = (uint16_t)(bf16_trick(f2u(o)) >> 16);
         }
     return 0;

@@ -44,10 +44,17 @@ def gpu_linear(native, xq, wq, xs, ws, bias=None, out_dtype=torch.bfloat16):
 
 
 @pytest.mark.parametrize("mode,K", [(0, 512), (0, 5120), (0, 8192), (0, 48), (1, 256), (1, 1280), (1, 5120),
-                                    (1, 6144)])
+                                    (1, 6144),
+                                    # rows wider than one wave holds: four waves per row
+                                    (0, 8208), (0, 13824), (0, 20480), (0, 32768), (1, 6400), (1, 8192),
+                                    (1, 13824), (1, 20480), (1, 32768)])
 def test_quant_rows_random(native, mode, K):
     g = torch.Generator().manual_seed(99 + K)
-    x = (torch.randn((257, K), generator=g) * 2).to(torch.bfloat16)
+    rows = 257 if K <= 8192 else 67
+    x = (torch.randn((rows, K), generator=g) * 2).to(torch.bfloat16)
+    # the row maximum in each of the four waves' parts in turn, so a wrong combination of partial maxima shows
+    for r in range(4):
+        x[r, (K // 4) * r + 3] = 40.0 + r
     xq, xs = gpu_quant(native, x.cuda(), mode)
     rq, rs = lib.quant_rows(x.view(torch.int16).numpy().view(np.uint16), mode)
     assert np.array_equal(xs.cpu().numpy().view(np.uint32), rs.view(np.uint32))
@@ -214,7 +221,8 @@ def gpu_quant_pre(native, x, pre, s=None, h=None, rows=1, eps=0.0):
 
 
 @pytest.mark.parametrize("pre", [0, 1, 2, 3])
-@pytest.mark.parametrize("K,groups,rows", [(1024, 3, 5), (5120, 2, 64), (6144, 1, 7)])
+@pytest.mark.parametrize("K,groups,rows", [(1024, 3, 5), (5120, 2, 64), (6144, 1, 7), (8192, 2, 9),
+                                           (13824, 3, 4), (20480, 1, 6)])
 def test_quant_rows_pre_against_oracle(native, pre, K, groups, rows):
     g = torch.Generator().manual_seed(pre * 100 + K)
     x = (torch.randn((groups * rows, K), generator=g) * 1.5).to(torch.bfloat16)
@@ -238,14 +246,15 @@ def test_quant_rows_pre_against_oracle(native, pre, K, groups, rows):
     assert bad.size == 0, bad[:8].tolist()
 
 
-@pytest.mark.parametrize("kind", ["mod", "gelu", "lnmod"])
-def test_pending_input_quantised_with_its_operation(native, kind):
+@pytest.mark.parametrize("kind,K", [("mod", 5120), ("gelu", 5120), ("lnmod", 4096), ("mod", 13824),
+                                    ("gelu", 20480), ("lnmod", 8192)])
+def test_pending_input_quantised_with_its_operation(native, kind, K):
     from fake_quant import FakeQT, Lin
     fi = sub("enhancers.fused_int8")
     fs = sub("enhancers.fused_state")
     fs.stats(reset=True)
     g = torch.Generator().manual_seed(21)
-    B, N, K = 2, 160, 5120
+    B, N = 2, 160
     src = (torch.randn((B, N, K), generator=g)).to(torch.bfloat16).cuda()
     scale = (torch.randn((B, 1, K), generator=g) * 0.2).to(torch.bfloat16).cuda()
     shift = (torch.randn((B, 1, K), generator=g) * 0.2).to(torch.bfloat16).cuda()
@@ -300,5 +309,33 @@ def test_tilings_bias_and_residual_whole_output(native, M, N):
     assert rc == 0, native.last_error()
     torch.cuda.synchronize()
     gr = gate.float().repeat_interleave(M // G, dim=0)
-    ref_r = (resid.float() + gr * t).to(torch.bfloat16)
+    ref_r = (resid.float() + gr * t.to(torch.bfloat16).float()).to(torch.bfloat16)
     assert torch.equal(y.cpu().view(torch.int16), ref_r.view(torch.int16))
+
+
+def test_pending_layernorm_at_a_width_that_is_not_a_power_of_two_is_materialised(native):
+    # LayerNorm is fused only where torch's own kernel splits rows like the restatement (powers of two): at 5120
+    # the layer quantises the real input (torch's layer_norm, then the scale-and-shift), counted as an "ln" fallback
+    from fake_quant import FakeQT, Lin
+    fi = sub("enhancers.fused_int8")
+    fs = sub("enhancers.fused_state")
+    fs.stats(reset=True)
+    g = torch.Generator().manual_seed(22)
+    B, N, K = 2, 96, 5120
+    src = torch.randn((B, N, K), generator=g).to(torch.bfloat16).cuda()
+    scale = (torch.randn((B, 1, K), generator=g) * 0.2).to(torch.bfloat16).cuda()
+    shift = (torch.randn((B, 1, K), generator=g) * 0.2).to(torch.bfloat16).cuda()
+    norm = torch.nn.LayerNorm(K, elementwise_affine=False, eps=1e-6)
+    w_q = torch.randint(-127, 128, (256, K), generator=g, dtype=torch.int64).to(torch.int8)
+    ws = torch.rand(256, generator=g) * 0.01
+    lin = Lin(FakeQT(w_q.cuda(), ws.cuda()))
+    with fi._Overrides([lin]):
+        pre = fi._set_pre(src, "lnmod", scale, shift, norm=norm)
+        y = lin(src)
+        fi._clear_pre()
+    torch.cuda.synchronize()
+    assert pre["used"] and fs.stats()["ln"]["fallback"] == 1 and fs.stats()["qkv"]["used"] == 1
+    real = norm(src) * (1 + scale) + shift
+    rq, rs = lib.quant_rows(_bits(real.reshape(-1, K)), 1)
+    expect = lib.linear_i8(rq, w_q.numpy(), rs, ws.numpy(), out_dt=lib.BF16)
+    assert np.array_equal(_bits(y.reshape(-1, 256)), expect)

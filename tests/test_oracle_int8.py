@@ -105,7 +105,7 @@ def test_linear_accumulator_and_epilogue():
 
 def test_residual_epilogue():
     rng = np.random.default_rng(4)
-    M, N, K, rows = 8, 32, 256, 4
+    M, N, K, rows = 64, 96, 256, 4
     xq = rng.integers(-128, 128, size=(M, K)).astype(np.int8)
     wq = rng.integers(-128, 128, size=(N, K)).astype(np.int8)
     xs = np.full(M, 0.01, np.float32)
@@ -116,8 +116,17 @@ def test_residual_epilogue():
     acc = torch.from_numpy(xq.astype(np.float64) @ wq.astype(np.float64).T).float()
     t = (acc * torch.from_numpy(xs)[:, None]) * torch.from_numpy(ws)[None, :]
     g = torch.from_numpy(_bits_to_f32(gate)).repeat_interleave(rows, 0)
-    ref = (torch.from_numpy(_bits_to_f32(resid)) + g * t).to(torch.bfloat16)
+    # the plain linear's bf16 output, then the gated residual in float32 (gate * out exact) rounded once to bf16
+    tb = t.to(torch.bfloat16).float()
+    ref = (torch.from_numpy(_bits_to_f32(resid)) + g * tb).to(torch.bfloat16)
     assert np.array_equal(got, ref.view(torch.int16).numpy().view(np.uint16))
+    # ... which is torch's own addcmul on the bf16 tensors, as the unfused block computes it
+    r16 = torch.from_numpy(_bits_to_f32(resid)).to(torch.bfloat16)
+    add = torch.addcmul(r16, g.to(torch.bfloat16), t.to(torch.bfloat16))
+    assert np.array_equal(got, add.view(torch.int16).numpy().view(np.uint16))
+    # and not the unrounded product: dropping the bf16 rounding of the linear's value changes some results
+    loose = (torch.from_numpy(_bits_to_f32(resid)) + g * t).to(torch.bfloat16)
+    assert not np.array_equal(got, loose.view(torch.int16).numpy().view(np.uint16))
 
 
 def test_rejects_bad_convrot_width():
