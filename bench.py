@@ -397,11 +397,25 @@ def dequant_leg(torch, native, raws, shapes, qtype, mid, out_dt, steps, warmup):
     return ms_step, ms_step / len(shapes), algo
 
 
+def probe_lib():
+    """libwf_probe.so, the byte-moving kernel the ceiling leg runs (measurement only: built from csrc/probe/ beside
+    the product library, never part of it)."""
+    import ctypes
+    path = os.path.join(ROOT, PKG, "lib", "libwf_probe.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built (make -C {PKG}/csrc)")
+    lib = ctypes.CDLL(path)
+    p, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.wfp_hbm_stream.argtypes, lib.wfp_hbm_stream.restype = [p, p, i64, i32, i32, p], i32
+    lib.wfp_last_error.argtypes, lib.wfp_last_error.restype = [], ctypes.c_char_p
+    return lib
+
+
 def hbm_stream_leg(torch, native, nbytes, reads, writes, steps, warmup):
-    """What HBM delivers to a kernel that only moves bytes (wf_hbm_stream: reads:writes 16-byte chunks per thread,
+    """What HBM delivers to a kernel that only moves bytes (wfp_hbm_stream: reads:writes 16-byte chunks per thread,
     non-temporal stores) for about `nbytes` per launch, with the dequant legs' rotation over ROTATE_BYTES. Returns
     (bytes per launch, mean us per launch)."""
-    lib = native.lib()
+    lib = probe_lib()
     dev = torch.device("cuda:0")
     stream = native.stream_of(dev)
     items = nbytes // (16 * (reads + writes))
@@ -413,9 +427,9 @@ def hbm_stream_leg(torch, native, nbytes, reads, writes, steps, warmup):
         t.fill_(1)
 
     def launch(r):
-        rc = lib.wf_hbm_stream(ins[r].data_ptr(), outs[r].data_ptr(), items, reads, writes, stream)
+        rc = lib.wfp_hbm_stream(ins[r].data_ptr(), outs[r].data_ptr(), items, reads, writes, stream)
         if rc != 0:
-            raise RuntimeError(native.last_error())
+            raise RuntimeError(lib.wfp_last_error().decode())
 
     for i in range(warmup):
         launch(i % rot)

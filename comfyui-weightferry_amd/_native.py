@@ -63,7 +63,6 @@ EXPORTS = {
     "wf_ring_stats": (_int, [_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
                              ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
     "wf_ring_close": (_int, [_p]),
-    "wf_hbm_stream": (_int, [_p, _p, _i64, _int, _int, _p]),
 }
 
 _lib = None

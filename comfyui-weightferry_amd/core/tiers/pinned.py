@@ -23,6 +23,7 @@ class PinnedHost:
     def __init__(self, nbytes, align=0):
         self.nbytes = int(nbytes)
         total = self.nbytes + int(align)
+        self._held = 0                 # bytes counted in registered_bytes() for this buffer
         self._ptr = None
         self._base = None
         self.registered = False
@@ -42,6 +43,7 @@ class PinnedHost:
             except Exception:  # noqa: BLE001 -- no GPU runtime at all
                 self._base = torch.empty(total, dtype=torch.uint8, device="cpu")
         if self.registered:
+            self._held = total
             with _LOCK:
                 _REGISTERED["bytes"] += total
                 _REGISTERED["count"] += 1
@@ -66,8 +68,9 @@ class PinnedHost:
             except Exception:  # noqa: BLE001 -- releasing at shutdown: nothing left to do
                 pass
             with _LOCK:
-                _REGISTERED["bytes"] -= self.nbytes
+                _REGISTERED["bytes"] -= self._held
                 _REGISTERED["count"] -= 1
+            self._held = 0
         self.registered = False
 
     def __del__(self):

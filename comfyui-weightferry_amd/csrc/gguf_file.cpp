@@ -13,6 +13,7 @@
 // The file is untrusted input: every count, length, dimension, type and offset is checked against the file size
 // before use, and a malformed file is an error (WF_EINVAL with a message), never a read past a buffer.
 #include <errno.h>
+#include <stdint.h>
 #include <fcntl.h>
 #include <string.h>
 #include <sys/stat.h>
@@ -243,7 +244,10 @@ bool parse(File& f) {
         const TypeGeom g = type_geom(t.type);
         if (g.block == 0) return c.fail("tensor of a GGML type this reader does not size");
         if (t.dims[0] % g.block != 0) return c.fail("row length not a whole number of blocks");
-        t.nbytes = elems / g.block * g.bytes;
+        const int64_t blocks = elems / g.block;
+        if (blocks > INT64_MAX / g.bytes) return c.fail("tensor byte count overflows");
+        t.nbytes = blocks * g.bytes;
+        if (t.nbytes <= 0) return c.fail("tensor of no bytes");
         if (off > (uint64_t)f.size) return c.fail("tensor offset beyond the file");
         t.offset = (int64_t)off;     // relative until the data section is known
         f.tensors.push_back(std::move(t));

@@ -174,12 +174,6 @@ int wf_ring_resync(void* ring);
 int wf_ring_stats(void* ring, double* read_s, double* wait_s, int64_t* bytes, int64_t* reads);
 int wf_ring_close(void* ring);
 
-/* Measurement only, with no counterpart in the reference: a kernel that moves `items` x 16 x (reads + writes)
- * bytes with no arithmetic -- thread t reads in[t + r * items] (16-byte chunks, r < reads) and writes
- * out[t + w * items] non-temporally (w < writes) -- so a benchmark can set a kernel's HBM rate beside what HBM
- * delivers for the same read:write mix and size. Mixes 1:0, 0:1, 1:1, 1:2 and 2:7; `out` is required (16 bytes at
- * least for the read-only mix, which may store one word there). */
-int wf_hbm_stream(const void* in, void* out, int64_t items, int reads, int writes, void* stream);
 
 #ifdef __cplusplus
 }

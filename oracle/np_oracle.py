@@ -208,3 +208,37 @@ def gemm_ref_f64(x, w, bias=None):
     if bias is not None:
         y = y + np.asarray(bias, dtype=np.float64)[None, :]
     return y
+
+
+# ----------------------------------------------------------------------------------- ConvRot row quantisation
+# Sum orders of one radix-4 stage (a, b, c, d) -> 4 outputs. "ltr" is the reference's: every output summed left
+# to right (enhancers/fused_block.py:40-43, enhancers/fused_kernels.py:65-81). The others are plausible slips
+# (pairwise sums, right-to-left) kept so tests can show which inputs tell the orders apart.
+_STAGE_ORDERS = {
+    "ltr": lambda a, b, c, d: (((a + b) + c) - d, ((a + b) - c) + d, ((a - b) + c) + d, ((-a + b) + c) + d),
+    "pair": lambda a, b, c, d: ((a + b) + (c - d), (a + b) + (d - c), (a - b) + (c + d), (b - a) + (c + d)),
+    "rtl": lambda a, b, c, d: (a + (b + (c - d)), a + (b + (d - c)), a + ((c + d) - b), ((b + c) + d) - a),
+}
+
+
+def quant_rows_convrot(x_bf16_bits, order="ltr"):
+    """The ConvRot-256 row quantisation of _quant_row with PRE_NONE (enhancers/fused_kernels.py:137-174) in numpy
+    float32, every operation rounded on its own: radix-4 stages of stride 1, 4, 16, 64 in the given sum order,
+    * 0.0625, amax clamped to 3.38953139e38, scale = max(amax / 127, 1e-30), q = clamp(rint(bf16(bf16(y) /
+    bf16(scale))), -128, 127) (IEEE division, ties to even). x: bf16 bits [M, K], K % 256 == 0.
+    Returns (int8 [M, K], float32 scales [M])."""
+    x = np.asarray(x_bf16_bits, dtype=np.uint16)
+    M, K = x.shape
+    y = (x.astype(np.uint32) << 16).view(np.float32).reshape(M, K // 256, 256)
+    fn = _STAGE_ORDERS[order]
+    with np.errstate(over="ignore", invalid="ignore"):
+        for S in (1, 4, 16, 64):
+            v = y.reshape(M, K // 256, 256 // (4 * S), 4, S)
+            outs = fn(v[:, :, :, 0], v[:, :, :, 1], v[:, :, :, 2], v[:, :, :, 3])
+            y = np.stack(outs, axis=3).astype(np.float32).reshape(M, K // 256, 256)
+        y = (y.reshape(M, K) * np.float32(0.0625)).astype(np.float32)
+        amax = np.minimum(np.abs(y).max(axis=1), np.float32(3.38953139e38)).astype(np.float32)
+        scale = np.maximum((amax / np.float32(127.0)).astype(np.float32), np.float32(1e-30)).astype(np.float32)
+        sb = bf16_bits_rule(scale)
+        q = np.rint(bf16_bits_rule((bf16_bits_rule(y) / sb[:, None]).astype(np.float32)))
+    return np.clip(q, -128, 127).astype(np.int8), scale

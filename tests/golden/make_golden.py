@@ -9,7 +9,10 @@ Contents (numpy .npz, no pickles):
 * quant_rows.npz: ``x`` (5 rows of 512 bf16 bits, incl. a zero row and ties), ``q_<mode>`` int8 and ``s_<mode>``
   float32 for mode 0 (plain per token) and 1 (ConvRot-256);
 * linear_i8.npz: ``xq`` [4, 64], ``wq`` [6, 64] int8, ``xs`` [4], ``ws`` [6] float32, ``y`` the bf16 bits and
-  ``acc`` the int32 accumulators."""
+  ``acc`` the int32 accumulators;
+* convrot_order.npz: ``x`` (6 rows of 256 bf16 bits spanning 24 binades, drawn so that summing a radix-4 stage in
+  any other order than left to right changes at least one int8 value of every row), ``q`` int8 and ``s`` float32
+  of the ConvRot quantisation."""
 import os
 import sys
 
@@ -19,7 +22,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 
-from oracle import lib  # noqa: E402
+from oracle import lib, np_oracle  # noqa: E402
 
 TYPES = [2, 3, 6, 7, 8, 10, 11, 12, 13, 14]
 TYPE_SIZE = {2: 18, 3: 20, 6: 22, 7: 24, 8: 34, 10: 84, 11: 110, 12: 144, 13: 176, 14: 210}
@@ -71,6 +74,24 @@ def main():
     ws = (rng.random(6) * 0.01).astype(np.float32)
     y, acc = lib.linear_i8(xq, wq, xs, ws, out_dt=lib.BF16, want_acc=True)
     np.savez_compressed(os.path.join(HERE, "linear_i8.npz"), xq=xq, wq=wq, xs=xs, ws=ws, y=y, acc=acc)
+    np.savez_compressed(os.path.join(HERE, "convrot_order.npz"), **convrot_order_rows())
+
+
+def convrot_order_rows(n=6, seed=11, candidates=20000):
+    """Rows whose ConvRot int8 result depends on the stage sum order: bf16 values of random sign and magnitude
+    2^U(-12, 12), kept when both other orders of np_oracle give a different int8 row than the left-to-right one."""
+    rng = np.random.default_rng(seed)
+    f = rng.choice([-1.0, 1.0], (candidates, 256)) * 2.0 ** rng.uniform(-12, 12, (candidates, 256))
+    u = f.astype(np.float32).view(np.uint32)
+    x = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    ltr, _ = np_oracle.quant_rows_convrot(x, "ltr")
+    keep = np.ones(candidates, dtype=bool)
+    for order in ("pair", "rtl"):
+        other, _ = np_oracle.quant_rows_convrot(x, order)
+        keep &= (other != ltr).any(axis=1)
+    rows = x[np.nonzero(keep)[0][:n]]
+    q, s = lib.quant_rows(rows, 1)
+    return {"x": rows, "q": q, "s": s}
 
 
 if __name__ == "__main__":

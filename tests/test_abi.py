@@ -78,14 +78,19 @@ def test_check_maps_codes():
         native.check(native.EHIP, "x")
 
 
-def test_hbm_stream_argument_checks_without_gpu():
+def test_probe_is_a_separate_library_with_its_own_checks():
+    # the benchmark's byte mover lives in libwf_probe.so: the product library does not export it
     native = sub("_native")
-    lib = native.lib()
+    assert not hasattr(native.lib(), "wf_hbm_stream") and not hasattr(native.lib(), "wfp_hbm_stream")
+    probe = ctypes.CDLL(os.path.join(ROOT, "comfyui-weightferry_amd", "lib", "libwf_probe.so"))
+    probe.wfp_hbm_stream.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_void_p]
+    probe.wfp_last_error.restype = ctypes.c_char_p
     buf = ctypes.create_string_buffer(4096)
     p16 = (ctypes.addressof(buf) + 15) // 16 * 16
-    assert lib.wf_hbm_stream(p16, p16, 0, 1, 2, None) == native.EINVAL
-    assert lib.wf_hbm_stream(p16, None, 4, 1, 0, None) == native.EINVAL
-    assert lib.wf_hbm_stream(None, p16, 4, 1, 2, None) == native.EINVAL
-    assert lib.wf_hbm_stream(p16 + 4, p16, 4, 1, 2, None) == native.EINVAL
-    assert lib.wf_hbm_stream(p16, p16, 4, 3, 5, None) == native.EUNSUPPORTED
-    assert "3:5" in native.last_error()
+    assert probe.wfp_hbm_stream(p16, p16, 0, 1, 2, None) == -1
+    assert probe.wfp_hbm_stream(p16, None, 4, 1, 0, None) == -1
+    assert probe.wfp_hbm_stream(None, p16, 4, 1, 2, None) == -1
+    assert probe.wfp_hbm_stream(p16 + 4, p16, 4, 1, 2, None) == -1
+    assert probe.wfp_hbm_stream(p16, p16, 4, 3, 5, None) == -2
+    assert b"3:5" in probe.wfp_last_error()

@@ -155,6 +155,11 @@ def test_malformed_tensor_infos(tmp_path):
     rejects(tmp_path, tensor_file([32, 1, 1, 1, 2]), "dimension count")
     rejects(tmp_path, tensor_file([32, 2], alignment=48), "power-of-two")
     rejects(tmp_path, tensor_file([1 << 40, 1 << 30], qtype=0), "overflows")
+    # 2^62 elements pass the element-count check; their bytes (F32: 2^64, F16: 2^63) do not fit in 64 bits and
+    # must not wrap to a small or negative size that would pass the end-of-file check
+    rejects(tmp_path, tensor_file([1 << 31, 1 << 31], qtype=0), "byte count overflows")
+    rejects(tmp_path, tensor_file([1 << 31, 1 << 31], qtype=1), "byte count overflows")
+    rejects(tmp_path, tensor_file([1 << 31, 1 << 30], qtype=0), "byte count overflows")
 
 
 def test_missing_file_and_directory(tmp_path):

@@ -6,7 +6,7 @@ import os
 import numpy as np
 import pytest
 
-from oracle import lib
+from oracle import lib, np_oracle
 
 G = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 PER_BLOCK = {2: 32, 3: 32, 6: 32, 7: 32, 8: 32, 10: 256, 11: 256, 12: 256, 13: 256, 14: 256}
@@ -49,3 +49,22 @@ def test_linear_i8_fixtures():
     assert np.array_equal(acc, z["acc"]) and np.array_equal(y, z["y"])
     # the accumulators are the exact integer products
     assert np.array_equal(z["acc"], z["xq"].astype(np.int64) @ z["wq"].astype(np.int64).T)
+
+
+def test_convrot_stage_order_fixture():
+    # rows on which the order of a radix-4 stage's sums decides int8 values: the C oracle and the numpy
+    # restatement in the reference's left-to-right order both give the fixture, and each other order misses it
+    z = _load("convrot_order.npz")
+    xq, xs = lib.quant_rows(z["x"], 1)
+    assert np.array_equal(xq, z["q"]) and _same(xs, z["s"])
+    nq, ns = np_oracle.quant_rows_convrot(z["x"], "ltr")
+    assert np.array_equal(nq, z["q"]) and _same(ns, z["s"])
+    for order in ("pair", "rtl"):
+        oq, _ = np_oracle.quant_rows_convrot(z["x"], order)
+        assert (oq != z["q"]).any(axis=1).all(), order
+
+
+def test_numpy_convrot_restatement_equals_the_c_oracle():
+    q = _load("quant_rows.npz")
+    nq, ns = np_oracle.quant_rows_convrot(q["x"])
+    assert np.array_equal(nq, q["q_1"]) and _same(ns, q["s_1"])

@@ -67,3 +67,16 @@ def test_quantiser_and_int8_linear_match_fixtures(native):
     assert rc == 0, native.last_error()
     torch.cuda.synchronize()
     assert np.array_equal(_bits(y, 1), z["y"])
+
+
+def test_convrot_kernel_keeps_the_stage_sum_order(native):
+    # rows whose int8 values change under any other order of a radix-4 stage's sums (tests/golden/make_golden.py)
+    z = _load("convrot_order.npz")
+    x = torch.from_numpy(z["x"].view(np.int16)).cuda()
+    M, K = x.shape
+    xq = torch.empty((M, K), dtype=torch.int8, device="cuda")
+    xs = torch.empty(M, dtype=torch.float32, device="cuda")
+    rc = native.lib().wf_quant_rows_i8(x.data_ptr(), M, K, 1, xq.data_ptr(), xs.data_ptr(), native.stream_of(x.device))
+    assert rc == 0, native.last_error()
+    torch.cuda.synchronize()
+    assert np.array_equal(xq.cpu().numpy(), z["q"]) and _same(xs.cpu().numpy(), z["s"])

@@ -1,13 +1,24 @@
-"""The byte-moving kernel the benchmark sets beside the dequantisation (wf_hbm_stream) moves exactly the bytes it
-claims: every output chunk of every supported read:write mix holds (xor of the thread's input words, chunk index,
+"""The byte-moving kernel the benchmark sets beside the dequantisation (wfp_hbm_stream, in the measurement-only
+library libwf_probe.so) moves exactly the bytes it claims: every output chunk of every supported read:write mix holds (xor of the thread's input words, chunk index,
 thread index, 0), and nothing past the output is touched."""
 import numpy as np
 import pytest
 import torch
 
-from conftest import sub
+from conftest import ROOT, PKG_NAME, sub
 
 pytestmark = pytest.mark.gpu
+
+
+def _probe():
+    import ctypes
+    import os
+    sub("_native").lib()                 # torch's HIP runtime first, as for the product library
+    lib = ctypes.CDLL(os.path.join(ROOT, PKG_NAME, "lib", "libwf_probe.so"))
+    p, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.wfp_hbm_stream.argtypes, lib.wfp_hbm_stream.restype = [p, p, i64, i32, i32, p], i32
+    lib.wfp_last_error.restype = ctypes.c_char_p
+    return lib
 
 
 @pytest.mark.parametrize("reads,writes", [(1, 0), (0, 1), (1, 1), (1, 2), (2, 7)])
@@ -20,8 +31,9 @@ def test_stream_writes_every_chunk(reads, writes, items):
     inp = torch.from_numpy(src.view(np.int32)).to(dev)
     guard = 64                                                   # chunks after the output that must stay untouched
     out = torch.full(((max(1, writes) * items + guard) * 4,), -7, dtype=torch.int32, device=dev)
-    rc = native.lib().wf_hbm_stream(inp.data_ptr(), out.data_ptr(), items, reads, writes, native.stream_of(dev))
-    assert rc == 0, native.last_error()
+    probe = _probe()
+    rc = probe.wfp_hbm_stream(inp.data_ptr(), out.data_ptr(), items, reads, writes, native.stream_of(dev))
+    assert rc == 0, probe.wfp_last_error()
     torch.cuda.synchronize()
     got = out.cpu().numpy().view(np.uint32).reshape(-1, 4)
     acc = np.zeros(items, dtype=np.uint32)

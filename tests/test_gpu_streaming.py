@@ -143,6 +143,13 @@ def test_pinned_host_is_page_locked(native):
     assert torch.equal(d.cpu(), h.tensor)
     h.release()
     assert pinned.registered_bytes()["bytes"] == before
+    # with an alignment the buffer holds nbytes + align; the counter goes up and back down by that same amount
+    h = pinned.PinnedHost(1000, align=256)
+    assert h.registered and h.tensor.numel() == 1000 and h.ptr % 256 == 0
+    assert pinned.registered_bytes()["bytes"] == before + 1256
+    h.release()
+    h.release()
+    assert pinned.registered_bytes()["bytes"] == before
 
 
 def test_gguf_linear_fused_matches_dequant_flow(native):
