@@ -89,6 +89,9 @@ class _ChunkState(_StreamState):
         self.blocks_started = 0
         self._fwd = None
         self._retired = []                # unit events replaced in this forward (closed once it has run)
+        # host-side fences on both cross-stream dependencies (see leaf_pre); WEIGHTFERRY_CHUNK_HOST_FENCE=0 leaves
+        # them to the stream waits alone
+        self.host_fence = _env.get("WEIGHTFERRY_CHUNK_HOST_FENCE") != "0"
         if order_cache is not None:
             self.use_learned_order(order_cache)
 
@@ -210,7 +213,8 @@ class _ChunkState(_StreamState):
             buf, free, _ = self.spares[spare]
             self.spare_owner[spare] = u
             self.u_spare[u] = spare
-        free.synchronize()                # host-side fence (see leaf_pre)
+        if self.host_fence:
+            free.synchronize()            # host-side fence (see leaf_pre)
         _native.stream_wait(stream, free)
         self._copy(s, self.type_plan[t][0], buf, stream)
         ev = _native.Event()
@@ -295,7 +299,8 @@ class _ChunkState(_StreamState):
         # wrong bytes from the third forward on in some processes (after other streams had been created and
         # destroyed; never in the CPU protocol model, nor in block streaming). The host then runs at most the slots'
         # depth ahead of the GPU; the copies stay ahead of the compute.
-        self.unit_events[u].synchronize()
+        if self.host_fence:
+            self.unit_events[u].synchronize()
         _native.stream_wait(self.compute_stream(), self.unit_events[u])
         self._bind(s, views)
         self.u_bound[u] = True
