@@ -690,6 +690,223 @@ __global__ __launch_bounds__(64 * kSkWaves) void gemm_gguf_skinny(const uint16_t
     }
 }
 
+// ------------------------------------------------------------- few activation rows, split along K (M <= 16 MT)
+// The same weight stream as gemm_gguf_skinny, cut into many more workgroups: workgroup (tn, s) takes the 128 weight
+// rows [128 tn, +128) -- 4 waves of two 16-row groups -- over super-blocks [KS s, KS s + KS) of K only (slice s of
+// S). It issues the raw bytes of all its super-blocks first, then copies the slice's activations X[0:M, slice] into
+// LDS once (rows padded by 16 bytes, so the 16 rows of a fragment read fall in different banks); each wave then
+// dequantises its rows straight into B fragments as gemm_gguf_skinny does and reads its A fragments from LDS, so a
+// workgroup reads the activations from L2 once per 128 weight rows instead of once per 32. A slice's partial sums go
+// to part[s][m][n] (float32). The workgroups of a column tile count themselves on counters[tn]; the last one to
+// arrive adds the S partials in slice order 0, 1, ..., S - 1, adds the bias, rounds to bf16, stores, and sets the
+// counter back to 0 for the next launch: the result does not depend on which workgroup arrives last.
+// Hand-over between workgroups (which may sit on different XCDs, each with its own L2): the partials are written
+// and read as device-scope relaxed atomics -- stores and loads coherent across the L2s, without the writeback of a
+// whole L2 that a device-scope fence costs (two such fences per workgroup made the kernel several times slower) --
+// each thread waits until its stores are acknowledged before the workgroup's barrier, and only then is the counter
+// incremented; the last workgroup reads the partials after its increment has returned.
+constexpr int kSpWaves = 4;
+constexpr int kSpRows = 32 * kSpWaves;   // weight rows per workgroup
+
+template <int QT, int MID, bool BIAS, int MT, int KS>
+__global__ __launch_bounds__(64 * kSpWaves) void gemm_gguf_splitk(const uint16_t* __restrict__ X,
+                                                                  const uint8_t* __restrict__ W,
+                                                                  const uint16_t* __restrict__ bias,
+                                                                  uint16_t* __restrict__ Y, int M, int N, int K,
+                                                                  int S, unsigned* __restrict__ counters,
+                                                                  float* __restrict__ part) {
+    constexpr int TS = GGUFTs<QT>::TS, NR = 2;
+    constexpr int LROW = 512 * KS + 16;               // LDS bytes per activation row of the slice
+    constexpr int CPR = 32 * KS;                      // 16-byte chunks per activation row of the slice
+    __shared__ __align__(16) uint8_t xs[16 * MT * LROW];
+    __shared__ unsigned is_last;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 15, kq = lane >> 4;
+    const int NT = (N + kSpRows - 1) / kSpRows;
+    const int tn = blockIdx.x % NT, s = blockIdx.x / NT;
+    const int nsb = K / 256;
+    const int sb0 = s * KS;
+    const int nks = min(KS, nsb - sb0);               // super-blocks of this slice (>= 1)
+    const int n0 = tn * kSpRows + wave * 32;
+    const int64_t row_bytes = (int64_t)nsb * TS;
+    SkRaw<QT> w[KS][NR];
+#pragma unroll
+    for (int j = 0; j < KS; j++) {
+        if (j < nks) {
+#pragma unroll
+            for (int nr = 0; nr < NR; nr++)
+                sk_load<QT>(W + (int64_t)min(n0 + 16 * nr + r, N - 1) * row_bytes + (int64_t)(sb0 + j) * TS, kq,
+                            w[j][nr]);
+        }
+    }
+    // the slice's activations: rows past M repeat row M - 1 (their sums are never stored), columns past the slice's
+    // last super-block are zeros (never read)
+    for (int c = tid; c < 16 * MT * CPR; c += 64 * kSpWaves) {
+        const int row = c / CPR, cc = c - row * CPR;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (cc < 32 * nks)
+            v = *reinterpret_cast<const uint4*>(X + (int64_t)min(row, M - 1) * K + (int64_t)sb0 * 256 + 8 * cc);
+        *reinterpret_cast<uint4*>(xs + row * LROW + 16 * cc) = v;
+    }
+    __syncthreads();
+    f32x4 acc[NR][MT];
+#pragma unroll
+    for (int nr = 0; nr < NR; nr++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[nr][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto stage = [&](auto G, int j) {
+        constexpr int g = decltype(G)::value;
+        bf16x8 bw[NR];
+#pragma unroll
+        for (int nr = 0; nr < NR; nr++) bw[nr] = sk_dequant<QT, MID, g>(w[j][nr], kq);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const bf16x8 ax = *reinterpret_cast<const bf16x8*>(xs + (16 * mt + r) * LROW + 2 * (256 * j + 32 * g + 8 * kq));
+#pragma unroll
+            for (int nr = 0; nr < NR; nr++)
+                acc[nr][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bw[nr], acc[nr][mt], 0, 0, 0);
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < KS; j++) {
+        if (j < nks) {
+            stage(std::integral_constant<int, 0>{}, j);
+            stage(std::integral_constant<int, 1>{}, j);
+            stage(std::integral_constant<int, 2>{}, j);
+            stage(std::integral_constant<int, 3>{}, j);
+            stage(std::integral_constant<int, 4>{}, j);
+            stage(std::integral_constant<int, 5>{}, j);
+            stage(std::integral_constant<int, 6>{}, j);
+            stage(std::integral_constant<int, 7>{}, j);
+        }
+    }
+    // this slice's partial sums: lane (r, kq), register i holds row 16 mt + 4 kq + i, column n0 + 16 nr + r
+    float* ps = part + (int64_t)s * M * N;
+#pragma unroll
+    for (int nr = 0; nr < NR; nr++) {
+        const int n = n0 + 16 * nr + r;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = 16 * mt + 4 * kq + i;
+                if (m < M && n < N)
+                    __hip_atomic_store(ps + (int64_t)m * N + n, acc[nr][mt][i], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+    }
+    __builtin_amdgcn_s_waitcnt(0);                    // this thread's partials acknowledged
+    __syncthreads();                                  // ... and every thread's
+    if (tid == 0)
+        is_last = __hip_atomic_fetch_add(counters + tn, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                  (unsigned)(S - 1);
+    __syncthreads();
+    if (!is_last) return;
+    const int nb = tn * kSpRows;
+    for (int idx = tid; idx < M * kSpRows; idx += 64 * kSpWaves) {
+        const int m = idx / kSpRows, n = nb + (idx - m * kSpRows);
+        if (n >= N) continue;
+        float* p = part + (int64_t)m * N + n;
+        const int64_t slice = (int64_t)M * N;
+        // the partials in batches of 8 loads in flight (one at a time would wait out a memory latency each), then
+        // added in slice order
+        float t = 0.0f;
+        for (int q0 = 0; q0 < S; q0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                v[j] = q0 + j < S ? __hip_atomic_load(p + (q0 + j) * slice, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                  : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (q0 + j < S) t = (q0 + j == 0) ? v[j] : t + v[j];
+        }
+        if (BIAS) t = t + __uint_as_float((uint32_t)bias[n] << 16);
+        Y[(int64_t)m * N + n] = __builtin_bit_cast(uint16_t, (__bf16)t);
+    }
+    if (tid == 0) __hip_atomic_store(counters + tn, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Split-K plan of an [M, K] x [N, K] product: rows per fragment group MT, super-blocks per slice KS, slices S, column
+// tiles NT, and the workspace: a fixed block of kSplitCounters counters (the same place for every call, so calls of
+// any shape can share one workspace), then S * M * N float32 partial sums.
+static constexpr int kSplitCounters = 4096;     // column tiles: N <= 4096 * 128
+static constexpr int64_t kSplitCounterBytes = 4 * kSplitCounters;
+
+struct SplitPlan {
+    int mt, ks, s, nt;
+    int64_t counter_bytes, part_bytes;
+    int64_t bytes() const { return counter_bytes + part_bytes; }
+};
+
+// Where the split form is the faster one (measured on MI355X against gemm_gguf_skinny, Q4_K / Q6_K, Wan-14B shapes):
+// a deep product (K >= 2 N: 5120 x 13824, 14 slices of 4 super-blocks) with at most 8 rows, 4-7 % faster (Q4_K
+// 27.9 / 31.1 us against 29.2 / 32.6 us at 1 / 8 rows). Shallower products and more rows are faster in
+// gemm_gguf_skinny, whose one workgroup per 32 weight rows needs no hand-over of partial sums between workgroups
+// (5120 x 5120 Q4_K at 32 rows: 14.4 us against 27.9 us split).
+static constexpr int kSplitMaxRows = 8;
+
+static bool split_takes(int64_t M, int64_t N, int64_t K) {
+    return M >= 1 && M <= kSplitMaxRows && N >= 1 && N <= (int64_t)kSplitCounters * kSpRows && K >= 2 * N;
+}
+
+static SplitPlan split_plan(int64_t M, int64_t N, int64_t K) {
+    SplitPlan p{};
+    p.mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
+    p.nt = (int)((N + kSpRows - 1) / kSpRows);
+    const int nsb = (int)(K / 256);
+    // the widest slice (fewest partial sums) that still gives every CU a workgroup; LDS: MT * KS <= 8
+    int ks = 8 / p.mt < 4 ? 8 / p.mt : 4;
+    while (ks > 1 && (int64_t)p.nt * ((nsb + ks - 1) / ks) < 256) ks >>= 1;
+    p.ks = ks;
+    p.s = (nsb + ks - 1) / ks;
+    p.counter_bytes = kSplitCounterBytes;
+    p.part_bytes = (int64_t)p.s * M * N * 4;
+    return p;
+}
+
+template <int QT, int MID, int MT, int KS>
+static void launch_splitk_ks(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N,
+                             int K, const SplitPlan& p, void* ws, hipStream_t st) {
+    unsigned* counters = static_cast<unsigned*>(ws);
+    float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + p.counter_bytes);
+    const dim3 grid((unsigned)(p.nt * p.s));
+    if (bias)
+        gemm_gguf_splitk<QT, MID, true, MT, KS><<<grid, 64 * kSpWaves, 0, st>>>(X, W, bias, Y, M, N, K, p.s, counters, part);
+    else
+        gemm_gguf_splitk<QT, MID, false, MT, KS><<<grid, 64 * kSpWaves, 0, st>>>(X, W, bias, Y, M, N, K, p.s, counters, part);
+}
+
+template <int QT, int MID, int MT>
+static void launch_splitk_mt(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N,
+                             int K, const SplitPlan& p, void* ws, hipStream_t st) {
+    if constexpr (MT <= 2) {
+        if (p.ks == 4) { launch_splitk_ks<QT, MID, MT, 4>(X, W, bias, Y, M, N, K, p, ws, st); return; }
+    }
+    if constexpr (MT <= 4) {
+        if (p.ks == 2) { launch_splitk_ks<QT, MID, MT, 2>(X, W, bias, Y, M, N, K, p, ws, st); return; }
+    }
+    launch_splitk_ks<QT, MID, MT, 1>(X, W, bias, Y, M, N, K, p, ws, st);
+}
+
+template <int QT, int MID>
+static void launch_splitk(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
+                          const SplitPlan& p, void* ws, hipStream_t st) {
+    if (p.mt == 1) launch_splitk_mt<QT, MID, 1>(X, W, bias, Y, M, N, K, p, ws, st);
+    else if (p.mt == 2) launch_splitk_mt<QT, MID, 2>(X, W, bias, Y, M, N, K, p, ws, st);
+    else if (p.mt == 4) launch_splitk_mt<QT, MID, 4>(X, W, bias, Y, M, N, K, p, ws, st);
+    else launch_splitk_mt<QT, MID, 8>(X, W, bias, Y, M, N, K, p, ws, st);
+}
+
+template <int QT>
+static void launch_splitk_mid(int mid, const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M,
+                              int N, int K, const SplitPlan& p, void* ws, hipStream_t st) {
+    if (mid == WF_F16) launch_splitk<QT, WF_F16>(X, W, bias, Y, M, N, K, p, ws, st);
+    else if (mid == WF_BF16) launch_splitk<QT, WF_BF16>(X, W, bias, Y, M, N, K, p, ws, st);
+    else launch_splitk<QT, WF_F32>(X, W, bias, Y, M, N, K, p, ws, st);
+}
+
 template <int QT, int MID, int MT, int NR = 1>
 static void launch_skinny(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
                           hipStream_t s) {
@@ -734,37 +951,99 @@ static void launch_mid(int mid, const uint16_t* X, const uint8_t* W, const uint1
 
 }  // namespace wf
 
-extern "C" int wf_linear_gguf(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes,
-                              int qtype, int64_t N, const void* bias_bf16, void* out_bf16, int mid_dt,
-                              void* stream) {
-    using namespace wf;
+namespace wf {
+// argument checks shared by the entry points; WF_OK with M == 0 or N == 0 means nothing to do
+static int check_gguf(const char* who, const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes,
+                      int qtype, int64_t N, const void* bias_bf16, const void* out_bf16, int mid_dt) {
     if (qtype != 12 && qtype != 13 && qtype != 14) {
-        set_error("wf_linear_gguf: GGML type %d is not handled (Q4_K, Q5_K, Q6_K)", qtype);
+        set_error("%s: GGML type %d is not handled (Q4_K, Q5_K, Q6_K)", who, qtype);
         return WF_EUNSUPPORTED;
     }
-    if (mid_dt < 0 || mid_dt > 2) { set_error("wf_linear_gguf: dequant dtype %d", mid_dt); return WF_EUNSUPPORTED; }
-    if (M < 0 || N < 0 || K <= 0) { set_error("wf_linear_gguf: M, N, K = %lld, %lld, %lld", (long long)M, (long long)N, (long long)K); return WF_EINVAL; }
-    if (K % 256) { set_error("wf_linear_gguf: K = %lld is not a multiple of 256", (long long)K); return WF_EUNSUPPORTED; }
+    if (mid_dt < 0 || mid_dt > 2) { set_error("%s: dequant dtype %d", who, mid_dt); return WF_EUNSUPPORTED; }
+    if (M < 0 || N < 0 || K <= 0) {
+        set_error("%s: M, N, K = %lld, %lld, %lld", who, (long long)M, (long long)N, (long long)K);
+        return WF_EINVAL;
+    }
+    if (K % 256) { set_error("%s: K = %lld is not a multiple of 256", who, (long long)K); return WF_EUNSUPPORTED; }
     const int ts = qtype == 12 ? 144 : qtype == 13 ? 176 : 210;
     if (wq_bytes != N * (K / 256) * ts) {
-        set_error("wf_linear_gguf: %lld weight bytes for [%lld, %lld]", (long long)wq_bytes, (long long)N, (long long)K);
+        set_error("%s: %lld weight bytes for [%lld, %lld]", who, (long long)wq_bytes, (long long)N, (long long)K);
         return WF_EUNSUPPORTED;
     }
     if (M == 0 || N == 0) return WF_OK;
-    if (!x_bf16 || !wq || !out_bf16) { set_error("wf_linear_gguf: null pointer"); return WF_EINVAL; }
+    if (!x_bf16 || !wq || !out_bf16) { set_error("%s: null pointer", who); return WF_EINVAL; }
     if (!aligned(x_bf16, 16) || !aligned(wq, 16) || !aligned(out_bf16, 2) || (bias_bf16 && !aligned(bias_bf16, 2))) {
-        set_error("wf_linear_gguf: x and the weight blocks must be 16-byte aligned");
+        set_error("%s: x and the weight blocks must be 16-byte aligned", who);
         return WF_EUNSUPPORTED;
     }
-    if (M >= (1LL << 31) || N >= (1LL << 31) || K >= (1LL << 31)) { set_error("wf_linear_gguf: sizes too large"); return WF_EUNSUPPORTED; }
-    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (M >= (1LL << 31) || N >= (1LL << 31) || K >= (1LL << 31)) {
+        set_error("%s: sizes too large", who);
+        return WF_EUNSUPPORTED;
+    }
+    return WF_OK;
+}
+
+static void run_gguf(int qtype, int mid_dt, const void* x_bf16, const void* wq, const void* bias_bf16, void* out_bf16,
+                     int M, int N, int K, hipStream_t s) {
     const uint16_t* X = static_cast<const uint16_t*>(x_bf16);
     const uint8_t* W = static_cast<const uint8_t*>(wq);
     const uint16_t* B = static_cast<const uint16_t*>(bias_bf16);
     uint16_t* Y = static_cast<uint16_t*>(out_bf16);
-    if (qtype == 12) launch_mid<12>(mid_dt, X, W, B, Y, (int)M, (int)N, (int)K, s);
-    else if (qtype == 13) launch_mid<13>(mid_dt, X, W, B, Y, (int)M, (int)N, (int)K, s);
-    else launch_mid<14>(mid_dt, X, W, B, Y, (int)M, (int)N, (int)K, s);
+    if (qtype == 12) launch_mid<12>(mid_dt, X, W, B, Y, M, N, K, s);
+    else if (qtype == 13) launch_mid<13>(mid_dt, X, W, B, Y, M, N, K, s);
+    else launch_mid<14>(mid_dt, X, W, B, Y, M, N, K, s);
+}
+
+static void run_gguf_split(int qtype, int mid_dt, const void* x_bf16, const void* wq, const void* bias_bf16,
+                           void* out_bf16, int M, int N, int K, const SplitPlan& p, void* ws, hipStream_t s) {
+    const uint16_t* X = static_cast<const uint16_t*>(x_bf16);
+    const uint8_t* W = static_cast<const uint8_t*>(wq);
+    const uint16_t* B = static_cast<const uint16_t*>(bias_bf16);
+    uint16_t* Y = static_cast<uint16_t*>(out_bf16);
+    if (qtype == 12) launch_splitk_mid<12>(mid_dt, X, W, B, Y, M, N, K, p, ws, s);
+    else if (qtype == 13) launch_splitk_mid<13>(mid_dt, X, W, B, Y, M, N, K, p, ws, s);
+    else launch_splitk_mid<14>(mid_dt, X, W, B, Y, M, N, K, p, ws, s);
+}
+}  // namespace wf
+
+extern "C" int wf_linear_gguf(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes,
+                              int qtype, int64_t N, const void* bias_bf16, void* out_bf16, int mid_dt,
+                              void* stream) {
+    using namespace wf;
+    const int rc = check_gguf("wf_linear_gguf", x_bf16, M, K, wq, wq_bytes, qtype, N, bias_bf16, out_bf16, mid_dt);
+    if (rc != WF_OK || M == 0 || N == 0) return rc;
+    run_gguf(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, static_cast<hipStream_t>(stream));
     WF_LAUNCH_CHECK("wf_linear_gguf launch");
+    return WF_OK;
+}
+
+extern "C" int wf_linear_gguf_workspace(int64_t M, int64_t N, int64_t K, int64_t* bytes) {
+    using namespace wf;
+    if (!bytes) { set_error("wf_linear_gguf_workspace: null out-pointer"); return WF_EINVAL; }
+    *bytes = 0;
+    if (M < 0 || N < 0 || K <= 0 || K % 256) { set_error("wf_linear_gguf_workspace: M, N, K"); return WF_EINVAL; }
+    if (split_takes(M, N, K)) *bytes = split_plan(M, N, K).bytes();
+    return WF_OK;
+}
+
+extern "C" int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes,
+                                 int qtype, int64_t N, const void* bias_bf16, void* out_bf16, int mid_dt,
+                                 void* workspace, int64_t workspace_bytes, void* stream) {
+    using namespace wf;
+    const int rc = check_gguf("wf_linear_gguf_ws", x_bf16, M, K, wq, wq_bytes, qtype, N, bias_bf16, out_bf16, mid_dt);
+    if (rc != WF_OK || M == 0 || N == 0) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!split_takes(M, N, K)) {
+        run_gguf(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, s);
+    } else {
+        const SplitPlan p = split_plan(M, N, K);
+        if (!workspace || !aligned(workspace, 256) || workspace_bytes < p.bytes()) {
+            set_error("wf_linear_gguf_ws: a 256-byte aligned workspace of %lld bytes is needed (given %lld)",
+                      (long long)p.bytes(), (long long)workspace_bytes);
+            return WF_EINVAL;
+        }
+        run_gguf_split(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, p, workspace, s);
+    }
+    WF_LAUNCH_CHECK("wf_linear_gguf_ws launch");
     return WF_OK;
 }

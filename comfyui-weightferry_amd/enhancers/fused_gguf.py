@@ -7,6 +7,8 @@ dtype) and float32 accumulation; mode="dequant" keeps the reference's two-step f
 mode="auto" (the default of GGUFLinear) picks whichever measured faster on MI355X for the layer's shape
 (``prefer_fused``). Anything else -- other formats, dtypes, CPU tensors -- returns None from ``fused_linear`` and
 ``linear`` takes the two-step flow."""
+import ctypes
+
 import torch
 
 from .. import _native
@@ -14,6 +16,19 @@ from . import gguf_dequant
 
 _FUSED_TYPES = {12: 144, 13: 176, 14: 210}
 _MID = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+_workspaces = {}             # (device index, stream) -> uint8 workspace whose counter words are zero between calls
+
+
+def _workspace(device, stream, nbytes):
+    """The split-K workspace of this device and stream, at least ``nbytes``: allocated zeroed once (its counters
+    must be zero on entry, and every call leaves them zero) and grown when a larger product needs more. Calls on one
+    stream are ordered, so they can share it."""
+    key = (device.index, stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
 
 
 def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
@@ -31,12 +46,21 @@ def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
     if raw is None or raw.numel() != n_out * (k // 256) * _FUSED_TYPES[q]:
         return None
     x2 = x.reshape(-1, k).contiguous()
-    y = torch.empty((x2.shape[0], n_out), dtype=torch.bfloat16, device=x.device)
+    rows = x2.shape[0]
+    y = torch.empty((rows, n_out), dtype=torch.bfloat16, device=x.device)
     b = bias.contiguous() if bias is not None else None
+    lib = _native.lib()
     with torch.cuda.device(x.device):
-        rc = _native.lib().wf_linear_gguf(x2.data_ptr(), x2.shape[0], k, raw.data_ptr(), raw.numel(), q, n_out,
-                                          b.data_ptr() if b is not None else None, y.data_ptr(), _MID[mid],
-                                          _native.stream_of(x.device))
+        stream = _native.stream_of(x.device)
+        args = (x2.data_ptr(), rows, k, raw.data_ptr(), raw.numel(), q, n_out, b.data_ptr() if b is not None else None,
+                y.data_ptr(), _MID[mid])
+        need = ctypes.c_int64()
+        _native.call("wf_linear_gguf_workspace", rows, n_out, k, ctypes.byref(need))
+        if need.value:              # the split form (few rows of a deep product) with its workspace
+            ws = _workspace(x.device, stream, need.value)
+            rc = lib.wf_linear_gguf_ws(*args, ws.data_ptr(), ws.numel(), stream)
+        else:
+            rc = lib.wf_linear_gguf(*args, stream)
     if not _native.check(rc, "wf_linear_gguf"):
         return None
     return y.reshape(*x.shape[:-1], n_out)

@@ -103,6 +103,19 @@ int wf_linear_i8_residual(const int8_t* xq, const int8_t* wq, const float* xs, c
 int wf_linear_gguf(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes, int qtype, int64_t N,
                    const void* bias_bf16, void* out_bf16, int mid_dt, void* stream);
 
+/* wf_linear_gguf with a caller-provided workspace, for the same reference call site (enhancers/gguf_dequant.py:
+ * 296-326 followed by ComfyUI-GGUF's F.linear). A deep product (K >= 2 N) with 1 <= M <= 8 rows is split along K
+ * over many more workgroups than weight rows allow: each writes float32 partial sums into the workspace, and the
+ * last workgroup of each column tile adds them in a fixed order (the result is the same on every run). Workspace:
+ * 256-byte aligned, at least the bytes wf_linear_gguf_workspace gives; its first 16 KiB are counters that must be
+ * zero on entry and are zero again when the call has run, whatever its shape (a workspace cleared once can be reused
+ * by later calls of any shape on the same stream; calls that overlap on one workspace race). Any other shape does
+ * not use the workspace (wf_linear_gguf_workspace gives 0; workspace may be NULL) and is wf_linear_gguf. */
+int wf_linear_gguf_workspace(int64_t M, int64_t N, int64_t K, int64_t* bytes);
+int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes, int qtype, int64_t N,
+                      const void* bias_bf16, void* out_bf16, int mid_dt, void* workspace, int64_t workspace_bytes,
+                      void* stream);
+
 /* ---------------------------------------------------------------------------------------- block streaming
  * Exact-size page-locked host memory: replaces PinnedHost's cudaHostRegister / cudaHostUnregister
  * (core/tiers/pinned.py:84-129); allocated page-locked (hipHostMalloc) instead of registered after the fact. */

@@ -118,3 +118,74 @@ def test_rejects_what_it_does_not_handle(native):
     assert lib_.wf_linear_gguf(None, 4, 300, None, 0, 12, 4, None, None, 0, None) == native.EUNSUPPORTED   # K
     assert lib_.wf_linear_gguf(None, 4, 256, None, 144 * 4, 8, 4, None, None, 0, None) == native.EUNSUPPORTED
     assert lib_.wf_linear_gguf(None, 4, 256, None, 144 * 3, 12, 4, None, None, 0, None) == native.EUNSUPPORTED
+
+
+def fused_ws(native, x, raw_dev, qtype, N, bias=None, mid=0, ws=None):
+    """wf_linear_gguf_ws with a workspace of the size wf_linear_gguf_workspace asks for (zeroed here unless given)"""
+    import ctypes
+    M, K = x.shape
+    need = ctypes.c_int64()
+    assert native.lib().wf_linear_gguf_workspace(M, N, K, ctypes.byref(need)) == 0
+    if ws is None:
+        ws = torch.zeros(max(16384, need.value), dtype=torch.uint8, device=x.device)
+    assert ws.numel() >= need.value
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    rc = native.lib().wf_linear_gguf_ws(x.data_ptr(), M, K, raw_dev.data_ptr(), raw_dev.numel(), qtype, N,
+                                        bias.data_ptr() if bias is not None else None, y.data_ptr(), mid,
+                                        ws.data_ptr(), ws.numel(), native.stream_of(x.device))
+    assert rc == 0, native.last_error()
+    torch.cuda.synchronize()
+    return y, ws, need.value
+
+
+@pytest.mark.parametrize("qtype", [12, 13, 14])
+@pytest.mark.parametrize("mid", [0, 2])
+@pytest.mark.parametrize("M,N,K,with_bias", [(1, 300, 768, True), (5, 5120, 13824, False), (8, 61, 512, True),
+                                             (3, 1000, 2048, False), (7, 384, 5120, True), (8, 640, 1280, False),
+                                             (2, 130, 13824, True), (9, 320, 768, True), (4, 5120, 5120, False)])
+def test_split_k_whole_output(native, qtype, mid, M, N, K, with_bias):
+    # up to 8 activation rows of a deep product (K >= 2 N) take the split-K form (128 weight rows per workgroup, K in
+    # slices of 1-4 super-blocks, partial sums added by the last workgroup of each column tile): ragged M, N and
+    # slices, every output element checked; 9 rows, or K < 2 N, go to the few-rows kernel without the workspace
+    raw = encode.random_blocks(qtype, N * K // 256, seed=qtype * 5 + M, family="normal")
+    g = torch.Generator().manual_seed(M * 17 + N)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16) if with_bias else None
+    print(f"case split-K qtype={qtype} mid={mid} M={M} N={N} K={K}", flush=True)
+    y, ws, need = fused_ws(native, x.cuda(), torch.from_numpy(raw).cuda(), qtype, N,
+                           bias=bias.cuda() if with_bias else None, mid=mid)
+    assert (need > 0) == (M <= 8 and K >= 2 * N)
+    check(y, x, weight_bf16(raw, qtype, mid, N, K), bias=bias)
+    assert not ws[:16384].any()                          # the counters are back to zero
+
+
+def test_split_k_reuses_its_workspace_and_repeats_bits(native):
+    # two calls on one workspace (the second with fewer rows and another width), then the first again: the same
+    # bits as its first run -- the partial sums are added in slice order whichever workgroup arrives last
+    qtype, K = 12, 13824
+    raws = {N: torch.from_numpy(encode.random_blocks(qtype, N * K // 256, seed=N, family="normal")).cuda()
+            for N in (5120, 1280)}
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn((8, K), generator=g).to(torch.bfloat16).cuda()
+    y1, ws, n1 = fused_ws(native, x, raws[5120], qtype, 5120)
+    y2, ws, n2 = fused_ws(native, x[:3].contiguous(), raws[1280], qtype, 1280, ws=ws)
+    y3, ws, _ = fused_ws(native, x, raws[5120], qtype, 5120, ws=ws)
+    assert n1 > 0 and n2 > 0
+    assert torch.equal(y1.view(torch.int16), y3.view(torch.int16))
+    check(y2, x[:3].cpu(), weight_bf16(raws[1280].cpu().numpy(), qtype, 0, 1280, K))
+
+
+def test_split_k_rejects_a_short_workspace(native):
+    import ctypes
+    M, N, K = 8, 256, 768
+    need = ctypes.c_int64()
+    assert native.lib().wf_linear_gguf_workspace(M, N, K, ctypes.byref(need)) == 0 and need.value > 0
+    x = torch.zeros((M, K), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(N * K // 256 * 144, dtype=torch.uint8, device="cuda")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    ws = torch.zeros(need.value, dtype=torch.uint8, device="cuda")
+    st = native.stream_of(x.device)
+    assert native.lib().wf_linear_gguf_ws(x.data_ptr(), M, K, w.data_ptr(), w.numel(), 12, N, None, y.data_ptr(), 0,
+                                          ws.data_ptr(), need.value - 1, st) == native.EINVAL
+    assert native.lib().wf_linear_gguf_ws(x.data_ptr(), M, K, w.data_ptr(), w.numel(), 12, N, None, y.data_ptr(), 0,
+                                          None, 0, st) == native.EINVAL
