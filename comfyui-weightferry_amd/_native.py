@@ -33,6 +33,7 @@ EXPORTS = {
     "wf_linear_gguf": (_int, [_p, _i64, _i64, _p, _i64, _int, _i64, _p, _p, _int, _p]),
     "wf_linear_gguf_workspace": (_int, [_i64, _i64, _i64, ctypes.POINTER(_i64)]),
     "wf_linear_gguf_ws": (_int, [_p, _i64, _i64, _p, _i64, _int, _i64, _p, _p, _int, _p, _i64, _p]),
+    "wf_linear_gguf_noalloc": (_int, [_p, _i64, _i64, _p, _i64, _int, _i64, _p, _p, _int, _p]),
     "wf_host_alloc": (_int, [_sz, ctypes.POINTER(ctypes.c_void_p)]),
     "wf_host_free": (_int, [_p]),
     "wf_h2d_async": (_int, [_p, _p, _sz, _p]),

@@ -8,6 +8,7 @@
 // 16-wide step; result layout: lane l, register i -> row 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32. The tiling
 // and the pipeline are described at gemm_gguf_dl below.
 
+#include <mutex>
 #include <type_traits>
 
 #include "kquant.h"
@@ -1045,5 +1046,74 @@ extern "C" int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const
         run_gguf_split(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, p, workspace, s);
     }
     WF_LAUNCH_CHECK("wf_linear_gguf_ws launch");
+    return WF_OK;
+}
+
+// ------------------------------------------------------------------------------ the allocation-free entry point
+// wf_linear_gguf_noalloc: wf_linear_gguf_ws with the split form's counters and partial sums in `scratch`, device
+// memory the library holds from load time (one copy per GPU, until the process ends), so the call allocates nothing.
+// In host code `scratch` names a host-side stand-in; its device address comes from hipGetSymbolAddress, looked up once
+// per device with that device current, and only that address is handed to kernels.
+namespace wf {
+static constexpr int64_t kScratchBytes = (int64_t)16 << 20;     // counters (16 KiB) + partial sums
+}  // namespace wf
+
+static __device__ __align__(256) uint8_t scratch[wf::kScratchBytes];
+
+namespace wf {
+static constexpr int kMaxDevices = 64;
+static std::once_flag g_scratch_once[kMaxDevices];
+static void* g_scratch_ptr[kMaxDevices];
+static hipError_t g_scratch_err[kMaxDevices];
+
+// the device address of `scratch` on the current device
+static int scratch_address(void** out) {
+    int dev = -1;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) { set_error("wf_linear_gguf_noalloc: device %d", dev); return WF_EUNSUPPORTED; }
+    std::call_once(g_scratch_once[dev], [dev] {
+        void* p = nullptr;
+        g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? p : nullptr;
+    });
+    if (g_scratch_err[dev] != hipSuccess) return hip_fail(g_scratch_err[dev], "hipGetSymbolAddress(scratch)");
+    *out = g_scratch_ptr[dev];
+    return WF_OK;
+}
+
+// zeroes n 32-bit words (the split form's counters) on the stream: a kernel, not a memset, so the call can be
+// captured into a graph
+__global__ __launch_bounds__(256) void clear_words(unsigned* __restrict__ p, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+}  // namespace wf
+
+extern "C" int wf_linear_gguf_noalloc(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes,
+                                      int qtype, int64_t N, const void* bias_bf16, void* out_bf16, int mid_dt,
+                                      void* stream) {
+    using namespace wf;
+    const int rc = check_gguf("wf_linear_gguf_noalloc", x_bf16, M, K, wq, wq_bytes, qtype, N, bias_bf16, out_bf16,
+                              mid_dt);
+    if (rc != WF_OK || M == 0 || N == 0) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!split_takes(M, N, K)) {
+        run_gguf(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, s);
+    } else {
+        const SplitPlan p = split_plan(M, N, K);
+        if (p.bytes() > kScratchBytes) {
+            set_error("wf_linear_gguf_noalloc: [%lld, %lld] x [%lld, %lld] needs %lld bytes of scratch, more than the "
+                      "%lld the library holds (wf_linear_gguf_ws takes a workspace of any size)", (long long)M,
+                      (long long)K, (long long)N, (long long)K, (long long)p.bytes(), (long long)kScratchBytes);
+            return WF_EUNSUPPORTED;
+        }
+        void* ws = nullptr;
+        const int src = scratch_address(&ws);
+        if (src != WF_OK) return src;
+        clear_words<<<dim3((kSplitCounters + 255) / 256), 256, 0, s>>>(static_cast<unsigned*>(ws), kSplitCounters);
+        run_gguf_split(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, p, ws, s);
+    }
+    WF_LAUNCH_CHECK("wf_linear_gguf_noalloc launch");
     return WF_OK;
 }

@@ -116,6 +116,15 @@ int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const void* wq, 
                       const void* bias_bf16, void* out_bf16, int mid_dt, void* workspace, int64_t workspace_bytes,
                       void* stream);
 
+/* wf_linear_gguf_ws without the workspace argument: allocates nothing. No counterpart in the reference; it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). The split form's counters and partial sums live in a 16 MiB array the library holds on each GPU
+ * it runs on until the process ends; the counters are cleared by a small kernel on `stream` at the start of each call
+ * (no memset). A shape that needs more than 16 MiB there returns WF_EUNSUPPORTED with a message. Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (on different streams or threads) race. */
+int wf_linear_gguf_noalloc(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes, int qtype,
+                           int64_t N, const void* bias_bf16, void* out_bf16, int mid_dt, void* stream);
+
 /* ---------------------------------------------------------------------------------------- block streaming
  * Exact-size page-locked host memory: replaces PinnedHost's cudaHostRegister / cudaHostUnregister
  * (core/tiers/pinned.py:84-129); allocated page-locked (hipHostMalloc) instead of registered after the fact. */
