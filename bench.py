@@ -145,29 +145,49 @@ def fused_leg(torch, native):
                      "fused_frac_of_2500": round(flops / tf / 1e9 / 2500, 3),
                      "two_step_ms": round(tu, 3), "two_step_TFLOPS": round(flops / tu / 1e9, 1),
                      "flop": flops, "weight_bytes": wbytes}
-    # few activation rows (32 tokens): the fused kernel's few-rows form streams each weight once; bound by HBM
-    for qt, name in ((12, "q4_k"), (13, "q5_k"), (14, "q6_k")):
-        tf = tu = 0.0
-        wbytes = 0
-        for lname, N, K in WAN_LINEARS:
-            raw = torch.from_numpy(encode.encode(encode.weights((N, K), seed=N + K), qt)).to(dev)
-            x = torch.randn((32, K), device=dev).to(torch.bfloat16)
-            y = torch.empty((32, N), dtype=torch.bfloat16, device=dev)
-            w = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+    # few activation rows (32 tokens, and one token): the fused kernel's few-rows form streams each weight once;
+    # bound by HBM. "cold": every call reads another copy of the weight, the copies of a layer spanning > 600 MB, so
+    # MI355X's 256 MB last-level cache cannot serve a call from the one before (a weight in a real forward was last
+    # read a step earlier); "warm": the same weight every call. One token goes through fused_gguf.fused_linear, the
+    # drop-in's choice of form (the split form for the deep ffn_down, the few-rows form otherwise).
+    fg = importlib.import_module(PKG + ".enhancers.fused_gguf")
+    for rows in (32, 1):
+        for qt, name in ((12, "q4_k"), (13, "q5_k"), (14, "q6_k")):
+            tf = tc = tu = 0.0
+            wbytes = 0
+            for lname, N, K in WAN_LINEARS:
+                raw = torch.from_numpy(encode.encode(encode.weights((N, K), seed=N + K), qt)).to(dev)
+                ncopy = max(2, -(-600_000_000 // raw.numel()))
+                copies = [raw] + [raw.clone() for _ in range(ncopy - 1)]
+                x = torch.randn((rows, K), device=dev).to(torch.bfloat16)
+                y = torch.empty((rows, N), dtype=torch.bfloat16, device=dev)
+                w = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+                turn = [0]
 
-            def fused():
-                lib.wf_linear_gguf(x.data_ptr(), 32, K, raw.data_ptr(), raw.numel(), qt, N, None, y.data_ptr(), 0, st)
+                def fused(r=raw):
+                    if rows == 1:
+                        fg.fused_linear(x, r, qt, (N, K))
+                    else:
+                        lib.wf_linear_gguf(x.data_ptr(), rows, K, r.data_ptr(), r.numel(), qt, N, None, y.data_ptr(),
+                                           0, st)
 
-            def two_step():
-                lib.wf_dequant(raw.data_ptr(), raw.numel(), qt, 0, 1, w.data_ptr(), N * K, st)
-                torch.matmul(x, w.t(), out=y)
-            tf += _timed(torch, fused, 20, 3)
-            tu += _timed(torch, two_step, 20, 3)
-            wbytes += raw.numel()
-            del raw, x, y, w
-        res[f"{name}_32_tokens"] = {"fused_us": round(tf * 1e3, 1), "two_step_us": round(tu * 1e3, 1),
-                                    "fused_weight_GBps": round(wbytes / (tf / 1e3) / 1e9, 1),
-                                    "weight_bytes": wbytes}
+                def fused_cold():
+                    turn[0] += 1
+                    fused(copies[turn[0] % ncopy])
+
+                def two_step():
+                    lib.wf_dequant(raw.data_ptr(), raw.numel(), qt, 0, 1, w.data_ptr(), N * K, st)
+                    torch.matmul(x, w.t(), out=y)
+                tf += _timed(torch, fused, 20, 3)
+                tc += _timed(torch, fused_cold, 2 * ncopy, ncopy)
+                tu += _timed(torch, two_step, 20, 3)
+                wbytes += raw.numel()
+                del raw, copies, x, y, w
+            torch.cuda.empty_cache()
+            res[f"{name}_{rows}_token{'s' if rows > 1 else ''}"] = {
+                "fused_us_cold": round(tc * 1e3, 1), "fused_us_warm": round(tf * 1e3, 1),
+                "two_step_us": round(tu * 1e3, 1), "fused_weight_GBps_cold": round(wbytes / (tc / 1e3) / 1e9, 1),
+                "fused_weight_GBps_warm": round(wbytes / (tf / 1e3) / 1e9, 1), "weight_bytes": wbytes}
     torch.cuda.empty_cache()
     return res
 
