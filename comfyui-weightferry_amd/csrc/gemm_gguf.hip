@@ -10,6 +10,7 @@
 
 #include <mutex>
 #include <type_traits>
+#include <utility>
 
 #include "kquant.h"
 #include "lds_ring.h"
@@ -477,14 +478,14 @@ __global__ __launch_bounds__(512) void gemm_gguf_dl(const uint16_t* __restrict__
 // With few rows of activations the product is bound by reading the weight, so the layout streams the quantised
 // weight through the whole chip exactly once: workgroup b takes the 16 NR weight rows [16 NR b, +16 NR) over all
 // of K (NR groups of 16 rows, each activation fragment feeding NR MFMAs: every workgroup re-reads the activations
-// from L2, so NR = 2 halves that traffic -- 1.1-1.7x faster than NR = 1 on the Wan shapes at 16-64 rows), its 8
-// waves taking super-blocks w, w + 8, w + 16, ..., each with the raw bytes of its next two super-blocks in flight
-// (two register sets). Lane l dequantises the 8 values [8 (l / 16), +8) of each
+// from L2, so NR = 2 halves that traffic -- 1.1-1.7x faster than NR = 1 on the Wan shapes at 16-64 rows), its NW
+// waves taking super-blocks w, w + NW, w + 2 NW, ..., each with the raw bytes of its next two super-blocks in
+// flight (two register sets). Lane l dequantises the 8 values [8 (l / 16), +8) of each
 // 32-value stage of weight row 16 b + l % 16 straight into its B fragment of v_mfma_f32_16x16x32_bf16 (lane l:
 // column l % 16, K offset 8 (l / 16)); its A fragment is the 8 activations of row 16 mt + l % 16 at the same K
 // offset, read from global memory (a few rows: they stay in the L2). Result layout: lane l, register i -> row
-// 4 (l / 16) + i, column l % 16. The waves' partial sums meet in LDS and are added in wave order 0, 1, ..., 7. Rows
-// past M or N read the last valid row and are not stored.
+// 4 (l / 16) + i, column l % 16. The waves' partial sums meet in LDS and are added in wave order 0, 1, ..., NW - 1.
+// Rows past M or N read the last valid row and are not stored.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <int QT>
@@ -601,14 +602,22 @@ __device__ __forceinline__ bf16x8 sk_dequant(const SkRaw<QT>& w, int kq) {
     return __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
-constexpr int kSkWaves = 8;
+// f(std::integral_constant<int, 0>{}), ..., f(std::integral_constant<int, N - 1>{}), unrolled at compile time
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_seq(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_seq(f, std::make_integer_sequence<int, N>{});
+}
 
-template <int QT, int MID, bool BIAS, int MT, int NR = 1>
-__global__ __launch_bounds__(64 * kSkWaves) void gemm_gguf_skinny(const uint16_t* __restrict__ X,
-                                                                  const uint8_t* __restrict__ W,
-                                                                  const uint16_t* __restrict__ bias,
-                                                                  uint16_t* __restrict__ Y, int M, int N, int K) {
-    constexpr int TS = GGUFTs<QT>::TS, NW = kSkWaves;
+template <int QT, int MID, bool BIAS, int MT, int NR, int NW, bool AHEAD>
+__global__ __launch_bounds__(64 * NW) void gemm_gguf_skinny(const uint16_t* __restrict__ X,
+                                                            const uint8_t* __restrict__ W,
+                                                            const uint16_t* __restrict__ bias,
+                                                            uint16_t* __restrict__ Y, int M, int N, int K) {
+    constexpr int TS = GGUFTs<QT>::TS;
     __shared__ f32x4 red[NW][NR * MT][64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -627,47 +636,83 @@ __global__ __launch_bounds__(64 * kSkWaves) void gemm_gguf_skinny(const uint16_t
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[nr][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const int nsb = K / 256;
-    // NR groups of 16 weight rows share each activation fragment (NR MFMAs per activation load)
-    auto stage = [&](auto G, const SkRaw<QT> (&w)[NR], int sb) {
-        constexpr int g = decltype(G)::value;
-        bf16x8 bw[NR];
-#pragma unroll
-        for (int nr = 0; nr < NR; nr++) bw[nr] = sk_dequant<QT, MID, g>(w[nr], kq);
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            const bf16x8 ax = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(xrow[mt] + sb * 256 + 32 * g));
-#pragma unroll
-            for (int nr = 0; nr < NR; nr++)
-                acc[nr][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bw[nr], acc[nr][mt], 0, 0, 0);
-        }
-    };
-    auto superblock = [&](const SkRaw<QT> (&w)[NR], int sb) {
-        stage(std::integral_constant<int, 0>{}, w, sb);
-        stage(std::integral_constant<int, 1>{}, w, sb);
-        stage(std::integral_constant<int, 2>{}, w, sb);
-        stage(std::integral_constant<int, 3>{}, w, sb);
-        stage(std::integral_constant<int, 4>{}, w, sb);
-        stage(std::integral_constant<int, 5>{}, w, sb);
-        stage(std::integral_constant<int, 6>{}, w, sb);
-        stage(std::integral_constant<int, 7>{}, w, sb);
-    };
     auto load = [&](SkRaw<QT> (&w)[NR], int sb) {
 #pragma unroll
         for (int nr = 0; nr < NR; nr++) sk_load<QT>(wrow[nr] + (int64_t)sb * TS, kq, w[nr]);
     };
-    // super-blocks wave, wave + NW, ...: two raw register sets, each refilled two super-blocks ahead
-    SkRaw<QT> wa[NR], wb[NR];
-    int sb = wave;
-    if (sb < nsb) load(wa, sb);
-    if (sb + NW < nsb) load(wb, sb + NW);
-    while (sb < nsb) {
-        superblock(wa, sb);
-        if (sb + 2 * NW < nsb) load(wa, sb + 2 * NW);
-        sb += NW;
-        if (sb >= nsb) break;
-        superblock(wb, sb);
-        if (sb + 2 * NW < nsb) load(wb, sb + 2 * NW);
-        sb += NW;
+    // NR groups of 16 weight rows share each activation fragment (NR MFMAs per activation load)
+    auto mfmas = [&](const bf16x8 (&bw)[NR], const bf16x8& ax, int mt) {
+#pragma unroll
+        for (int nr = 0; nr < NR; nr++)
+            acc[nr][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bw[nr], acc[nr][mt], 0, 0, 0);
+    };
+    auto dequant = [&](auto G, const SkRaw<QT> (&w)[NR], bf16x8 (&bw)[NR]) {
+#pragma unroll
+        for (int nr = 0; nr < NR; nr++) bw[nr] = sk_dequant<QT, MID, decltype(G)::value>(w[nr], kq);
+    };
+    auto act = [&](int mt, int sb, int g) {
+        return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(xrow[mt] + sb * 256 + 32 * g));
+    };
+    SkRaw<QT> w[2][NR];
+    if constexpr (AHEAD) {
+        static_assert(MT == 1, "activations one super-block ahead: one row group");
+        // one activation row group: its 8 fragments of a super-block fit in registers, so they are loaded one
+        // super-block ahead, issued in the order A(next), compute(current), raw(current + 2). The loads a compute
+        // waits for are then always older than those left in flight, and the in-order load counter never holds a
+        // compute back for a prefetch. Super-blocks wave + NW i, i < cnt; loads past the last one repeat it (their
+        // registers are never used), so every round issues the same loads.
+        bf16x8 ax[2][8];
+        auto load_act = [&](bf16x8 (&a)[8], int sb) {
+#pragma unroll
+            for (int g = 0; g < 8; g++) a[g] = act(0, sb, g);
+        };
+        auto superblock = [&](const SkRaw<QT> (&wr)[NR], const bf16x8 (&a)[8]) {
+            static_for<8>([&](auto G) {
+                bf16x8 bw[NR];
+                dequant(G, wr, bw);
+                mfmas(bw, a[decltype(G)::value], 0);
+            });
+        };
+        const int cnt = wave < nsb ? (nsb - 1 - wave) / NW + 1 : 0;
+        auto sb_of = [&](int i) { return wave + NW * min(i, cnt - 1); };
+        if (cnt > 0) {
+            load(w[0], sb_of(0));
+            load_act(ax[0], sb_of(0));
+            load(w[1], sb_of(1));
+            int i = 0;
+            for (; i + 2 <= cnt; i += 2) {
+                load_act(ax[1], sb_of(i + 1));
+                superblock(w[0], ax[0]);
+                load(w[0], sb_of(i + 2));
+                load_act(ax[0], sb_of(i + 2));
+                superblock(w[1], ax[1]);
+                load(w[1], sb_of(i + 3));
+            }
+            if (i < cnt) superblock(w[0], ax[0]);
+        }
+    } else {
+        // activation fragments read at each stage; the raw bytes of the next two super-blocks stay in flight (two
+        // register sets, each refilled two super-blocks ahead)
+        auto superblock = [&](const SkRaw<QT> (&wr)[NR], int sb) {
+            static_for<8>([&](auto G) {
+                bf16x8 bw[NR];
+                dequant(G, wr, bw);
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) mfmas(bw, act(mt, sb, decltype(G)::value), mt);
+            });
+        };
+        int sb = wave;
+        if (sb < nsb) load(w[0], sb);
+        if (sb + NW < nsb) load(w[1], sb + NW);
+        while (sb < nsb) {
+            superblock(w[0], sb);
+            if (sb + 2 * NW < nsb) load(w[0], sb + 2 * NW);
+            sb += NW;
+            if (sb >= nsb) break;
+            superblock(w[1], sb);
+            if (sb + 2 * NW < nsb) load(w[1], sb + 2 * NW);
+            sb += NW;
+        }
     }
 #pragma unroll
     for (int nr = 0; nr < NR; nr++)
@@ -841,15 +886,16 @@ struct SplitPlan {
     int64_t bytes() const { return counter_bytes + part_bytes; }
 };
 
-// Where the split form is the faster one (measured on MI355X against gemm_gguf_skinny, Q4_K / Q6_K, Wan-14B shapes):
-// a deep product (K >= 2 N: 5120 x 13824, 14 slices of 4 super-blocks) with at most 8 rows, 4-7 % faster (Q4_K
-// 27.9 / 31.1 us against 29.2 / 32.6 us at 1 / 8 rows). Shallower products and more rows are faster in
-// gemm_gguf_skinny, whose one workgroup per 32 weight rows needs no hand-over of partial sums between workgroups
-// (5120 x 5120 Q4_K at 32 rows: 14.4 us against 27.9 us split).
+// Where the split form is the faster one (measured on MI355X against gemm_gguf_skinny, Q4_K / Q6_K, cold weights):
+// at most 8 rows of a narrow, deep product (N <= 2048, K >= 8192, K >= 2 N), whose few-rows grid leaves CUs idle:
+// 2048 x 8192 at 1 row 12.6 us against 17.1 (Q4_K), 16.3 against 20.3 (Q6_K). Wider products fill the chip with
+// few-rows workgroups, which need no hand-over of partial sums (5120 x 13824 Q4_K at 1 row: 25.2 us against 30.9
+// split; 3072 x 13824 Q6_K: 27.5 against 36.1); shallower ones gain nothing from more slices (1536 x 5120 Q4_K at 4
+// rows: 9.8 against 11.5).
 static constexpr int kSplitMaxRows = 8;
 
 static bool split_takes(int64_t M, int64_t N, int64_t K) {
-    return M >= 1 && M <= kSplitMaxRows && N >= 1 && N <= (int64_t)kSplitCounters * kSpRows && K >= 2 * N;
+    return M >= 1 && M <= kSplitMaxRows && N >= 1 && N <= 2048 && K >= 8192 && K >= 2 * N;
 }
 
 static SplitPlan split_plan(int64_t M, int64_t N, int64_t K) {
@@ -908,12 +954,12 @@ static void launch_splitk_mid(int mid, const uint16_t* X, const uint8_t* W, cons
     else launch_splitk<QT, WF_F32>(X, W, bias, Y, M, N, K, p, ws, st);
 }
 
-template <int QT, int MID, int MT, int NR = 1>
+template <int QT, int MID, int MT, int NR, int NW, bool AHEAD = false>
 static void launch_skinny(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
                           hipStream_t s) {
     const dim3 grid((unsigned)((N + 16 * NR - 1) / (16 * NR)));
-    if (bias) gemm_gguf_skinny<QT, MID, true, MT, NR><<<grid, 64 * kSkWaves, 0, s>>>(X, W, bias, Y, M, N, K);
-    else gemm_gguf_skinny<QT, MID, false, MT, NR><<<grid, 64 * kSkWaves, 0, s>>>(X, W, bias, Y, M, N, K);
+    if (bias) gemm_gguf_skinny<QT, MID, true, MT, NR, NW, AHEAD><<<grid, 64 * NW, 0, s>>>(X, W, bias, Y, M, N, K);
+    else gemm_gguf_skinny<QT, MID, false, MT, NR, NW, AHEAD><<<grid, 64 * NW, 0, s>>>(X, W, bias, Y, M, N, K);
 }
 
 template <int QT, int MID, int VM, int VN, int WM, int WN>
@@ -931,9 +977,18 @@ template <int QT, int MID>
 static void launch(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
                    hipStream_t s) {
     // few rows: 32 weight rows per workgroup (two 16-row groups sharing each activation fragment)
-    if (M <= 16) { launch_skinny<QT, MID, 1, 2>(X, W, bias, Y, M, N, K, s); return; }
-    if (M <= 32) { launch_skinny<QT, MID, 2, 2>(X, W, bias, Y, M, N, K, s); return; }
-    if (M <= 64) { launch_skinny<QT, MID, 4, 2>(X, W, bias, Y, M, N, K, s); return; }
+    // Up to 8 rows the activations go one super-block ahead: 10-22 % faster than the per-stage reads (Wan shapes,
+    // cold weights); from 9 rows on, their 16 distinct rows per fragment make it slower. Q6_K's dequantisation takes
+    // more registers: its 16-row, 4-wave workgroups (twice as many) run 5-20 % faster than 32 rows over 8 waves on
+    // the Wan shapes, and twice as fast on 2048-4096 x 13824, where 32-row workgroups leave CUs idle.
+    if (M <= 8) {
+        if constexpr (QT == 14) launch_skinny<QT, MID, 1, 1, 4, true>(X, W, bias, Y, M, N, K, s);
+        else launch_skinny<QT, MID, 1, 2, 8, true>(X, W, bias, Y, M, N, K, s);
+        return;
+    }
+    if (M <= 16) { launch_skinny<QT, MID, 1, 2, 8>(X, W, bias, Y, M, N, K, s); return; }
+    if (M <= 32) { launch_skinny<QT, MID, 2, 2, 8>(X, W, bias, Y, M, N, K, s); return; }
+    if (M <= 64) { launch_skinny<QT, MID, 4, 2, 8>(X, W, bias, Y, M, N, K, s); return; }
     auto cost = [&](int bn) {
         const int64_t tiles = (int64_t)((M + 255) / 256) * ((N + bn - 1) / bn);
         return (tiles + 255) / 256 * bn;

@@ -104,8 +104,8 @@ int wf_linear_gguf(const void* x_bf16, int64_t M, int64_t K, const void* wq, int
                    const void* bias_bf16, void* out_bf16, int mid_dt, void* stream);
 
 /* wf_linear_gguf with a caller-provided workspace, for the same reference call site (enhancers/gguf_dequant.py:
- * 296-326 followed by ComfyUI-GGUF's F.linear). A deep product (K >= 2 N) with 1 <= M <= 8 rows is split along K
- * over many more workgroups than weight rows allow: each writes float32 partial sums into the workspace, and the
+ * 296-326 followed by ComfyUI-GGUF's F.linear). A narrow, deep product (N <= 2048, K >= 8192, K >= 2 N) with
+ * 1 <= M <= 8 rows is split along K over many more workgroups than weight rows allow: each writes float32 partial sums into the workspace, and the
  * last workgroup of each column tile adds them in a fixed order (the result is the same on every run). Workspace:
  * 256-byte aligned, at least the bytes wf_linear_gguf_workspace gives; its first 16 KiB are counters that must be
  * zero on entry and are zero again when the call has run, whatever its shape (a workspace cleared once can be reused

@@ -140,13 +140,15 @@ def fused_ws(native, x, raw_dev, qtype, N, bias=None, mid=0, ws=None):
 
 @pytest.mark.parametrize("qtype", [12, 13, 14])
 @pytest.mark.parametrize("mid", [0, 2])
-@pytest.mark.parametrize("M,N,K,with_bias", [(1, 300, 768, True), (5, 5120, 13824, False), (8, 61, 512, True),
-                                             (3, 1000, 2048, False), (7, 384, 5120, True), (8, 640, 1280, False),
-                                             (2, 130, 13824, True), (9, 320, 768, True), (4, 5120, 5120, False)])
+@pytest.mark.parametrize("M,N,K,with_bias", [(1, 300, 8192, True), (5, 2048, 8192, False), (8, 61, 8448, True),
+                                             (3, 1000, 13824, False), (7, 384, 9728, True), (8, 640, 8192, False),
+                                             (2, 130, 13824, True), (9, 320, 8192, True), (4, 2048, 5120, False),
+                                             (6, 1000, 5120, True), (1, 4100, 8192, False)])
 def test_split_k_whole_output(native, qtype, mid, M, N, K, with_bias):
-    # up to 8 activation rows of a deep product (K >= 2 N) take the split-K form (128 weight rows per workgroup, K in
-    # slices of 1-4 super-blocks, partial sums added by the last workgroup of each column tile): ragged M, N and
-    # slices, every output element checked; 9 rows, or K < 2 N, go to the few-rows kernel without the workspace
+    # up to 8 activation rows of a narrow, deep product (N <= 2048, K >= 8192, K >= 2 N) take the split-K form (128
+    # weight rows per workgroup, K in slices of 1-4 super-blocks, partial sums added by the last workgroup of each
+    # column tile): ragged M, N and slices, every output element checked; 9 rows, N > 2048 or K < 8192 go to the
+    # few-rows kernel without the workspace
     raw = encode.random_blocks(qtype, N * K // 256, seed=qtype * 5 + M, family="normal")
     g = torch.Generator().manual_seed(M * 17 + N)
     x = torch.randn((M, K), generator=g).to(torch.bfloat16)
@@ -154,7 +156,7 @@ def test_split_k_whole_output(native, qtype, mid, M, N, K, with_bias):
     print(f"case split-K qtype={qtype} mid={mid} M={M} N={N} K={K}", flush=True)
     y, ws, need = fused_ws(native, x.cuda(), torch.from_numpy(raw).cuda(), qtype, N,
                            bias=bias.cuda() if with_bias else None, mid=mid)
-    assert (need > 0) == (M <= 8 and K >= 2 * N)
+    assert (need > 0) == (M <= 8 and N <= 2048 and K >= 8192 and K >= 2 * N)
     check(y, x, weight_bf16(raw, qtype, mid, N, K), bias=bias)
     assert not ws[:16384].any()                          # the counters are back to zero
 
@@ -164,12 +166,12 @@ def test_split_k_reuses_its_workspace_and_repeats_bits(native):
     # bits as its first run -- the partial sums are added in slice order whichever workgroup arrives last
     qtype, K = 12, 13824
     raws = {N: torch.from_numpy(encode.random_blocks(qtype, N * K // 256, seed=N, family="normal")).cuda()
-            for N in (5120, 1280)}
+            for N in (2048, 1280)}
     g = torch.Generator().manual_seed(3)
     x = torch.randn((8, K), generator=g).to(torch.bfloat16).cuda()
-    y1, ws, n1 = fused_ws(native, x, raws[5120], qtype, 5120)
+    y1, ws, n1 = fused_ws(native, x, raws[2048], qtype, 2048)
     y2, ws, n2 = fused_ws(native, x[:3].contiguous(), raws[1280], qtype, 1280, ws=ws)
-    y3, ws, _ = fused_ws(native, x, raws[5120], qtype, 5120, ws=ws)
+    y3, ws, _ = fused_ws(native, x, raws[2048], qtype, 2048, ws=ws)
     assert n1 > 0 and n2 > 0
     assert torch.equal(y1.view(torch.int16), y3.view(torch.int16))
     check(y2, x[:3].cpu(), weight_bf16(raws[1280].cpu().numpy(), qtype, 0, 1280, K))
@@ -177,7 +179,7 @@ def test_split_k_reuses_its_workspace_and_repeats_bits(native):
 
 def test_split_k_rejects_a_short_workspace(native):
     import ctypes
-    M, N, K = 8, 256, 768
+    M, N, K = 8, 256, 8192
     need = ctypes.c_int64()
     assert native.lib().wf_linear_gguf_workspace(M, N, K, ctypes.byref(need)) == 0 and need.value > 0
     x = torch.zeros((M, K), dtype=torch.bfloat16, device="cuda")

@@ -37,7 +37,7 @@ def _workspace(native, M, N, K):
 def test_noalloc_equals_the_workspace_entry_point(native, qtype):
     g = torch.Generator().manual_seed(qtype)
     K = 13824
-    cases = [(8, 5120, True), (3, 1280, False)]          # the second call smaller than the first
+    cases = [(8, 2048, True), (3, 1280, False)]          # the second call smaller than the first
     for M, N, with_bias in cases:
         print(f"case noalloc qtype={qtype} M={M} N={N} K={K}", flush=True)
         raw = torch.from_numpy(encode.random_blocks(qtype, N * K // 256, seed=N + qtype, family="normal")).cuda()
@@ -62,8 +62,8 @@ def test_noalloc_without_split_is_the_plain_entry_point(native):
 
 
 def test_noalloc_refuses_a_shape_beyond_its_scratch(native):
-    # 8 rows of a 32768 x 65536 Q4_K weight: 64 slices x 8 x 32768 float32 partial sums = 64 MiB > 16 MiB
-    M, N, K = 8, 32768, 65536
+    # 8 rows of a 2048 x 307200 Q4_K weight: 300 slices x 8 x 2048 float32 partial sums = 18.75 MiB > 16 MiB
+    M, N, K = 8, 2048, 307200
     need, _ = _workspace(native, M, N, K)
     assert need > 16 << 20
     raw = torch.empty(N * K // 256 * 144, dtype=torch.uint8, device="cuda")
