@@ -5,7 +5,7 @@ At import it installs the GGUF dequantisation patch when ComfyUI-GGUF is loaded,
 (__init__.py:94-95 of the reference), and registers the block-streaming node WeightFerryDiT under the reference's
 name (__init__.py:104-132).
 
-Sub-modules (the reference's names): enhancers.gguf_dequant, enhancers.fused_int8, enhancers.fused_kernels,
+Sub-modules (the reference's names): enhancers.gguf_dequant, enhancers.fused_int8, enhancers.int8_block,
 enhancers.fused_state, enhancers.fused_gguf (dequant + GEMM in one kernel), streaming.{common,state,profiler,
 load_steps,dit_node,node}, core.tiers.{pinned,sources,plan,gguf_file}, core.env, utils.logging; the kernels live in
 lib/libweightferry_hip.so

@@ -28,8 +28,13 @@ from collections import namedtuple
 import torch
 
 from .. import _native
-from .fused_kernels import PRE_GELU, PRE_LNMOD, PRE_MOD, QUANT_MODES
 from .fused_state import _count, _state, _tls  # noqa: F401 -- _state is part of this module's public surface
+
+# the operation wf_quant_rows_i8_pre applies to a row before its rotation (the reference's codes,
+# enhancers/fused_kernels.py:14-18): GELU of the bf16 input; the scale-and-shift bf16(bf16(x * (1 + scale)) + shift);
+# LayerNorm without affine, then that scale-and-shift. Rows with no operation go through wf_quant_rows_i8.
+PRE_GELU, PRE_MOD, PRE_LNMOD = 1, 2, 3
+QUANT_MODES = {"plain": 0, "convrot": 1}
 
 # widest rows the quantiser takes (wf_quant_rows_i8: four waves per row beyond 6144 / 8192 values)
 _QUANT_MAX_K = {QUANT_MODES["plain"]: 32768, QUANT_MODES["convrot"]: 32768}
