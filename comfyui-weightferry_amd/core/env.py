@@ -20,6 +20,9 @@ DEFAULTS = {
     "WEIGHTFERRY_MODEL_FILE": None,        # the GGUF file the SSD tier reads blocks from (else a cache file)
     "WEIGHTFERRY_CACHE_DIR": None,         # directory of the SSD tier's cache files (default: temp directory)
     "WEIGHTFERRY_RAM_MARGIN_GB": "6",      # RAM kept free besides the RAM tier when its budget is automatic
+    "WEIGHTFERRY_DISK_THREADS": None,      # reader threads of the ring (default: the probe's fastest count)
+    "WEIGHTFERRY_DISK_PROBE_MB": "512",    # size of the drive probe's scratch file
+    "WEIGHTFERRY_PERSIST_GB": "0",         # > 0: keep SSD-tier cache files for later runs, this many GB at most
     # chunk (sub-block) streaming
     "WEIGHTFERRY_CHUNK": None,             # "1": the node streams chunks of blocks; "0" / unset: whole blocks
     "WEIGHTFERRY_CHUNK_MB": "96",          # bytes of layers per chunk

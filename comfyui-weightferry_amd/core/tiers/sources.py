@@ -8,6 +8,7 @@ layout, with file-adjacent pieces merged (a file written in the flat layout's or
 block). ``DiskRing`` is the native ring (wf_ring_*): reader threads fill ``depth`` pinned buffers in cyclic block
 order; the streaming state copies out of them with submit / wait, host code with acquire / release."""
 import ctypes
+import os
 
 import numpy as np
 import torch
@@ -83,6 +84,25 @@ def gguf_block_source(path, block_param_names, offsets, reader=None):
             raise ValueError(f"block of {names[0]} has other tensor sizes than the first streamed block")
         blocks.append(merge_pieces(pcs))
     return PieceFileSource(path, blocks), sizes0
+
+
+def read_packed(source, d, off, n, out):
+    """Bytes [off, off + n) of block d's packed bytes, read from the source's file with ordinary reads into ``out``
+    (a writable buffer of n bytes); bytes no piece covers (padding) are zero. For the few reads outside the ring's
+    order (layers called before a forward's first block)."""
+    mv = memoryview(out).cast("B")
+    if mv.nbytes != n:
+        raise ValueError(f"a {mv.nbytes}-byte buffer for {n} bytes")
+    mv[:] = bytes(n)
+    with open(source.path, "rb", buffering=0) as f:
+        for fo, ln, po in source.pieces()[d]:
+            a, b = max(off, po), min(off + n, po + ln)
+            done = 0
+            while a + done < b:
+                got = os.preadv(f.fileno(), [mv[a - off + done:b - off]], fo + a - po + done)
+                if got <= 0:
+                    raise OSError(f"{source.path}: short read at {fo + a - po + done}")
+                done += got
 
 
 class DiskRing:

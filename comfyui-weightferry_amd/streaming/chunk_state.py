@@ -22,7 +22,16 @@ Copies: a unit's parameters are grouped into runs of consecutive parameters of t
 is one hipMemcpyAsync of the host bytes (alignment padding included) into the slot, placed so every parameter keeps
 its 256-byte alignment. When a block calls its layers in registration order, a unit is one copy.
 
-Not supported here (block streaming is used instead): the SSD tier, the single-buffer mode, the profiler."""
+SSD tier: a block without a host flat is read by the native ring (host mode: acquire / release), in the tier's
+order; the ring buffer holding it is the copy source of its units (and of its layers in the calibration forward)
+until a unit of the next SSD-tier block needs the ring, and is handed back after the copies queued out of it (on
+every stream that copied from it). Blocks a forward skips are read and handed straight back, so the ring stays in
+step; a forward that stops before the tier's last block restarts the ring's cycle. A unit is never copied for a
+block that has finished: when a block starts, units of earlier blocks that were not copied are dropped for this
+forward. A layer of an SSD-tier block called before any block of the forward is read from the file on its own (not
+through the ring, which is in the tier's order).
+
+Not supported here (block streaming is used instead): the single-buffer mode, the profiler."""
 import time
 
 import torch
@@ -56,8 +65,13 @@ class _ChunkState(_StreamState):
     """Per-model chunk streaming state (double-buffered, RAM tier)."""
 
     def __init__(self, owner, device, streaming_blocks, host_flats, host_views, rest, specs, offsets, chunk_bytes,
-                 num_slots, order_cache=None):
-        super().__init__(owner, device, streaming_blocks, host_flats, host_views, rest, [], [], True)
+                 num_slots, order_cache=None, ring=None, disk_index=None, source=None):
+        super().__init__(owner, device, streaming_blocks, host_flats, host_views, rest, [], [], True, ring=ring,
+                         disk_index=disk_index)
+        self.source = source
+        self._held = None                 # [block, host address, ring slot, streams that copied from it]
+        self._ring_next = 0               # position in the SSD tier of the next block the ring serves
+        self._staging = None              # (pinned buffer, event of its last copy) for layers read outside the ring
         self.chunk_mode = True
         self.specs, self.offsets = specs, offsets
         self.chunk_bytes = int(chunk_bytes)
@@ -106,12 +120,77 @@ class _ChunkState(_StreamState):
         for j, view in pairs:
             params[j].data = view
 
-    def _copy(self, s, runs, dst, stream):
-        src = self.host_flats[s].data_ptr()
+    def _copy(self, s, runs, dst, stream, src=None):
+        if src is None:
+            src = self._host_base(s, stream)
         base = dst.data_ptr()
         for host_off, buf_off, n in runs:
             _native.call("wf_h2d_async", base + buf_off, src + host_off, n, stream)
             self.copies += 1
+
+    # ---- the SSD tier's ring
+    def _host_base(self, s, stream):
+        """Host address of block s's packed bytes for a copy on ``stream``: its pinned flat, or the ring buffer
+        holding it (the ring is moved on to it first)."""
+        if s not in self.disk_index:
+            return self.host_flats[s].data_ptr()
+        if self._held is None or self._held[0] != s:
+            self._ring_release()
+            d, n = self.disk_index[s], len(self.disk_index)
+            while self._ring_next != d:   # SSD-tier blocks this forward skipped
+                _, slot = self.ring.acquire(self._ring_next)
+                self.ring.release(slot)
+                self._ring_next = (self._ring_next + 1) % n
+            buf, slot = self.ring.acquire(d)
+            self._ring_next = (d + 1) % n
+            self._held = [s, buf.data_ptr(), slot, set()]
+        self._held[3].add(stream)
+        return self._held[1]
+
+    def _ring_release(self):
+        """Hand the held ring buffer back, refilled only after every copy queued out of it."""
+        if self._held is None:
+            return
+        _, _, slot, streams = self._held
+        self._held = None
+        streams = sorted(streams)
+        last = streams[-1]
+        for other in streams[:-1]:
+            ev = _native.Event()
+            ev.record(other)
+            _native.stream_wait(last, ev)
+            self._retired.append(ev)
+        self.ring.release(slot, last)
+
+    def _staged_copy(self, s, runs, dst, stream):
+        """Copy runs of SSD-tier block s into ``dst`` on ``stream`` from the file itself (via the staging buffer),
+        leaving the ring where it is."""
+        src, runs = self._read_outside(s, runs)
+        self._copy(s, runs, dst, stream, src=src)
+        ev = _native.Event()
+        ev.record(stream)
+        if self._staging[1] is not None:
+            self._retired.append(self._staging[1])
+        self._staging = (self._staging[0], ev)
+
+    def _read_outside(self, s, runs):
+        """Runs of an SSD-tier block read from the source file into the pinned staging buffer, back to back (after
+        the staging buffer's previous copy); returns (staging address, runs re-based on it)."""
+        from ..core.tiers.sources import read_packed
+        total = sum(n for _, _, n in runs)
+        if self._staging is None or self._staging[0].numel() < total:
+            size = max(total, max(self.leaf_bytes.values()))
+            buf = torch.empty(size, dtype=torch.uint8, pin_memory=torch.cuda.is_available())
+            self._staging = (buf, None)
+        buf, ev = self._staging
+        if ev is not None:
+            ev.synchronize()
+        out, pos = [], 0
+        for host_off, buf_off, n in runs:
+            read_packed(self.source, self.disk_index[s], host_off, n, buf[pos:pos + n].numpy())
+            out.append((pos, buf_off, n))
+            pos += n
+        return buf.data_ptr(), out
 
     # ---- calibration (the first forward after the capture)
     def _calib_leaf_pre(self, module):
@@ -119,7 +198,11 @@ class _ChunkState(_StreamState):
         if s == 0 and leaf not in self.order:
             self.order.append(leaf)
         # on the compute stream: ordered after every kernel of the previous leaf that read the scratch buffer
-        self._copy(s, self.leaf_plan[leaf][0], self.scratch, self.compute_stream())
+        compute = self.compute_stream()
+        if s in self.disk_index and self.blocks_started == 0:
+            self._staged_copy(s, self.leaf_plan[leaf][0], self.scratch, compute)
+        else:
+            self._copy(s, self.leaf_plan[leaf][0], self.scratch, compute)
         self._bind(s, self.scratch_views[leaf])
 
     def use_learned_order(self, order_cache):
@@ -194,6 +277,7 @@ class _ChunkState(_StreamState):
         self.u_issued = [False] * n
         self.u_bound = [False] * n
         self.u_complete = [False] * n
+        self.u_dead = [False] * n         # dropped for this forward: its layers, if called, go the outside way
         self.u_spare = {}                 # unit -> spare index
         self.u_done = [set() for _ in range(n)]
         self.next_issue = 0
@@ -267,7 +351,11 @@ class _ChunkState(_StreamState):
         runs, where, total = self.leaf_plan[leaf]
         if self.outside_buf is None or self.outside_buf.numel() < total:
             self.outside_buf = torch.empty(max(self.leaf_bytes.values()), dtype=torch.uint8, device=self.device)
-        self._copy(s, runs, self.outside_buf, self.compute_stream())
+        compute = self.compute_stream()
+        if s in self.disk_index:
+            self._staged_copy(s, runs, self.outside_buf, compute)
+        else:
+            self._copy(s, runs, self.outside_buf, compute)
         self._bind(s, self._views(self.outside_buf, where))
         self._fwd["outside"] += 1
 
@@ -284,6 +372,9 @@ class _ChunkState(_StreamState):
             return
         t = self.type_of_leaf[leaf]
         u = s * self.n_types + t
+        if self.u_dead[u]:
+            self._bind_outside(s, leaf)
+            return
         if self.u_bound[u]:
             return
         if not self.u_issued[u]:
@@ -311,16 +402,23 @@ class _ChunkState(_StreamState):
         s, leaf = self.mod_info[id(module)]
         t = self.type_of_leaf[leaf]
         u = s * self.n_types + t
+        if self.u_dead[u]:
+            return
         self.u_done[u].add(leaf)
         if len(self.u_done[u]) == len(self.types[t]):
             self._complete(u)
 
     def block_pre(self, s):
         if self.calibrating:
+            self.blocks_started += 1
             return
-        # units of earlier blocks that a caching wrapper skipped never ran: their slots are free
+        # units of earlier blocks that were never copied (a caching wrapper skipped their block, or layers it does
+        # not call) are dropped for this forward; those copied but not run free their slots
         for u in range(s * self.n_types):
-            if self.u_issued[u] and not self.u_complete[u]:
+            if not self.u_issued[u]:
+                self.u_issued[u] = self.u_complete[u] = self.u_dead[u] = True
+        for u in range(s * self.n_types):
+            if not self.u_complete[u]:
                 self._complete(u)
         if self.blocks_started == 0:
             self.pump()
@@ -343,6 +441,13 @@ class _ChunkState(_StreamState):
 
     def end_forward(self):
         fwd = self._fwd
+        if self.ring is not None:
+            self._ring_release()
+            if self._ring_next != 0:
+                # the forward stopped before the SSD tier's last block: the ring restarts its cycle (it waits for
+                # the copies out of its buffers itself)
+                self.ring.resync()
+                self._ring_next = 0
         if self.calibrating:
             self.finish_calibration()
         elif fwd is not None and _env.get("WEIGHTFERRY_CHUNK_LOG") == "1":
@@ -367,6 +472,8 @@ class _ChunkState(_StreamState):
                     p.data = r
 
     def close(self):
+        if self.ring is not None and self._held is not None:
+            self._ring_release()
         super().close()
         for e in getattr(self, "slot_free_events", []) + getattr(self, "unit_events", []) + self._retired:
             if e is not None:
@@ -374,5 +481,8 @@ class _ChunkState(_StreamState):
         self._retired = []
         for _, ev, _ in self.spares:
             ev.close()
+        if self._staging is not None and self._staging[1] is not None:
+            self._staging[1].close()
+        self._staging = None
         self.chunk_slots, self.spares = [], []
         self.scratch = self.outside_buf = None

@@ -81,9 +81,12 @@ def apply_streaming(dit, device="cuda", resident_blocks=0, prefetch_slots=2, pin
     param_name)`` gives a parameter's tensor name in the model file (default "<block list>.<index>.<param name>",
     ComfyUI-GGUF's naming of a DiT's state dict).
 
+    With WEIGHTFERRY_PERSIST_GB > 0 the cache file is kept for later loads with the same block bytes
+    (core.tiers.cache_files.PersistentEntry).
+
     ``chunk``: sub-block streaming (streaming.chunk_state): the GPU holds ``chunk_slots`` chunks of at most
     ``chunk_bytes`` of a block's layers instead of whole blocks; the first forward learns the blocks' call order,
-    kept in ``order_cache`` (a dict) when one is given. RAM tier and double buffering only."""
+    kept in ``order_cache`` (a dict) when one is given. Double buffering only; the SSD tier as above."""
     blocks = list(_blocks(dit))
     if not blocks:
         raise ValueError("the model has no block list (blocks / transformer_blocks / layers / block)")
@@ -95,17 +98,29 @@ def apply_streaming(dit, device="cuda", resident_blocks=0, prefetch_slots=2, pin
     for i in resident_idx:
         blocks[i].to(device)
     owner = object()
+    ssd = _ssd_tier(dit, blocks, stream_idx, model_file, ram_blocks, ssd_layout, ring_depth, ring_threads, direct_io,
+                    tensor_name, ssd_dir)
     if chunk:
-        if ram_blocks is not None and ram_blocks < len(stream_idx):
-            raise ValueError("chunk streaming keeps every streamed block in RAM (no SSD tier)")
         if not double_buffer:
             raise ValueError("chunk streaming is double-buffered")
         state = _build_chunk_state(owner, device, [blocks[i] for i in stream_idx], chunk_bytes, chunk_slots,
-                                   pin_memory, order_cache)
+                                   pin_memory, order_cache, ssd)
         _install_first_block_hook(dit, blocks[0], state, owner)
         _install_chunk_hooks(dit, state, owner)
         setattr(dit, _STATE_ATTR, state)
         return StreamedModel(dit, state, resident_idx, stream_idx, owner)
+    state = _build_state(owner, device, [blocks[i] for i in stream_idx], prefetch_slots, pin_memory, profile, ssd,
+                         double_buffer)
+    _install_first_block_hook(dit, blocks[0], state, owner)
+    _install_block_stream_hooks(dit, state, owner)
+    _install_resident_profile_hooks(dit, blocks, resident_idx, state, owner)
+    setattr(dit, _STATE_ATTR, state)
+    return StreamedModel(dit, state, resident_idx, stream_idx, owner)
+
+
+def _ssd_tier(dit, blocks, stream_idx, model_file, ram_blocks, ssd_layout, ring_depth, ring_threads, direct_io,
+              tensor_name, ssd_dir):
+    """The SSD tier's description for the state builders, or None when every streamed block stays in RAM."""
     ssd = None
     if model_file is None and ram_blocks is not None and ram_blocks < len(stream_idx):
         from ..core.tiers.plan import ssd_positions
@@ -129,10 +144,4 @@ def apply_streaming(dit, device="cuda", resident_blocks=0, prefetch_slots=2, pin
                              f"{want[bad]}")
         ssd = {"positions": positions, "source": source, "depth": ring_depth, "threads": ring_threads,
                "direct": direct_io}
-    state = _build_state(owner, device, [blocks[i] for i in stream_idx], prefetch_slots, pin_memory, profile, ssd,
-                         double_buffer)
-    _install_first_block_hook(dit, blocks[0], state, owner)
-    _install_block_stream_hooks(dit, state, owner)
-    _install_resident_profile_hooks(dit, blocks, resident_idx, state, owner)
-    setattr(dit, _STATE_ATTR, state)
-    return StreamedModel(dit, state, resident_idx, stream_idx, owner)
+    return ssd

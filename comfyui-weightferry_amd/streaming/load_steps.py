@@ -8,6 +8,7 @@ import torch
 
 from ..core import env as _env
 from ..core.tiers.pinned import PinnedHost
+from ..utils.logging import log_info
 from .common import _ACTIVE_ATTR, _flat_layout, _specs, _views
 from .profiler import _StreamProfiler
 from .state import _StreamState
@@ -53,6 +54,69 @@ def _num_slots(prefetch_slots):
     return n
 
 
+def _ssd_cache(blocks, positions, specs, offsets, flat_bytes, ssd):
+    """No model file to read: the SSD tier's blocks go into a cache file (their final bytes, as captured), or come
+    from a persistent entry an earlier load wrote with the same content (WEIGHTFERRY_PERSIST_GB > 0). Returns (the
+    ring's source, the store to delete at teardown or None)."""
+    from ..core.tiers import cache_files as cf
+    cap = float(_env.get("WEIGHTFERRY_PERSIST_GB") or 0) * 1024 ** 3
+    entry = None
+    if cap > 0:
+        layout = ([(tuple(sh), str(dt)) for sh, dt in specs], list(offsets), int(flat_bytes), len(positions))
+        key = cf.content_key(layout, (list(blocks[s].parameters()) for s in positions))
+        entry = cf.PersistentEntry(cf.persistent_dir(ssd.get("cache_dir")), key, len(positions), flat_bytes)
+        if entry.complete():
+            log_info(f"DiT Layer Streaming [persist]: SSD cache reused ({entry.bin}).")
+            return entry.source(), None
+    store = (entry.open_store() if entry is not None
+             else cf.DiskBlockStore(ssd.get("cache_dir") or cf.default_cache_dir(), flat_bytes, len(positions)))
+    stage = torch.empty(flat_bytes, dtype=torch.uint8)
+    views = _views(stage, specs, offsets)
+    for k, s_idx in enumerate(positions):
+        stage.zero_()
+        for p, v in zip(blocks[s_idx].parameters(), views):
+            v.copy_(p.data)
+        store.write_block(k, stage)
+    store.finalize()
+    if entry is not None:
+        freed = entry.commit(cap)
+        log_info(f"DiT Layer Streaming [persist]: SSD cache kept for later runs ({entry.bin})"
+                 + (f"; {freed / 1024 ** 3:.1f} GB of older entries removed." if freed else "."))
+    return store.source(), store
+
+
+def _rest_binding(blocks, host_views):
+    """Bind each block's parameters to its host views; a block without (the SSD tier's) keeps its tensors. Returns
+    the per-block tensors the parameters go back to between forwards."""
+    rest = []
+    for blk, views in zip(blocks, host_views):
+        if views is None:
+            rest.append([p.data for p in blk.parameters()])
+            continue
+        for p, v in zip(blk.parameters(), views):
+            p.data = v
+        rest.append(views)
+    return rest
+
+
+def _open_ring(blocks, positions, specs, offsets, flat_bytes, ssd, device):
+    """The SSD tier's reader ring over its source (the model file's ranges, or a cache file written now): (ring,
+    store to delete at teardown, source), or Nones without SSD-tier blocks."""
+    if not positions:
+        return None, None, None
+    from ..core.tiers.sources import DiskRing
+    source, store = ssd.get("source"), None
+    if source is None:
+        source, store = _ssd_cache(blocks, positions, specs, offsets, flat_bytes, ssd)
+    if source.n_blocks != len(positions):
+        raise ValueError(f"the SSD source has {source.n_blocks} blocks for {len(positions)} positions")
+    if source.block_bytes > flat_bytes:
+        raise ValueError(f"SSD-tier blocks of {source.block_bytes} bytes do not fit the {flat_bytes}-byte slots")
+    ring = DiskRing(source, depth=int(ssd.get("depth", 2)), pin=True, threads=int(ssd.get("threads", 1)),
+                    direct=bool(ssd.get("direct", True)), device=device)
+    return ring, store, source
+
+
 def _build_state(owner, device, blocks, prefetch_slots=2, pin_memory=True, profile=None, ssd=None, double_buffer=True):
     """Capture + slots + state for the given streamed blocks; the blocks' parameters end up bound to their host
     views (their "rest" tensors) until a forward binds them to a slot. ``ssd``: the SSD tier, a dict with
@@ -72,37 +136,8 @@ def _build_state(owner, device, blocks, prefetch_slots=2, pin_memory=True, profi
     num_slots = _num_slots(prefetch_slots) if double_buffer else 1
     slot_flats = [torch.empty(flat_bytes, dtype=torch.uint8, device=device) for _ in range(num_slots)]
     slot_views = [_views(f, specs, offsets) for f in slot_flats]
-    rest = []
-    for blk, views in zip(blocks, host_views):
-        if views is None:
-            rest.append([p.data for p in blk.parameters()])
-            continue
-        for p, v in zip(blk.parameters(), views):
-            p.data = v
-        rest.append(views)
-    ring = store = None
-    if positions:
-        from ..core.tiers.sources import DiskRing
-        source = ssd.get("source")
-        if source is None:
-            # no model file to read: the SSD tier's blocks go into a cache file (their final bytes, as captured)
-            from ..core.tiers.cache_files import DiskBlockStore, default_cache_dir
-            store = DiskBlockStore(ssd.get("cache_dir") or default_cache_dir(), flat_bytes, len(positions))
-            stage = torch.empty(flat_bytes, dtype=torch.uint8)
-            views = _views(stage, specs, offsets)
-            for k, s_idx in enumerate(positions):
-                stage.zero_()
-                for p, v in zip(blocks[s_idx].parameters(), views):
-                    v.copy_(p.data)
-                store.write_block(k, stage)
-            store.finalize()
-            source = store.source()
-        if source.n_blocks != len(positions):
-            raise ValueError(f"the SSD source has {source.n_blocks} blocks for {len(positions)} positions")
-        if source.block_bytes > flat_bytes:
-            raise ValueError(f"SSD-tier blocks of {source.block_bytes} bytes do not fit the {flat_bytes}-byte slots")
-        ring = DiskRing(source, depth=int(ssd.get("depth", 2)), pin=True, threads=int(ssd.get("threads", 1)),
-                        direct=bool(ssd.get("direct", True)), device=device)
+    rest = _rest_binding(blocks, host_views)
+    ring, store, _ = _open_ring(blocks, positions, specs, offsets, flat_bytes, ssd, device)
     state = _StreamState(owner, device, list(blocks), host_flats, host_views, rest, slot_flats, slot_views,
                          is_double=double_buffer, ring=ring, disk_index={s: k for k, s in enumerate(positions)})
     state.disk_store = store
@@ -115,29 +150,31 @@ def _build_state(owner, device, blocks, prefetch_slots=2, pin_memory=True, profi
     return state
 
 
-def _build_chunk_state(owner, device, blocks, chunk_bytes=None, num_slots=None, pin_memory=True, order_cache=None):
+def _build_chunk_state(owner, device, blocks, chunk_bytes=None, num_slots=None, pin_memory=True, order_cache=None,
+                       ssd=None):
     """Capture + chunk streaming state (streaming/load_steps.py:736-753 of the reference): the blocks' host flats as
     for block streaming; the GPU holds ``num_slots`` chunk slots (WEIGHTFERRY_CHUNK_SLOTS, default 4) of at most
     ``chunk_bytes`` of layers each (WEIGHTFERRY_CHUNK_MB, default 96 MB) plus a spare, sized once the first forward
-    has shown the blocks' call order."""
+    has shown the blocks' call order. ``ssd``: the SSD tier as for _build_state; its blocks' chunks are copied out
+    of the reader ring's buffers."""
     from .chunk_state import _ChunkState
     specs = _check_block_layouts(blocks)
     offsets, flat_bytes = _flat_layout(specs)
-    holders, host_flats, host_views = _capture_streamed_blocks(blocks, specs, offsets, flat_bytes, pin_memory)
-    rest = []
-    for blk, views in zip(blocks, host_views):
-        for p, v in zip(blk.parameters(), views):
-            p.data = v
-        rest.append(views)
+    positions = list((ssd or {}).get("positions") or [])
+    holders, host_flats, host_views = _capture_streamed_blocks(blocks, specs, offsets, flat_bytes, pin_memory,
+                                                               skip=set(positions))
+    rest = _rest_binding(blocks, host_views)
+    ring, store, source = _open_ring(blocks, positions, specs, offsets, flat_bytes, ssd, device)
     if chunk_bytes is None:
         chunk_bytes = int(float(_env.get("WEIGHTFERRY_CHUNK_MB")) * 1024 ** 2)
     if num_slots is None:
         num_slots = int(_env.get("WEIGHTFERRY_CHUNK_SLOTS"))
     state = _ChunkState(owner, device, list(blocks), host_flats, host_views, rest, specs, offsets, chunk_bytes,
-                        num_slots, order_cache)
+                        num_slots, order_cache, ring=ring, disk_index={s: k for k, s in enumerate(positions)},
+                        source=source)
     state.holders = holders
     state.flat_bytes = flat_bytes
-    state.disk_store = None
+    state.disk_store = store
     return state
 
 

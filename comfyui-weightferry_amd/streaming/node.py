@@ -13,16 +13,19 @@ Block 0 stays resident (resident_blocks >= 1), as in the reference.
 WEIGHTFERRY_CHUNK=1 streams chunks of blocks instead of whole blocks (streaming.chunk_state; the reference's
 dit_node.py:215-246): the GPU holds WEIGHTFERRY_CHUNK_SLOTS chunks of WEIGHTFERRY_CHUNK_MB of layers, the call
 order learned at the first load is kept with the node for later loads, and with resident_blocks <= 1 block 0
-streams too (WEIGHTFERRY_CHUNK_BLOCK0=0 keeps it resident). Chunk mode needs Double Buffer and the RAM tier; with
-either missing the node streams whole blocks.
+streams too (WEIGHTFERRY_CHUNK_BLOCK0=0 keeps it resident). Chunk mode needs Double Buffer (without it the node
+streams whole blocks); with tiering Auto the chunks of SSD-tier blocks are copied out of the reader ring.
 
 Tiering "Auto" puts the streamed blocks over the RAM budget (``ram_budget_gb``; 0: the available RAM minus
 WEIGHTFERRY_RAM_MARGIN_GB, see core.tiers.plan.plan_tiers) on the SSD tier:
 read straight from the GGUF model file named by WEIGHTFERRY_MODEL_FILE (ComfyUI-GGUF's loaded tensors do not carry
-their file's path), or else from a cache file of their captured bytes (WEIGHTFERRY_CACHE_DIR). Options of the reference that belong to other paths -- SageAttention, fp8 storage format,
+their file's path), or else from a cache file of their captured bytes (WEIGHTFERRY_CACHE_DIR; kept for later runs
+with WEIGHTFERRY_PERSIST_GB > 0). The ring's depth and reader threads follow the drive's measured read rate
+(core.tiers.disk_io.probe_disk, remembered for a week). Options of the reference that belong to other paths -- SageAttention, fp8 storage format,
 self-managed residents, auto-configuration, the VRAM budget -- are accepted and logged as not applied; the node
 then streams as with their defaults."""
 import math
+import os
 
 from ..core import env as _env
 from ..utils.logging import log_info, log_warn
@@ -123,9 +126,8 @@ class WeightFerryDiT:
         env_tier = _env.get("WEIGHTFERRY_TIERING")
         tier_auto = (env_tier == "auto") if env_tier else tiering == TIERING_AUTO
         chunk = _env.get("WEIGHTFERRY_CHUNK") == "1"
-        if chunk and (not double or tier_auto):
-            log_info("DiT Layer Streaming [chunks]: chunk streaming needs Double Buffer and the RAM tier; "
-                     "streaming whole blocks.")
+        if chunk and not double:
+            log_info("DiT Layer Streaming [chunks]: chunk streaming needs Double Buffer; streaming whole blocks.")
             chunk = False
         # chunk mode streams block 0 as well when it has the other blocks' layout (the reference's stream_block0)
         uniform0 = len(blocks) > 1 and [(tuple(p.shape), p.dtype) for p in blocks[0].parameters()] == \
@@ -152,34 +154,34 @@ class WeightFerryDiT:
             if not mm.is_device_cuda(dev):
                 return
             _teardown(dit)                    # a previous capture of this model (or another config's)
-            ram_blocks, depth = None, 2
-            if chunk:
-                sm = dit_node.apply_streaming(dit, device=dev, resident_blocks=resident_k, pin_memory=pin_memory,
-                                              chunk=True, order_cache=order_cache)
-                sm.owner_node = owner
-                setattr(dit, _NODE_ATTR, sm)
-                log_info(f"DiT Layer Streaming [Late Offload]: {num_stream} blocks offloaded to pinned RAM, "
-                         f"streamed in chunks.")
-                return
+            ram_blocks, depth, threads = None, 2, 2
             if tier_auto:
+                from ..core.tiers.cache_files import default_cache_dir
                 from ..core.tiers.plan import plan_tiers
                 per = sum(q.numel() * q.element_size() for q in blocks[resident_k].parameters())
-                plan = plan_tiers(num_stream, per, ram_budget_bytes=int(budget * 1024 ** 3) if budget > 0 else None)
-                ram_blocks, depth = plan["ram_blocks"], max(2, plan["ring_depth"])
+                # the drive the SSD tier reads: the model file's, or the cache file's
+                disk_dir = os.path.dirname(os.path.abspath(model_file)) if model_file else default_cache_dir()
+                plan = plan_tiers(num_stream, per, ram_budget_bytes=int(budget * 1024 ** 3) if budget > 0 else None,
+                                  disk_dir=disk_dir)
+                ram_blocks, depth, threads = plan["ram_blocks"], max(2, plan["ring_depth"]), plan["ring_threads"]
+                rate = plan["disk_read_gbps"]
                 log_info(f"DiT Layer Streaming [tiers]: RAM budget {plan['budget'] / 1024 ** 3:.1f} GB: "
                          f"{plan['ram_blocks']} blocks in RAM, {plan['disk_blocks']} on the SSD tier"
-                         + (f" (ring of {plan['ring_depth']})." if plan["disk_blocks"] else "."))
+                         + (f" (ring of {plan['ring_depth']}, {threads} readers"
+                            + (f", drive {rate:.1f} GB/s)." if rate else ").") if plan["disk_blocks"] else "."))
             sm = dit_node.apply_streaming(dit, device=dev, resident_blocks=resident_k, prefetch_slots=prefetch_slots,
                                           pin_memory=pin_memory, model_file=model_file or None, ram_blocks=ram_blocks,
                                           double_buffer=double or (ram_blocks is not None and ram_blocks < num_stream),
-                                          ring_depth=depth, ring_threads=2)
+                                          ring_depth=depth, ring_threads=threads, chunk=chunk,
+                                          order_cache=order_cache if chunk else None)
             sm.owner_node = owner
             setattr(dit, _NODE_ATTR, sm)
             n_ssd = len(sm.state.disk_index)
             src = model_file or (sm.state.disk_store.path if sm.state.disk_store is not None else "?")
+            how = ", streamed in chunks" if chunk else ""
             log_info(f"DiT Layer Streaming [Late Offload]: {num_stream} blocks offloaded ({num_stream - n_ssd} in "
-                     f"pinned RAM, {n_ssd} read from {src})." if n_ssd else
-                     f"DiT Layer Streaming [Late Offload]: {num_stream} blocks offloaded to pinned RAM.")
+                     f"pinned RAM, {n_ssd} read from {src}){how}." if n_ssd else
+                     f"DiT Layer Streaming [Late Offload]: {num_stream} blocks offloaded to pinned RAM{how}.")
 
         def on_detach(p, unpatch_all=True, *args, **kwargs):
             sm = getattr(dit, _NODE_ATTR, None)

@@ -206,12 +206,145 @@ def test_chunk_types_cut_by_bytes():
     assert runs == [(0, 0, 512), (768, 512, 4000)] and where == {0: 0, 1: 256, 3: 512} and total == 4608
 
 
-def test_chunk_mode_rejects_ssd_and_single_buffer():
+def test_chunk_mode_rejects_single_buffer():
     dn = sub("streaming.dit_node")
     with pytest.raises(ValueError):
-        dn.apply_streaming(Model(3, []), device="cpu", pin_memory=False, chunk=True, ram_blocks=1)
-    with pytest.raises(ValueError):
         dn.apply_streaming(Model(3, []), device="cpu", pin_memory=False, chunk=True, double_buffer=False)
+
+
+class FakeRing:
+    """The native reader ring in host mode (acquire / release) on the CPU: it reads the SSD tier's blocks from the
+    source's file into ``depth`` buffers in cyclic order as eagerly as it can -- a buffer is refilled as soon as the
+    event its release recorded has run on the stand-in's streams -- so a copy queued out of a buffer after the
+    buffer was handed back would read another block's bytes, and a layer would see the wrong tag."""
+
+    fn = None
+    made = []
+
+    def __init__(self, source, depth=2, pin=True, threads=1, direct=True, device=None):
+        self.source, self.depth, self.n = source, int(depth), source.n_blocks
+        self.bufs = [torch.zeros(source.block_bytes, dtype=torch.uint8) for _ in range(self.depth)]
+        self.pos = [None] * self.depth            # position each buffer holds
+        self.gate = [None] * self.depth           # event a refill waits for
+        self.cons = self.reads = self.resyncs = 0
+        FakeRing.made.append(self)
+        self._refill()
+
+    def _refill(self):
+        read_packed = sub("core.tiers.sources").read_packed
+        for pos in range(self.cons, self.cons + self.depth):
+            b = pos % self.depth
+            if self.pos[b] == pos or (self.gate[b] is not None and self.gate[b] not in self.fn.L.recorded):
+                continue
+            read_packed(self.source, pos % self.n, 0, self.source.block_bytes, self.bufs[b].numpy())
+            self.pos[b], self.gate[b] = pos, None
+            self.reads += 1
+
+    def acquire(self, d):
+        assert d == self.cons % self.n, (d, self.cons)
+        b = self.cons % self.depth
+        self._refill()
+        if self.pos[b] != self.cons:
+            self.fn.run_all()                     # the reader waits for the copies out of that buffer
+            self._refill()
+        assert self.pos[b] == self.cons
+        return self.bufs[b], b
+
+    def release(self, slot, stream=None):
+        assert slot == self.cons % self.depth and self.pos[slot] == self.cons
+        if stream is not None:
+            ev = self.fn.Event()
+            ev.record(stream)
+            self.gate[slot] = (ev.handle, ev.gen)
+        self.cons += 1
+        self._refill()
+
+    def resync(self):
+        self.fn.run_all()
+        self.cons, self.resyncs = 0, self.resyncs + 1
+        self.pos, self.gate = [None] * self.depth, [None] * self.depth
+        self._refill()
+
+    def close(self):
+        pass
+
+
+@pytest.fixture
+def ring(fake, monkeypatch):
+    FakeRing.fn, FakeRing.made = fake, []
+    monkeypatch.setattr(sub("core.tiers.sources"), "DiskRing", FakeRing)
+    return FakeRing
+
+
+@pytest.mark.parametrize("fence", ["1", "0"])
+@pytest.mark.parametrize("ram_blocks,depth", [(3, 2), (1, 3), (4, 2)])
+def test_ssd_tier_chunks_come_out_of_the_ring(ring, monkeypatch, tmp_path, fence, ram_blocks, depth):
+    # 6 streamed blocks, some on the SSD tier (a cache file of their captured bytes): the calibration forward and
+    # the chunked ones copy their units out of the ring's buffers; every layer sees its own bytes, with or without
+    # the host fences, and the ring serves each SSD-tier block once per forward
+    monkeypatch.setenv("WEIGHTFERRY_CHUNK_HOST_FENCE", fence)
+    dn = sub("streaming.dit_node")
+    seen = []
+    model = Model(6, seen)
+    sm = dn.apply_streaming(model, device="cpu", pin_memory=False, chunk=True, chunk_bytes=512, chunk_slots=2,
+                            ram_blocks=ram_blocks, ring_depth=depth, ssd_dir=str(tmp_path))
+    st = sm.state
+    n_disk = 6 - ram_blocks
+    assert len(st.disk_index) == n_disk and all(st.host_flats[s] is None for s in st.disk_index)
+    r = ring.made[0]
+    for _ in range(4):
+        seen.clear()
+        sm(torch.zeros(1))
+        ring.fn.run_all()
+        _check(seen, _tags(6, "cadb"))
+        assert r.cons % n_disk == 0 and st._held is None
+    assert r.resyncs == 0 and r.cons == 4 * n_disk
+    # parameters of SSD-tier blocks go back to their own tensors between forwards
+    for s in st.disk_index:
+        assert all(p.data.data_ptr() == t.data_ptr() for p, t in zip(model.blocks[s].parameters(), st.rest[s]))
+    sm.teardown(device="cpu")
+
+
+def test_ssd_tier_chunks_with_skipped_block_and_outside_layer(ring, tmp_path):
+    # blocks 0, 2, 3 and 5 on the SSD tier: the forward skips block 3 (the ring reads it and hands it straight
+    # back) and calls a layer of block 0 before any block (read from the file, not through the ring)
+    dn = sub("streaming.dit_node")
+    seen = []
+    model = Model(6, seen, outside=True, skip=(3,))
+    sm = dn.apply_streaming(model, device="cpu", pin_memory=False, chunk=True, chunk_bytes=512, chunk_slots=2,
+                            ram_blocks=2, ssd_dir=str(tmp_path))
+    assert sorted(sm.state.disk_index) == [0, 2, 3, 5]
+    for _ in range(3):
+        seen.clear()
+        sm(torch.zeros(1))
+        ring.fn.run_all()
+        _check(seen, _tags(6, "cadb", skip=(3,), outside=True))
+    assert ring.made[0].resyncs == 0 and ring.made[0].cons == 3 * 4
+
+
+def test_ssd_tier_forward_stopped_part_way(ring, tmp_path):
+    # a forward that fails in block 3: the ring's cycle restarts, and the next forwards are right
+    dn = sub("streaming.dit_node")
+    seen = []
+    model = Model(6, seen)
+
+    def boom(mod, args):
+        if getattr(model, "fail", False):
+            raise RuntimeError("stop")
+    model.blocks[3].register_forward_pre_hook(boom)
+    sm = dn.apply_streaming(model, device="cpu", pin_memory=False, chunk=True, chunk_bytes=512, chunk_slots=2,
+                            ram_blocks=2, ssd_dir=str(tmp_path))
+    sm(torch.zeros(1))                            # calibration
+    model.fail = True
+    with pytest.raises(RuntimeError):
+        sm(torch.zeros(1))
+    model.fail = False
+    assert ring.made[0].resyncs == 1
+    for _ in range(2):
+        seen.clear()
+        sm(torch.zeros(1))
+        ring.fn.run_all()
+        _check(seen, _tags(6, "cadb"))
 
 
 class DeferredFake(FakeNative):
@@ -268,10 +401,17 @@ class WanLike(torch.nn.Module):
         return x
 
 
-@pytest.mark.parametrize("blocks,slots,chunk_kb", [(40, 4, 38), (12, 4, 38), (40, 2, 38), (40, 4, 17)])
-def test_host_far_ahead_of_the_gpu(monkeypatch, blocks, slots, chunk_kb):
-    # the whole forward is enqueued before anything runs; every layer must still read its own bytes
+@pytest.mark.parametrize("blocks,slots,chunk_kb,ram_blocks,fence", [
+    (40, 4, 38, None, "1"), (12, 4, 38, None, "1"), (40, 2, 38, None, "1"), (40, 4, 17, None, "1"),
+    (40, 4, 38, None, "0"), (12, 4, 38, 6, "0"), (12, 2, 17, 3, "0"), (40, 4, 38, 20, "0"), (12, 4, 38, 6, "1")])
+def test_host_far_ahead_of_the_gpu(monkeypatch, tmp_path, blocks, slots, chunk_kb, ram_blocks, fence):
+    # the whole forward is enqueued before anything runs (without the host fences: nothing runs until the forward's
+    # end); every layer must still read its own bytes -- with SSD-tier blocks too, whose ring buffers are refilled
+    # as soon as the copies queued out of them have run
+    monkeypatch.setenv("WEIGHTFERRY_CHUNK_HOST_FENCE", fence)
     fn = DeferredFake()
+    FakeRing.fn, FakeRing.made = fn, []
+    monkeypatch.setattr(sub("core.tiers.sources"), "DiskRing", FakeRing)
     state_mod = sub("streaming.state")
     chunk_mod = sub("streaming.chunk_state")
     monkeypatch.setattr(state_mod, "_native", fn)
@@ -293,7 +433,8 @@ def test_host_far_ahead_of_the_gpu(monkeypatch, blocks, slots, chunk_kb):
 
     model = M()
     sm = dn.apply_streaming(model, device="cpu", pin_memory=False, chunk=True, chunk_bytes=chunk_kb * 1024,
-                            chunk_slots=slots)
+                            chunk_slots=slots, ram_blocks=ram_blocks, ssd_dir=str(tmp_path))
+    assert len(sm.state.disk_index) == (0 if ram_blocks is None else blocks - ram_blocks)
     for f in range(5):
         seen.clear()
         sm(torch.zeros(1))

@@ -212,7 +212,8 @@ def test_cache_file_store_round_trip_and_stale_cleanup(tmp_path):
 def test_plan_tiers():
     GB = 1 << 30
     p = plan.plan_tiers(40, GB // 5, ram_budget_bytes=100 * GB)
-    assert p == {"ram_blocks": 40, "disk_blocks": 0, "ring_depth": 0, "budget": 100 * GB, "ssd_bound": False}
+    assert p == {"ram_blocks": 40, "disk_blocks": 0, "ring_depth": 0, "ring_threads": 1, "budget": 100 * GB,
+                 "ssd_bound": False, "disk_read_gbps": None, "disk_error": None}
     # 4 GB for 200 MB blocks: a ring of 4 (default) takes 0.8 GB, 16 blocks fit in the rest
     p = plan.plan_tiers(40, 200 << 20, ram_budget_bytes=4 * GB)
     assert p["ring_depth"] == 4 and p["ram_blocks"] == (4 * GB - 4 * (200 << 20)) // (200 << 20) == 16

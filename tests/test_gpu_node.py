@@ -3,7 +3,7 @@ DIFFUSION_MODEL wrapper, as ComfyUI calls them): every forward is bit-identical 
 (the reference's criterion, tests/test_streaming.py:222) -- after a load, twice; when ComfyUI skipped ON_LOAD (lazy
 capture in the wrapper); with Single Buffer; after a re-load; with tiering Auto putting blocks over the RAM
 budget on the SSD tier (read from the GGUF file); and in chunk mode (WEIGHTFERRY_CHUNK=1, block 0 streamed too, the
-learned call order reused by a re-load). A detach gives the weights back on the CPU."""
+learned call order reused by a re-load), with tiering Auto as well. A detach gives the weights back on the CPU."""
 import pytest
 import torch
 
@@ -102,6 +102,7 @@ def test_tiering_auto_reads_blocks_over_the_budget_from_the_file(native, comfy, 
     syn.write_gguf_model(model, path)
     per_block = sum(p.numel() * p.element_size() for p in model.blocks[1].parameters())
     monkeypatch.setenv("WEIGHTFERRY_MODEL_FILE", path)
+    monkeypatch.setenv("WEIGHTFERRY_DISK_PROBE_MB", "16")
     mp = node.WeightFerryDiT().apply_streaming(fake_comfy.FakeModelPatcher(model), resident_blocks=1,
                                                tiering="Auto (GPU / RAM / SSD)",
                                                ram_budget_gb=6.5 * per_block / 1024 ** 3)[0]
@@ -121,6 +122,7 @@ def test_tiering_auto_without_a_model_file_uses_a_cache_file(native, comfy, tmp_
     per_block = sum(p.numel() * p.element_size() for p in model.blocks[1].parameters())
     monkeypatch.delenv("WEIGHTFERRY_MODEL_FILE", raising=False)
     monkeypatch.setenv("WEIGHTFERRY_CACHE_DIR", str(tmp_path / "cache"))
+    monkeypatch.setenv("WEIGHTFERRY_DISK_PROBE_MB", "16")
     mp = node.WeightFerryDiT().apply_streaming(fake_comfy.FakeModelPatcher(model), resident_blocks=1,
                                                tiering="Auto (GPU / RAM / SSD)",
                                                ram_budget_gb=5.5 * per_block / 1024 ** 3)[0]
@@ -147,5 +149,30 @@ def test_chunk_mode_streams_block0_and_reuses_the_order(native, comfy, reference
     sm = getattr(model, node._NODE_ATTR)
     assert not sm.state.calibrating and sm.state.n_types >= 3
     _check(mp, x, ctx, ref, times=2)
+    mp.detach()
+    assert all(p.device.type == "cpu" for b in model.blocks for p in b.parameters())
+
+
+def test_chunk_mode_with_tiering_auto(native, comfy, tmp_path, monkeypatch):
+    # WEIGHTFERRY_CHUNK=1 and tiering Auto: the blocks over the budget go to the SSD tier (a cache file), whose
+    # chunks come out of the reader ring; the ring's readers follow the drive probe (kept in the cache folder)
+    x, ctx, ref = _reference10()
+    node = sub("streaming.node")
+    model = _stack(n=10)
+    per_block = sum(p.numel() * p.element_size() for p in model.blocks[1].parameters())
+    monkeypatch.delenv("WEIGHTFERRY_MODEL_FILE", raising=False)
+    monkeypatch.setenv("WEIGHTFERRY_CACHE_DIR", str(tmp_path / "cache"))
+    monkeypatch.setenv("WEIGHTFERRY_DISK_PROBE_MB", "16")
+    monkeypatch.setenv("WEIGHTFERRY_CHUNK", "1")
+    monkeypatch.setenv("WEIGHTFERRY_CHUNK_MB", "0.3")
+    mp = node.WeightFerryDiT().apply_streaming(fake_comfy.FakeModelPatcher(model), resident_blocks=1,
+                                               tiering="Auto (GPU / RAM / SSD)",
+                                               ram_budget_gb=6.5 * per_block / 1024 ** 3)[0]
+    mp.load()
+    sm = getattr(model, node._NODE_ATTR)
+    assert sm.state.chunk_mode and len(sm.state.disk_index) >= 4
+    import os
+    assert os.path.exists(str(tmp_path / "cache" / "weightferry_disk_probe.json"))
+    _check(mp, x, ctx, ref, times=3)
     mp.detach()
     assert all(p.device.type == "cpu" for b in model.blocks for p in b.parameters())

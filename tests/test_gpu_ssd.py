@@ -3,7 +3,8 @@ bytes into its GPU slot, and a streamed forward whose blocks partly come from a 
 bit-identical to the same stack resident on the GPU (the reference's criterion, tests/test_streaming.py:222,
 torch.equal) -- over several forwards (the ring's cycle runs on into the next forward), for several ring depths /
 reader counts / O_DIRECT settings and SSD layouts, and after a forward that stopped part way (the ring restarts its
-cycle)."""
+cycle); in chunk mode, whose SSD-tier chunks are copied out of the ring's buffers; and with the persistent cache
+entry a later load reads instead of writing."""
 import numpy as np
 import pytest
 import torch
@@ -159,3 +160,73 @@ def test_ssd_tier_from_a_cache_file(native, tmp_path):
         sm.teardown()
     import os
     assert not os.path.exists(path)
+
+
+@pytest.mark.parametrize("ram_blocks,source,slots", [(3, "file", 3), (1, "cache", 2), (0, "file", 4)])
+def test_chunk_streaming_with_ssd_tier_equals_resident(native, tmp_path, ram_blocks, source, slots):
+    # chunk mode: the SSD-tier blocks' chunks (and, in the calibration forward, their layers) are copied out of the
+    # ring's buffers; every forward is bit-identical to the stack resident on the GPU
+    dn = sub("streaming.dit_node")
+    syn = sub("streaming.synthetic")
+    x, ctx = _inputs()
+    with torch.no_grad():
+        ref = _stack().cuda()(x, ctx)
+    torch.cuda.synchronize()
+    model = _stack()
+    if source == "file":
+        path = str(tmp_path / "wan6.gguf")
+        syn.write_gguf_model(model, path)
+        streamed = _stack(seed=1)          # other weights in RAM: SSD-tier blocks must come from the file
+        for i in set(range(6)) - set(sub("core.tiers.plan").ssd_positions(6, 6 - ram_blocks)):
+            streamed.blocks[i].load_state_dict(model.blocks[i].state_dict())
+        kw = {"model_file": path}
+    else:
+        streamed, kw = model, {"ssd_dir": str(tmp_path / "cache")}
+    print(f"case chunk+ssd ram_blocks={ram_blocks} source={source} slots={slots}", flush=True)
+    sm = dn.apply_streaming(streamed, device="cuda", chunk=True, chunk_bytes=300_000, chunk_slots=slots,
+                            ram_blocks=ram_blocks, ring_depth=2, ring_threads=2, **kw)
+    try:
+        assert len(sm.state.disk_index) == 6 - ram_blocks and sm.state.calibrating
+        for f in range(4):
+            with torch.no_grad():
+                y = sm(x, ctx)
+            torch.cuda.synchronize()
+            assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), f
+        assert not sm.state.calibrating and sm.state.n_types >= 2
+    finally:
+        sm.teardown()
+
+
+def test_persistent_ssd_cache_reused_by_a_later_load(native, tmp_path, monkeypatch):
+    # WEIGHTFERRY_PERSIST_GB: the first load writes the SSD tier's cache entry and keeps it; a later load of the
+    # same weights reads it without writing, and both stream bit-identically to the resident stack
+    monkeypatch.setenv("WEIGHTFERRY_PERSIST_GB", "1")
+    dn = sub("streaming.dit_node")
+    cf = sub("core.tiers.cache_files")
+    import os
+    x, ctx = _inputs()
+    with torch.no_grad():
+        ref = _stack().cuda()(x, ctx)
+    torch.cuda.synchronize()
+    paths = []
+    for load in range(2):
+        sm = dn.apply_streaming(_stack(), device="cuda", ram_blocks=2, ssd_dir=str(tmp_path / "cache"),
+                                ring_depth=2, ring_threads=2)
+        try:
+            if load == 0:
+                assert sm.state.disk_store is not None and sm.state.disk_store.keep
+                paths.append(sm.state.disk_store.path)
+
+                def no_write(*a, **k):
+                    raise AssertionError("written again")
+                monkeypatch.setattr(cf.DiskBlockStore, "write_block", no_write)
+            else:
+                assert sm.state.disk_store is None and sm.state.ring is not None
+            for _ in range(2):
+                with torch.no_grad():
+                    y = sm(x, ctx)
+                torch.cuda.synchronize()
+                assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), load
+        finally:
+            sm.teardown()
+        assert os.path.exists(paths[0])
