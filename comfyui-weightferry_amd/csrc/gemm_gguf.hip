@@ -8,6 +8,8 @@
 // 16-wide step; result layout: lane l, register i -> row 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32. The tiling
 // and the pipeline are described at gemm_gguf_dl below.
 
+#include <algorithm>
+#include <cstdint>
 #include <mutex>
 #include <type_traits>
 #include <utility>
@@ -891,6 +893,158 @@ __global__ __launch_bounds__(64 * kSpWaves) void gemm_gguf_splitk(const uint16_t
     if (tid == 0) __hip_atomic_store(counters + tn, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ------------------------------------------------------------------- medium row counts (64 < M <= kPanelMaxRows)
+// Between the few-rows kernel (every workgroup reads its activation fragments from L2: too much traffic beyond 64
+// rows) and the tiled kernel (256 x 320 output tiles: 16-128 workgroups on 256 CUs below 2048 rows), a workgroup
+// takes a panel: 128 weight rows (4 waves, each two 16-row groups as in the few-rows kernel) against BM = 16 MT
+// activation rows, over a slice of KS super-blocks of K. The activations stream through a two-buffer LDS ring, one
+// super-block (BM rows x 512 bytes) per buffer, copied by the load unit straight into LDS (buffer_load ... lds) one
+// super-block ahead, 16-byte chunk c of row r at chunk c ^ (r & 15) (the 16 rows of a fragment read fall in 16
+// different bank groups). The weight's raw bytes of the next super-block load into the second of two register sets
+// meanwhile, and each lane dequantises into its B fragments as in the few-rows kernel; A fragments come from LDS.
+// K is split into S slices only as far as needed to give the chip 256 workgroups: with S > 1 each slice writes its
+// float32 partial sums (part[s][m][n]) and gguf_panel_sum adds them in slice order (deterministic), adds the bias
+// and rounds to bf16.
+constexpr int kPnWaves = 4;
+constexpr int kPnRows = 32 * kPnWaves;   // weight rows per workgroup
+
+template <int QT, int MID, bool BIAS, int MT, bool PART>
+__global__ __launch_bounds__(64 * kPnWaves) void gemm_gguf_panel(const uint16_t* __restrict__ X,
+                                                                 const uint8_t* __restrict__ W,
+                                                                 const uint16_t* __restrict__ bias,
+                                                                 uint16_t* __restrict__ Y, float* __restrict__ part,
+                                                                 int M, int N, int K, int NT, int MTI, int KS) {
+    constexpr int TS = GGUFTs<QT>::TS, NR = 2, BM = 16 * MT;
+    constexpr int RPW = BM / 2 / kPnWaves;             // 1 KiB DMA runs per wave per super-block
+    __shared__ __align__(1024) uint8_t xs0[BM * 512], xs1[BM * 512];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 15, kq = lane >> 4;
+    int b = blockIdx.x;
+    const int tn = b % NT;
+    b /= NT;
+    const int tm = b % MTI, s = b / MTI;
+    const int nsb = K / 256, sb0 = s * KS, nks = min(KS, nsb - sb0);
+    const int m0 = tm * BM, n0 = tn * kPnRows + wave * 32;
+    const int64_t row_bytes = (int64_t)nsb * TS;
+    const uint8_t* wrow[NR];
+#pragma unroll
+    for (int nr = 0; nr < NR; nr++) wrow[nr] = W + (int64_t)min(n0 + 16 * nr + r, N - 1) * row_bytes;
+    // rows past M read as zeros (the buffer's range ends at row M); their sums are never stored
+    const __amdgpu_buffer_rsrc_t rx = tile_rsrc(X + (int64_t)m0 * K, (int64_t)(M - m0) * K * 2);
+    uint32_t aoff[RPW];
+#pragma unroll
+    for (int q = 0; q < RPW; q++) {
+        const int p = 64 * (wave + kPnWaves * q) + lane;          // 16-byte LDS chunk this lane fills
+        const int row = p >> 5, c = (p & 31) ^ (row & 15);
+        aoff[q] = (uint32_t)row * (uint32_t)K * 2u + 16u * (uint32_t)c;
+    }
+    auto issue_a = [&](uint8_t* buf, int sb) {
+#pragma unroll
+        for (int q = 0; q < RPW; q++) lds_dma16(rx, buf + 1024 * (wave + kPnWaves * q), aoff[q] + (uint32_t)sb * 512u);
+    };
+    SkRaw<QT> w0[NR], w1[NR];
+    auto load_raw = [&](SkRaw<QT> (&wr)[NR], int sb) {
+#pragma unroll
+        for (int nr = 0; nr < NR; nr++) sk_load<QT>(wrow[nr] + (int64_t)sb * TS, kq, wr[nr]);
+    };
+    f32x4 acc[NR][MT];
+#pragma unroll
+    for (int nr = 0; nr < NR; nr++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[nr][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute = [&](const uint8_t* buf, const SkRaw<QT> (&wr)[NR]) {
+        static_for<8>([&](auto G) {
+            constexpr int g = decltype(G)::value;
+            bf16x8 bw[NR];
+#pragma unroll
+            for (int nr = 0; nr < NR; nr++) bw[nr] = sk_dequant<QT, MID, g>(wr[nr], kq);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const bf16x8 ax = *reinterpret_cast<const bf16x8*>(buf + (16 * mt + r) * 512 + 16 * ((4 * g + kq) ^ r));
+#pragma unroll
+                for (int nr = 0; nr < NR; nr++)
+                    acc[nr][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bw[nr], acc[nr][mt], 0, 0, 0);
+            }
+        });
+    };
+    // the ring: super-block i of the slice in buffer i % 2; at the top of each round every wave's copies of that
+    // super-block have landed (own loads: the counter; the others': the barrier), and every wave is past its reads of
+    // the other buffer, which then receives super-block i + 1
+    issue_a(xs0, sb0);
+    load_raw(w0, sb0);
+    for (int i = 0; i < nks; i += 2) {
+        wait_vm<0>();
+        wave_barrier_sync();
+        if (i + 1 < nks) {
+            issue_a(xs1, sb0 + i + 1);
+            load_raw(w1, sb0 + i + 1);
+        }
+        compute(xs0, w0);
+        if (i + 1 >= nks) break;
+        wait_vm<0>();
+        wave_barrier_sync();
+        if (i + 2 < nks) {
+            issue_a(xs0, sb0 + i + 2);
+            load_raw(w0, sb0 + i + 2);
+        }
+        compute(xs1, w1);
+    }
+    // lane (r, kq), register i: row m0 + 16 mt + 4 kq + i, column n0 + 16 nr + r
+#pragma unroll
+    for (int nr = 0; nr < NR; nr++) {
+        const int n = n0 + 16 * nr + r;
+        const float bn = !PART && BIAS && n < N ? __uint_as_float((uint32_t)bias[n] << 16) : 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = m0 + 16 * mt + 4 * kq + i;
+                if (m >= M || n >= N) continue;
+                if constexpr (PART) {
+                    part[((int64_t)s * M + m) * N + n] = acc[nr][mt][i];
+                } else {
+                    float t = acc[nr][mt][i];
+                    if (BIAS) t = t + bn;
+                    Y[(int64_t)m * N + n] = __builtin_bit_cast(uint16_t, (__bf16)t);
+                }
+            }
+    }
+}
+
+// y = bf16(part[0] + part[1] + ... + part[S - 1] (+ bias)), four consecutive outputs per thread
+template <bool BIAS>
+__global__ __launch_bounds__(256) void gguf_panel_sum(const float* __restrict__ part, const uint16_t* __restrict__ bias,
+                                                      uint16_t* __restrict__ Y, int64_t MN, int N, int S) {
+    const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i0 >= MN) return;
+    float t[4];
+    if ((N & 3) == 0) {                               // then MN % 4 == 0 and every slice starts 16-byte aligned
+        float4 v = *reinterpret_cast<const float4*>(part + i0);
+        t[0] = v.x; t[1] = v.y; t[2] = v.z; t[3] = v.w;
+        for (int q = 1; q < S; q++) {
+            v = *reinterpret_cast<const float4*>(part + (int64_t)q * MN + i0);
+            t[0] = t[0] + v.x; t[1] = t[1] + v.y; t[2] = t[2] + v.z; t[3] = t[3] + v.w;
+        }
+        const int n = (int)(i0 % N);
+        uint16_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float y = t[e];
+            if (BIAS) y = y + __uint_as_float((uint32_t)bias[n + e] << 16);
+            o[e] = __builtin_bit_cast(uint16_t, (__bf16)y);
+        }
+        *reinterpret_cast<uint2*>(Y + i0) = make_uint2(o[0] | ((uint32_t)o[1] << 16), o[2] | ((uint32_t)o[3] << 16));
+        return;
+    }
+    for (int e = 0; e < 4 && i0 + e < MN; e++) {
+        float y = part[i0 + e];
+        for (int q = 1; q < S; q++) y = y + part[(int64_t)q * MN + i0 + e];
+        if (BIAS) y = y + __uint_as_float((uint32_t)bias[(i0 + e) % N] << 16);
+        Y[i0 + e] = __builtin_bit_cast(uint16_t, (__bf16)y);
+    }
+}
+
 // Split-K plan of an [M, K] x [N, K] product: rows per fragment group MT, super-blocks per slice KS, slices S, column
 // tiles NT, and the workspace: a fixed block of kSplitCounters counters (the same place for every call, so calls of
 // any shape can share one workspace), then S * M * N float32 partial sums.
@@ -1056,12 +1210,85 @@ static int check_gguf(const char* who, const void* x_bf16, int64_t M, int64_t K,
     return WF_OK;
 }
 
+// Medium row counts: the panel kernel's plan. MT = 8 (128 activation rows per panel); slices S so that
+// NT x MTI x S >= 256 workgroups, at least two super-blocks each, and partial sums no larger than max_part bytes
+// (0: one slice, no workspace). Up to 512 rows it beats the tiled kernel (Wan block, Q4_K, one slice: 563 against
+// 856 us at 128 rows, 684 against 887 at 512); from 1024 rows the tiled kernel's 256 x 320 tiles, which dequantise
+// each weight value once per 256 rows instead of once per 128, are faster (909 against 1334 us).
+static constexpr int64_t kPanelMaxRows = 512;
+
+static bool panel_takes(int64_t M) { return M > 64 && M <= kPanelMaxRows; }
+
+struct PanelPlan {
+    int mt, mti, nt, ks, s;
+    int64_t part_bytes;
+};
+
+static PanelPlan panel_plan(int64_t M, int64_t N, int64_t K, int64_t max_part) {
+    PanelPlan p{};
+    p.mt = 8;
+    p.mti = (int)((M + 16 * p.mt - 1) / (16 * p.mt));
+    p.nt = (int)((N + kPnRows - 1) / kPnRows);
+    const int nsb = (int)(K / 256);
+    const int64_t tiles = (int64_t)p.nt * p.mti;
+    int s = (int)std::min<int64_t>((256 + tiles - 1) / tiles, std::max(1, nsb / 2));
+    while (s > 1 && (int64_t)s * M * N * 4 > max_part) s--;
+    p.ks = (nsb + s - 1) / s;
+    p.s = (nsb + p.ks - 1) / p.ks;
+    p.part_bytes = p.s > 1 ? (int64_t)p.s * M * N * 4 : 0;
+    return p;
+}
+
+template <int QT, int MID, int MT>
+static void launch_panel_mt(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N,
+                            int K, const PanelPlan& p, void* ws, hipStream_t st) {
+    const dim3 grid((unsigned)(p.nt * p.mti * p.s));
+    float* part = static_cast<float*>(ws);
+    if (p.s > 1) {
+        gemm_gguf_panel<QT, MID, false, MT, true><<<grid, 64 * kPnWaves, 0, st>>>(X, W, bias, Y, part, M, N, K, p.nt,
+                                                                                   p.mti, p.ks);
+        const int64_t MN = (int64_t)M * N;
+        const dim3 g2((unsigned)((MN + 1023) / 1024));
+        if (bias) gguf_panel_sum<true><<<g2, 256, 0, st>>>(part, bias, Y, MN, N, p.s);
+        else gguf_panel_sum<false><<<g2, 256, 0, st>>>(part, bias, Y, MN, N, p.s);
+    } else if (bias) {
+        gemm_gguf_panel<QT, MID, true, MT, false><<<grid, 64 * kPnWaves, 0, st>>>(X, W, bias, Y, part, M, N, K, p.nt,
+                                                                                   p.mti, p.ks);
+    } else {
+        gemm_gguf_panel<QT, MID, false, MT, false><<<grid, 64 * kPnWaves, 0, st>>>(X, W, bias, Y, part, M, N, K, p.nt,
+                                                                                    p.mti, p.ks);
+    }
+}
+
+template <int QT>
+static void launch_panel(int mid, const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M,
+                         int N, int K, const PanelPlan& p, void* ws, hipStream_t st) {
+    if (mid == WF_F16) launch_panel_mt<QT, WF_F16, 8>(X, W, bias, Y, M, N, K, p, ws, st);
+    else if (mid == WF_BF16) launch_panel_mt<QT, WF_BF16, 8>(X, W, bias, Y, M, N, K, p, ws, st);
+    else launch_panel_mt<QT, WF_F32, 8>(X, W, bias, Y, M, N, K, p, ws, st);
+}
+
+static void run_gguf_panel(int qtype, int mid_dt, const void* x_bf16, const void* wq, const void* bias_bf16,
+                           void* out_bf16, int M, int N, int K, const PanelPlan& p, void* ws, hipStream_t s) {
+    const uint16_t* X = static_cast<const uint16_t*>(x_bf16);
+    const uint8_t* W = static_cast<const uint8_t*>(wq);
+    const uint16_t* B = static_cast<const uint16_t*>(bias_bf16);
+    uint16_t* Y = static_cast<uint16_t*>(out_bf16);
+    if (qtype == 12) launch_panel<12>(mid_dt, X, W, B, Y, M, N, K, p, ws, s);
+    else if (qtype == 13) launch_panel<13>(mid_dt, X, W, B, Y, M, N, K, p, ws, s);
+    else launch_panel<14>(mid_dt, X, W, B, Y, M, N, K, p, ws, s);
+}
+
 static void run_gguf(int qtype, int mid_dt, const void* x_bf16, const void* wq, const void* bias_bf16, void* out_bf16,
                      int M, int N, int K, hipStream_t s) {
     const uint16_t* X = static_cast<const uint16_t*>(x_bf16);
     const uint8_t* W = static_cast<const uint8_t*>(wq);
     const uint16_t* B = static_cast<const uint16_t*>(bias_bf16);
     uint16_t* Y = static_cast<uint16_t*>(out_bf16);
+    if (panel_takes(M)) {                             // without a workspace: one slice
+        run_gguf_panel(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, M, N, K, panel_plan(M, N, K, 0), nullptr, s);
+        return;
+    }
     if (qtype == 12) launch_mid<12>(mid_dt, X, W, B, Y, M, N, K, s);
     else if (qtype == 13) launch_mid<13>(mid_dt, X, W, B, Y, M, N, K, s);
     else launch_mid<14>(mid_dt, X, W, B, Y, M, N, K, s);
@@ -1096,6 +1323,7 @@ extern "C" int wf_linear_gguf_workspace(int64_t M, int64_t N, int64_t K, int64_t
     *bytes = 0;
     if (M < 0 || N < 0 || K <= 0 || K % 256) { set_error("wf_linear_gguf_workspace: M, N, K"); return WF_EINVAL; }
     if (split_takes(M, N, K)) *bytes = split_plan(M, N, K).bytes();
+    else if (panel_takes(M)) *bytes = panel_plan(M, N, K, INT64_MAX).part_bytes;
     return WF_OK;
 }
 
@@ -1106,7 +1334,15 @@ extern "C" int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const
     const int rc = check_gguf("wf_linear_gguf_ws", x_bf16, M, K, wq, wq_bytes, qtype, N, bias_bf16, out_bf16, mid_dt);
     if (rc != WF_OK || M == 0 || N == 0) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (!split_takes(M, N, K)) {
+    if (!split_takes(M, N, K) && panel_takes(M)) {
+        const PanelPlan p = panel_plan(M, N, K, INT64_MAX);
+        if (p.part_bytes > 0 && (!workspace || !aligned(workspace, 256) || workspace_bytes < p.part_bytes)) {
+            set_error("wf_linear_gguf_ws: a 256-byte aligned workspace of %lld bytes is needed (given %lld)",
+                      (long long)p.part_bytes, (long long)workspace_bytes);
+            return WF_EINVAL;
+        }
+        run_gguf_panel(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, p, workspace, s);
+    } else if (!split_takes(M, N, K)) {
         run_gguf(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, s);
     } else {
         const SplitPlan p = split_plan(M, N, K);
@@ -1170,7 +1406,16 @@ extern "C" int wf_linear_gguf_noalloc(const void* x_bf16, int64_t M, int64_t K, 
                               mid_dt);
     if (rc != WF_OK || M == 0 || N == 0) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (!split_takes(M, N, K)) {
+    if (!split_takes(M, N, K) && panel_takes(M)) {
+        // the panel form's partial sums in the scratch array, as many slices as fit there
+        const PanelPlan p = panel_plan(M, N, K, kScratchBytes);
+        void* ws = nullptr;
+        if (p.part_bytes > 0) {
+            const int src = scratch_address(&ws);
+            if (src != WF_OK) return src;
+        }
+        run_gguf_panel(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, p, ws, s);
+    } else if (!split_takes(M, N, K)) {
         run_gguf(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, s);
     } else {
         const SplitPlan p = split_plan(M, N, K);

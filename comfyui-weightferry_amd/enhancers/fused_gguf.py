@@ -66,20 +66,27 @@ def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
     return y.reshape(*x.shape[:-1], n_out)
 
 
-# Rows of activations up to which the fused kernel (its few-rows form: the weight streamed through the chip once)
-# beats the two-step flow, and from which its tiled form does for Q4_K / Q5_K weights no wider than they are deep.
-# Measured on MI355X (Wan-14B shapes 5120 x 5120, 13824 x 5120, 5120 x 13824): at 32 rows 24-61 us fused against
-# 39-67 us two-step; from 128 to 4096 rows the two-step flow (one dequantisation, then hipBLASLt) is faster; at 8192
-# rows the fused kernel takes 5120 x 5120 and 5120 x 13824 (Q4_K / Q5_K) 5-20 % faster, 13824 x 5120 and Q6_K not.
+# Where the fused kernel beats the two-step flow (one dequantisation, then hipBLASLt), measured on MI355X over the
+# Wan-14B shapes (5120 x 5120, 13824 x 5120, 5120 x 13824), µs per block of six layers:
+#   * up to 64 rows, its few-rows form (the weight streamed through the chip once): 32 rows 124-134 µs against
+#     269-334 two-step (Q4_K);
+#   * 65-256 rows, its panel form (128 x 128 panels, K in slices): Q4_K 273 against 370 µs at 128 rows, 426 against
+#     507 at 256; Q6_K only up to 128 rows (352 against 366; 583 against 511 at 256);
+#   * from 512 to 4096 rows the two-step flow is faster (Q4_K at 512 rows: 742 against 493; at 4096: 1.94 against
+#     1.76 ms);
+#   * from 8192 rows the tiled form takes 5120 x 5120 and 5120 x 13824 (Q4_K / Q5_K) 5-20 % faster, 13824 x 5120
+#     and Q6_K not.
 FEW_ROWS = 64
+PANEL_ROWS = {12: 256, 13: 256, 14: 128}
 MANY_ROWS = 8192
 
 
 def prefer_fused(rows, qtype, n_out, k):
     """mode "auto": True when the fused kernel is the faster way to compute this layer on MI355X."""
-    if rows <= FEW_ROWS:
+    q = int(qtype)
+    if rows <= FEW_ROWS or rows <= PANEL_ROWS.get(q, 0):
         return True
-    return rows >= MANY_ROWS and int(qtype) in (12, 13) and n_out <= k
+    return rows >= MANY_ROWS and q in (12, 13) and n_out <= k
 
 
 def linear(x, data, qtype, oshape, bias=None, mid_dtype=None, mode="auto"):

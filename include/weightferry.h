@@ -98,8 +98,8 @@ int wf_linear_i8_residual(const int8_t* xq, const int8_t* wq, const float* xs, c
  * the kernel exactly as wf_dequant does with dequant dtype mid_dt and output bf16; float32 accumulation. No
  * reference function does this in one step: it replaces `dequantize` (enhancers/gguf_dequant.py:296-326) followed
  * by ComfyUI-GGUF's torch.nn.functional.linear on the bf16 weight. x: bf16 [M, K], 16-byte aligned; bias: bf16 [N]
- * or NULL; out: bf16 [M, N]. K % 256 == 0. M <= 64 runs the few-rows form (the weight streamed once), larger M the
- * tiled form. */
+ * or NULL; out: bf16 [M, N]. K % 256 == 0. M <= 64 runs the few-rows form (the weight streamed once), 65-512 rows
+ * the panel form (128 x 128 panels over all of K), larger M the tiled form (256 x 320 tiles). */
 int wf_linear_gguf(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes, int qtype, int64_t N,
                    const void* bias_bf16, void* out_bf16, int mid_dt, void* stream);
 
@@ -109,8 +109,11 @@ int wf_linear_gguf(const void* x_bf16, int64_t M, int64_t K, const void* wq, int
  * last workgroup of each column tile adds them in a fixed order (the result is the same on every run). Workspace:
  * 256-byte aligned, at least the bytes wf_linear_gguf_workspace gives; its first 16 KiB are counters that must be
  * zero on entry and are zero again when the call has run, whatever its shape (a workspace cleared once can be reused
- * by later calls of any shape on the same stream; calls that overlap on one workspace race). Any other shape does
- * not use the workspace (wf_linear_gguf_workspace gives 0; workspace may be NULL) and is wf_linear_gguf. */
+ * by later calls of any shape on the same stream; calls that overlap on one workspace race). With 65-512 rows
+ * (at least four super-blocks of K) the panel form splits K into slices, enough to give the chip 256 workgroups:
+ * each slice writes float32 partial sums into the workspace (S * M * N * 4 bytes, no counters) and a second kernel
+ * adds them in slice order. Any other shape does not use the workspace (wf_linear_gguf_workspace gives 0; workspace
+ * may be NULL) and is wf_linear_gguf. */
 int wf_linear_gguf_workspace(int64_t M, int64_t N, int64_t K, int64_t* bytes);
 int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes, int qtype, int64_t N,
                       const void* bias_bf16, void* out_bf16, int mid_dt, void* workspace, int64_t workspace_bytes,
@@ -120,8 +123,9 @@ int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const void* wq, 
  * callers that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc). The split form's counters and partial sums live in a 16 MiB array the library holds on each GPU
  * it runs on until the process ends; the counters are cleared by a small kernel on `stream` at the start of each call
- * (no memset). A shape that needs more than 16 MiB there returns WF_EUNSUPPORTED with a message. Every call on a GPU
- * shares that GPU's array: calls that overlap on one GPU (on different streams or threads) race. */
+ * (no memset). A shape that needs more than 16 MiB there returns WF_EUNSUPPORTED with a message. The panel form
+ * (65-512 rows) takes as many K slices as fit the array (one, and no scratch, at worst). Every call on a GPU shares
+ * that GPU's array: calls that overlap on one GPU (on different streams or threads) race. */
 int wf_linear_gguf_noalloc(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes, int qtype,
                            int64_t N, const void* bias_bf16, void* out_bf16, int mid_dt, void* stream);
 

@@ -12,8 +12,12 @@ def test_prefer_fused_rule():
     for rows in (1, 16, 32, 64):
         assert fg.prefer_fused(rows, 12, 5120, 5120)
         assert fg.prefer_fused(rows, 14, 13824, 5120)
-    # between the two thresholds the two-step flow is faster for every format and shape
-    for rows in (65, 512, 4096, 8191):
+    # medium rows: the panel form up to 256 rows for Q4_K / Q5_K, up to 128 for Q6_K
+    for rows in (65, 128, 256):
+        assert fg.prefer_fused(rows, 12, 5120, 5120) and fg.prefer_fused(rows, 13, 13824, 5120)
+    assert fg.prefer_fused(128, 14, 5120, 5120) and not fg.prefer_fused(129, 14, 5120, 5120)
+    # between those and the many-rows threshold the two-step flow is faster for every format and shape
+    for rows in (257, 512, 4096, 8191):
         for q in (12, 13, 14):
             assert not fg.prefer_fused(rows, q, 5120, 5120)
     # many rows: Q4_K / Q5_K weights no wider than deep take the fused kernel, the rest the two-step flow

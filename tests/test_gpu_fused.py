@@ -48,7 +48,7 @@ def check(y, x, w, rows=None, bias=None):
 
 @pytest.mark.parametrize("qtype", [12, 13, 14])
 @pytest.mark.parametrize("mid", [0, 2])
-@pytest.mark.parametrize("M,N,K", [(77, 300, 512), (256, 256, 256), (512, 768, 5120)])
+@pytest.mark.parametrize("M,N,K", [(77, 300, 512), (256, 256, 256), (512, 768, 5120), (2100, 300, 512)])
 def test_fused_against_dequant_then_gemm(native, qtype, mid, M, N, K):
     raw = encode.random_blocks(qtype, N * K // 256, seed=qtype + M, family="normal")
     g = torch.Generator().manual_seed(M + N)
@@ -102,7 +102,7 @@ def test_wan_block_shapes_sampled_rows(native, qtype, N, K):
                                              (48, 777, 1280, True), (65, 256, 768, False)])
 def test_few_rows_whole_output(native, qtype, mid, M, N, K, with_bias):
     # up to 64 activation rows take the few-rows kernel (16 weight rows per workgroup, K split over its 8 waves,
-    # 1 to 4 row tiles of 16; K = 256 and 512 leave waves with no super-block); 65 rows the tiled kernel: ragged M
+    # 1 to 4 row tiles of 16; K = 256 and 512 leave waves with no super-block); 65 rows the panel kernel: ragged M
     # and N, every output element checked
     raw = encode.random_blocks(qtype, N * K // 256, seed=qtype * 7 + M, family="normal")
     g = torch.Generator().manual_seed(M * 31 + N)
@@ -191,3 +191,61 @@ def test_split_k_rejects_a_short_workspace(native):
                                           ws.data_ptr(), need.value - 1, st) == native.EINVAL
     assert native.lib().wf_linear_gguf_ws(x.data_ptr(), M, K, w.data_ptr(), w.numel(), 12, N, None, y.data_ptr(), 0,
                                           None, 0, st) == native.EINVAL
+
+
+def noalloc(native, x, raw_dev, qtype, N, bias=None, mid=0):
+    M, K = x.shape
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    rc = native.lib().wf_linear_gguf_noalloc(x.data_ptr(), M, K, raw_dev.data_ptr(), raw_dev.numel(), qtype, N,
+                                             bias.data_ptr() if bias is not None else None, y.data_ptr(), mid,
+                                             native.stream_of(x.device))
+    assert rc == 0, native.last_error()
+    torch.cuda.synchronize()
+    return y
+
+
+@pytest.mark.parametrize("qtype", [12, 13, 14])
+@pytest.mark.parametrize("M,N,K,with_bias,mid", [(65, 300, 512, True, 0), (128, 256, 2048, False, 2),
+                                                 (129, 1002, 1024, True, 0), (300, 520, 5120, False, 0),
+                                                 (512, 130, 768, True, 2), (257, 384, 1024, False, 0)])
+def test_panel_whole_output(native, qtype, M, N, K, with_bias, mid):
+    # 65 to 512 activation rows take the panel form (128 weight rows x 128 activation rows per workgroup): through
+    # wf_linear_gguf in one K slice; through wf_linear_gguf_ws in as many slices as give 256 workgroups (two
+    # super-blocks at least), their float32 partial sums added in slice order by a second kernel; allocation-free
+    # with the slices its scratch holds. Ragged M and N (N % 4 != 0 takes the reduction's element path), every output
+    # element checked; the three agree bit for bit where they run the same slices
+    raw = encode.random_blocks(qtype, N * K // 256, seed=qtype * 3 + M, family="normal")
+    g = torch.Generator().manual_seed(M * 7 + N)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16) if with_bias else None
+    xd, rd, bd = x.cuda(), torch.from_numpy(raw).cuda(), bias.cuda() if with_bias else None
+    print(f"case panel qtype={qtype} mid={mid} M={M} N={N} K={K}", flush=True)
+    w = weight_bf16(raw, qtype, mid, N, K)
+    y1 = fused(native, xd, rd, qtype, N, bias=bd, mid=mid)
+    check(y1, x, w, bias=bias)
+    y2, _, need = fused_ws(native, xd, rd, qtype, N, bias=bd, mid=mid)
+    check(y2, x, w, bias=bias)
+    nsb = K // 256
+    assert (need > 0) == (nsb >= 4)                  # two super-blocks per slice at least
+    if need:
+        assert need % (M * N * 4) == 0 and need // (M * N * 4) >= 2
+    else:
+        assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    y3 = noalloc(native, xd, rd, qtype, N, bias=bd, mid=mid)
+    if need <= 16 << 20:
+        assert torch.equal(y3.view(torch.int16), y2.view(torch.int16))
+    check(y3, x, w, bias=bias)
+
+
+def test_panel_workspace_is_checked(native):
+    import ctypes
+    M, N, K = 128, 256, 2048
+    need = ctypes.c_int64()
+    assert native.lib().wf_linear_gguf_workspace(M, N, K, ctypes.byref(need)) == 0 and need.value > 0
+    x = torch.zeros((M, K), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(N * K // 256 * 144, dtype=torch.uint8, device="cuda")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    ws = torch.zeros(need.value, dtype=torch.uint8, device="cuda")
+    st = native.stream_of(x.device)
+    assert native.lib().wf_linear_gguf_ws(x.data_ptr(), M, K, w.data_ptr(), w.numel(), 12, N, None, y.data_ptr(), 0,
+                                          ws.data_ptr(), need.value - 1, st) == native.EINVAL
