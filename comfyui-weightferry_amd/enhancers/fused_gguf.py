@@ -72,21 +72,16 @@ def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
 #     269-334 two-step (Q4_K);
 #   * 65-256 rows, its panel form (128 x 128 panels, K in slices): Q4_K 273 against 370 µs at 128 rows, 426 against
 #     507 at 256; Q6_K only up to 128 rows (352 against 366; 583 against 511 at 256);
-#   * from 512 to 4096 rows the two-step flow is faster (Q4_K at 512 rows: 742 against 493; at 4096: 1.94 against
-#     1.76 ms);
-#   * from 8192 rows the tiled form takes 5120 x 5120 and 5120 x 13824 (Q4_K / Q5_K) 5-20 % faster, 13824 x 5120
-#     and Q6_K not.
+#   * from 512 rows on the two-step flow is faster: Q4_K 742 against 493 µs at 512 rows, 2.23 against 1.89 ms at
+#     4096, 4.29 against 4.06 ms at 8192 (the tiled form wins only 5120 x 5120 there, by 5 %; Q5_K and Q6_K none).
+# mode "fused" still takes the tiled form at any row count.
 FEW_ROWS = 64
 PANEL_ROWS = {12: 256, 13: 256, 14: 128}
-MANY_ROWS = 8192
 
 
 def prefer_fused(rows, qtype, n_out, k):
     """mode "auto": True when the fused kernel is the faster way to compute this layer on MI355X."""
-    q = int(qtype)
-    if rows <= FEW_ROWS or rows <= PANEL_ROWS.get(q, 0):
-        return True
-    return rows >= MANY_ROWS and q in (12, 13) and n_out <= k
+    return rows <= FEW_ROWS or rows <= PANEL_ROWS.get(int(qtype), 0)
 
 
 def linear(x, data, qtype, oshape, bias=None, mid_dtype=None, mode="auto"):

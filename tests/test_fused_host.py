@@ -16,14 +16,10 @@ def test_prefer_fused_rule():
     for rows in (65, 128, 256):
         assert fg.prefer_fused(rows, 12, 5120, 5120) and fg.prefer_fused(rows, 13, 13824, 5120)
     assert fg.prefer_fused(128, 14, 5120, 5120) and not fg.prefer_fused(129, 14, 5120, 5120)
-    # between those and the many-rows threshold the two-step flow is faster for every format and shape
-    for rows in (257, 512, 4096, 8191):
+    # from there on the two-step flow is faster for every format and shape
+    for rows in (257, 512, 4096, 8192, 32768):
         for q in (12, 13, 14):
-            assert not fg.prefer_fused(rows, q, 5120, 5120)
-    # many rows: Q4_K / Q5_K weights no wider than deep take the fused kernel, the rest the two-step flow
-    assert fg.prefer_fused(8192, 12, 5120, 5120) and fg.prefer_fused(32768, 13, 5120, 13824)
-    assert not fg.prefer_fused(8192, 12, 13824, 5120)
-    assert not fg.prefer_fused(8192, 14, 5120, 5120)
+            assert not fg.prefer_fused(rows, q, 5120, 5120) and not fg.prefer_fused(rows, q, 5120, 13824)
 
 
 def test_auto_routes_by_rows(monkeypatch):
