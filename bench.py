@@ -60,8 +60,25 @@ def _args():
     return a
 
 
+WARM_S = 0.05
+
+
+def _warm_clock(torch, fn, seconds=WARM_S):
+    """Call fn() until `seconds` have passed (at least once). MI355X raises its clock over tens of milliseconds of
+    load after an idle spell (host-side set-up between measurements): the first ~10 calls of a 0.5 ms kernel ran
+    10 % slower than later ones, so whichever variant was timed first looked slower."""
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= seconds:
+            return
+
+
 def _timed(torch, fn, n, warm):
-    """Mean ms of fn() over n back-to-back calls on torch's current stream (events at both ends)."""
+    """Mean ms of fn() over n back-to-back calls on torch's current stream (events at both ends), after `warm`
+    calls and at least WARM_S seconds of calls."""
+    _warm_clock(torch, fn)
     for _ in range(warm):
         fn()
     torch.cuda.synchronize()
@@ -103,6 +120,25 @@ def int8_leg(torch, native):
                                       "frac_of_5000": round(tops / 5000, 3)}
             del wq, y
         del x, xq
+    # the same 16384 x 5120 x 5120 product on all-ones operands (the fewest toggling bits: the chip keeps a higher
+    # clock under its power budget) and hipBLASLt's int8 GEMM (torch._int_mm, int32 out, no epilogue) on random
+    # operands: the first is the kernel's rate without the power cap's clock reduction, the second the library's
+    # rate under the same cap
+    M, N = 16384, 5120
+    xq = torch.ones((M, K), dtype=torch.int8, device=dev)
+    wq = torch.ones((N, K), dtype=torch.int8, device=dev)
+    xs = torch.ones(M, dtype=torch.float32, device=dev)
+    ws = torch.full((N,), 1.0 / K, dtype=torch.float32, device=dev)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    ms = _timed(torch, lambda: lib.wf_linear_i8(xq.data_ptr(), wq.data_ptr(), xs.data_ptr(), ws.data_ptr(), None,
+                                                y.data_ptr(), 1, M, N, K, st), 10, 2)
+    out["gemm_M16384_N5120_ones"] = {"us": round(ms * 1e3, 1), "TOPS": round(2 * M * N * K / ms / 1e9, 1)}
+    xq = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev, generator=g)
+    wq = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+    wt = wq.t()
+    ms = _timed(torch, lambda: torch._int_mm(xq, wt), 10, 2)
+    out["hipblaslt_int_mm_M16384_N5120"] = {"us": round(ms * 1e3, 1), "TOPS": round(2 * M * N * K / ms / 1e9, 1)}
+    del xq, wq, wt, xs, ws, y
     torch.cuda.empty_cache()
     return out
 
@@ -145,13 +181,14 @@ def fused_leg(torch, native):
                      "fused_frac_of_2500": round(flops / tf / 1e9 / 2500, 3),
                      "two_step_ms": round(tu, 3), "two_step_TFLOPS": round(flops / tu / 1e9, 1),
                      "flop": flops, "weight_bytes": wbytes}
-    # few activation rows (32 tokens, and one token): the fused kernel's few-rows form streams each weight once;
-    # bound by HBM. "cold": every call reads another copy of the weight, the copies of a layer spanning > 600 MB, so
-    # MI355X's 256 MB last-level cache cannot serve a call from the one before (a weight in a real forward was last
-    # read a step earlier); "warm": the same weight every call. One token goes through fused_gguf.fused_linear, the
-    # drop-in's choice of form (the split form for the deep ffn_down, the few-rows form otherwise).
+    # few activation rows (128 and 32 tokens, and one token): the fused kernel's few-rows form streams each weight
+    # once, its panel form (65-512 rows) once per 128 rows. "cold": every call reads another copy of the weight, the
+    # copies of a layer spanning > 600 MB, so MI355X's 256 MB last-level cache cannot serve a call from the one
+    # before (a weight in a real forward was last read a step earlier); "warm": the same weight every call. One and
+    # 128 tokens go through fused_gguf.fused_linear, the drop-in's choice of form with its workspace (the panel form
+    # in K slices at 128 rows; few-rows at one row).
     fg = importlib.import_module(PKG + ".enhancers.fused_gguf")
-    for rows in (32, 1):
+    for rows in (128, 32, 1):
         for qt, name in ((12, "q4_k"), (13, "q5_k"), (14, "q6_k")):
             tf = tc = tu = 0.0
             wbytes = 0
@@ -165,7 +202,7 @@ def fused_leg(torch, native):
                 turn = [0]
 
                 def fused(r=raw):
-                    if rows == 1:
+                    if rows == 1 or rows > 64:
                         fg.fused_linear(x, r, qt, (N, K))
                     else:
                         lib.wf_linear_gguf(x.data_ptr(), rows, K, r.data_ptr(), r.numel(), qt, N, None, y.data_ptr(),
@@ -400,6 +437,13 @@ def dequant_leg(torch, native, raws, shapes, qtype, mid, out_dt, steps, warmup):
         if rc != 0:
             raise RuntimeError(native.last_error())
 
+    turn = [0]
+
+    def one_step():
+        turn[0] += 1
+        for m in range(len(shapes)):
+            launch(turn[0] % rot, m)
+    _warm_clock(torch, one_step)
     for i in range(warmup):
         for m in range(len(shapes)):
             launch(i % rot, m)

@@ -396,12 +396,6 @@ __global__ __launch_bounds__(512) void gemm_gguf_dl(const uint16_t* __restrict__
     // step, before this step's activation loads, so waiting for all but those activation loads lands them; once
     // dequantised, the registers take what changes for stage s + 4 (one set of raw registers, each load a whole
     // step ahead of its use).
-    // The dequantisation (VALU) runs between the MFMAs of the step's second K half: with the two phases one after
-    // the other, both waves of a SIMD were in the same phase at once (the barrier lines them up), so the matrix
-    // core sat idle through the dequantisation (MFMA busy 53 %); interleaved, one MFMA then up to 12 VALU
-    // instructions, the wave issues dequantisation while its MFMAs execute: 12-15 % less time per Wan block at
-    // 4096 rows. That half's weight fragments are read from LDS just before their MFMAs (two registers live
-    // instead of ten), which keeps the interleaved loop within 256 registers.
     auto step = [&](int kt, auto J, uint4* xc, uint4* wc, uint4* xn, uint4* wn_, uint4* xf, uint4* wf) {
         constexpr int j = decltype(J)::value;
         const int s = kt + j;
@@ -409,25 +403,14 @@ __global__ __launch_bounds__(512) void gemm_gguf_dl(const uint16_t* __restrict__
         using G4 = std::integral_constant<int, (j + 4) & 7>;
         wave_barrier_sync();
         issue_x(xf, s + 3);
-#pragma unroll
-        for (int i = 0; i < WM; i++) fa[1][i] = __builtin_bit_cast(bf16x8, xc[abase[1] + 128 * i]);
+        fread(xc, wc, 1, 1);
         mfmas(0);
+        mfmas(1);
         __builtin_amdgcn_sched_barrier(0);
         wait_vm<IX>();                                 // all but this step's activation loads have landed
         __builtin_amdgcn_sched_barrier(0);             // nothing that reads the raw bytes moves above the wait
-#pragma unroll
-        for (int jn = 0; jn < WN; jn++) {
-            const bf16x8 b = __builtin_bit_cast(bf16x8, wc[bbase[1] + 128 * jn]);
-#pragma unroll
-            for (int i = 0; i < WM; i++)
-                acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[1][i], b, acc[i][jn], 0, 0, 0);
-        }
         wstore(G3{}, wf, w1, s + 3);
         if constexpr (two) wstore2(G3{}, wf, w2, s + 3);
-        static_for<WM * WN>([&](auto) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // one MFMA,
-            __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);   // then up to 12 VALU instructions
-        });
         __builtin_amdgcn_sched_barrier(0);             // the next loads reuse the raw registers
         wload(G4{}, w1, s + 4);
         if constexpr (two) wload2(G4{}, w2, s + 4);
