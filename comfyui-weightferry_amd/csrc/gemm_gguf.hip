@@ -263,16 +263,6 @@ __device__ __forceinline__ void q_dequant_q(const QRawQ<QT>& w, uint32_t sh, uin
     }
 }
 
-// f(std::integral_constant<int, 0>{}), ..., f(std::integral_constant<int, N - 1>{}), unrolled at compile time
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_seq(F&& f, std::integer_sequence<int, I...>) {
-    (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    static_for_seq(f, std::make_integer_sequence<int, N>{});
-}
-
 template <int QT, int MID, bool BIAS, int VM, int VN, int WM, int WN>
 __global__ __launch_bounds__(512) void gemm_gguf_dl(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
                                                     const uint16_t* __restrict__ bias, uint16_t* __restrict__ Y,

@@ -1,7 +1,10 @@
 // Helpers of the GEMM kernels that stream operands global -> LDS with the load unit (buffer_load ... lds) through a
-// ring of LDS stages: buffer resources with zero fill past the end, the 16-byte LDS DMA, the 4-chunk row swizzle and
-// a barrier without the workgroup fence.
+// ring of LDS stages: buffer resources with zero fill past the end, the 16-byte LDS DMA, the 4-chunk row swizzle, a
+// barrier without the workgroup fence, and a compile-time loop.
 #pragma once
+
+#include <type_traits>
+#include <utility>
 
 #include "wf_common.h"
 
@@ -58,6 +61,16 @@ template <int N>
 __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// f(std::integral_constant<int, 0>{}), ..., f(std::integral_constant<int, N - 1>{}), unrolled at compile time
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_seq(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_seq(f, std::make_integer_sequence<int, N>{});
 }
 
 }  // namespace wf
