@@ -871,10 +871,11 @@ __global__ __launch_bounds__(64 * kSpWaves) void gemm_gguf_splitk(const uint16_t
 // rows) and the tiled kernel (256 x 320 output tiles: 16-128 workgroups on 256 CUs below 2048 rows), a workgroup
 // takes a panel: 128 weight rows (4 waves, each two 16-row groups as in the few-rows kernel) against BM = 16 MT
 // activation rows, over a slice of KS super-blocks of K. The activations stream through a two-buffer LDS ring, one
-// super-block (BM rows x 512 bytes) per buffer, copied by the load unit straight into LDS (buffer_load ... lds) one
-// super-block ahead, 16-byte chunk c of row r at chunk c ^ (r & 15) (the 16 rows of a fragment read fall in 16
-// different bank groups). The weight's raw bytes of the next super-block load into the second of two register sets
-// meanwhile, and each lane dequantises into its B fragments as in the few-rows kernel; A fragments come from LDS.
+// half super-block (BM rows x 256 bytes) per buffer -- 64 KiB at 128 rows, so two workgroups share a CU --, copied
+// by the load unit straight into LDS (buffer_load ... lds) one half ahead, 16-byte chunk c of row r at chunk
+// c ^ (r & 15) (the 16 rows of a fragment read fall in 16 different bank groups). The weight's raw bytes of the next
+// super-block load into the second of two register sets meanwhile, and each lane dequantises into its B fragments
+// as in the few-rows kernel; A fragments come from LDS.
 // K is split into S slices only as far as needed to give the chip 256 workgroups: with S > 1 each slice writes its
 // float32 partial sums (part[s][m][n]) and gguf_panel_sum adds them in slice order (deterministic), adds the bias
 // and rounds to bf16.
@@ -882,14 +883,14 @@ constexpr int kPnWaves = 4;
 constexpr int kPnRows = 32 * kPnWaves;   // weight rows per workgroup
 
 template <int QT, int MID, bool BIAS, int MT, bool PART>
-__global__ __launch_bounds__(64 * kPnWaves) void gemm_gguf_panel(const uint16_t* __restrict__ X,
+__global__ __launch_bounds__(64 * kPnWaves) __attribute__((amdgpu_waves_per_eu(2))) void gemm_gguf_panel(const uint16_t* __restrict__ X,
                                                                  const uint8_t* __restrict__ W,
                                                                  const uint16_t* __restrict__ bias,
                                                                  uint16_t* __restrict__ Y, float* __restrict__ part,
                                                                  int M, int N, int K, int NT, int MTI, int KS) {
     constexpr int TS = GGUFTs<QT>::TS, NR = 2, BM = 16 * MT;
-    constexpr int RPW = BM / 2 / kPnWaves;             // 1 KiB DMA runs per wave per super-block
-    __shared__ __align__(1024) uint8_t xs0[BM * 512], xs1[BM * 512];
+    constexpr int RPW = BM / 4 / kPnWaves;             // 1 KiB DMA runs per wave per half super-block
+    __shared__ __align__(1024) uint8_t xs0[BM * 256], xs1[BM * 256];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 15, kq = lane >> 4;
@@ -909,12 +910,14 @@ __global__ __launch_bounds__(64 * kPnWaves) void gemm_gguf_panel(const uint16_t*
 #pragma unroll
     for (int q = 0; q < RPW; q++) {
         const int p = 64 * (wave + kPnWaves * q) + lane;          // 16-byte LDS chunk this lane fills
-        const int row = p >> 5, c = (p & 31) ^ (row & 15);
+        const int row = p >> 4, c = (p & 15) ^ (row & 15);
         aoff[q] = (uint32_t)row * (uint32_t)K * 2u + 16u * (uint32_t)c;
     }
-    auto issue_a = [&](uint8_t* buf, int sb) {
+    // half h of super-block sb: activations [256 sb + 128 h, + 128) of each row
+    auto issue_a = [&](uint8_t* buf, int sb, int h) {
 #pragma unroll
-        for (int q = 0; q < RPW; q++) lds_dma16(rx, buf + 1024 * (wave + kPnWaves * q), aoff[q] + (uint32_t)sb * 512u);
+        for (int q = 0; q < RPW; q++)
+            lds_dma16(rx, buf + 1024 * (wave + kPnWaves * q), aoff[q] + (uint32_t)sb * 512u + (uint32_t)h * 256u);
     };
     SkRaw<QT> w0[NR], w1[NR];
     auto load_raw = [&](SkRaw<QT> (&wr)[NR], int sb) {
@@ -926,42 +929,49 @@ __global__ __launch_bounds__(64 * kPnWaves) void gemm_gguf_panel(const uint16_t*
     for (int nr = 0; nr < NR; nr++)
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[nr][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    auto compute = [&](const uint8_t* buf, const SkRaw<QT> (&wr)[NR]) {
-        static_for<8>([&](auto G) {
-            constexpr int g = decltype(G)::value;
+    // the four stages of half H of a super-block: A fragments from the half's buffer (chunk 4 (g % 4) + kq of row
+    // 16 mt + r, at chunk ^ r), B fragments dequantised from the super-block's raw bytes
+    auto compute = [&](auto H, const uint8_t* buf, const SkRaw<QT> (&wr)[NR]) {
+        static_for<4>([&](auto G) {
+            constexpr int gl = decltype(G)::value, g = 4 * decltype(H)::value + gl;
             bf16x8 bw[NR];
 #pragma unroll
             for (int nr = 0; nr < NR; nr++) bw[nr] = sk_dequant<QT, MID, g>(wr[nr], kq);
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
-                const bf16x8 ax = *reinterpret_cast<const bf16x8*>(buf + (16 * mt + r) * 512 + 16 * ((4 * g + kq) ^ r));
+                const bf16x8 ax = *reinterpret_cast<const bf16x8*>(buf + (16 * mt + r) * 256 + 16 * ((4 * gl + kq) ^ r));
 #pragma unroll
                 for (int nr = 0; nr < NR; nr++)
                     acc[nr][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bw[nr], acc[nr][mt], 0, 0, 0);
             }
         });
     };
-    // the ring: super-block i of the slice in buffer i % 2; at the top of each round every wave's copies of that
-    // super-block have landed (own loads: the counter; the others': the barrier), and every wave is past its reads of
-    // the other buffer, which then receives super-block i + 1
-    issue_a(xs0, sb0);
-    load_raw(w0, sb0);
-    for (int i = 0; i < nks; i += 2) {
+    // the ring, one half super-block (BM rows x 256 bytes, 32 KiB at 128 rows) per buffer, so that two workgroups
+    // fit a CU's LDS (two waves per SIMD): half 0 of every super-block in buffer 0, half 1 in buffer 1. At the top
+    // of each half every wave's copies of it have landed (own loads: the counter; the others': the barrier) and
+    // every wave is past its reads of the other buffer, which then receives the next half; the next super-block's
+    // raw weight bytes load during half 1, into the register set the previous super-block used.
+    using H0 = std::integral_constant<int, 0>;
+    using H1 = std::integral_constant<int, 1>;
+    auto superblock = [&](int i, SkRaw<QT> (&cur)[NR], SkRaw<QT> (&nxt)[NR]) {
+        wait_vm<0>();
+        wave_barrier_sync();
+        issue_a(xs1, sb0 + i, 1);
+        compute(H0{}, xs0, cur);
         wait_vm<0>();
         wave_barrier_sync();
         if (i + 1 < nks) {
-            issue_a(xs1, sb0 + i + 1);
-            load_raw(w1, sb0 + i + 1);
+            issue_a(xs0, sb0 + i + 1, 0);
+            load_raw(nxt, sb0 + i + 1);
         }
-        compute(xs0, w0);
+        compute(H1{}, xs1, cur);
+    };
+    issue_a(xs0, sb0, 0);
+    load_raw(w0, sb0);
+    for (int i = 0; i < nks; i += 2) {
+        superblock(i, w0, w1);
         if (i + 1 >= nks) break;
-        wait_vm<0>();
-        wave_barrier_sync();
-        if (i + 2 < nks) {
-            issue_a(xs0, sb0 + i + 2);
-            load_raw(w0, sb0 + i + 2);
-        }
-        compute(xs1, w1);
+        superblock(i + 1, w1, w0);
     }
     // lane (r, kq), register i: row m0 + 16 mt + 4 kq + i, column n0 + 16 nr + r
 #pragma unroll

@@ -70,13 +70,13 @@ def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
 # Wan-14B shapes (5120 x 5120, 13824 x 5120, 5120 x 13824), µs per block of six layers:
 #   * up to 64 rows, its few-rows form (the weight streamed through the chip once): 32 rows 124-134 µs against
 #     269-334 two-step (Q4_K);
-#   * 65-256 rows, its panel form (128 x 128 panels, K in slices): Q4_K 263 against 365 µs at 128 rows, 405 against
-#     495 at 256; Q6_K only up to 128 rows (344 against 369; 560 against 502 at 256);
-#   * from 512 rows on the two-step flow is faster: Q4_K 715 against 483 µs at 512 rows; Q5_K 1.85 against 1.76 ms
-#     at 4096; at 8192 the tiled form wins only 5120 x 5120, by 5 % (Q4_K), and loses the other shapes.
+#   * 65-256 rows, its panel form (128 x 128 panels, K in slices): Q4_K 183 against 367 µs at 128 rows, 290 against
+#     496 at 256; Q5_K 198 / 306 against 363 / 500; Q6_K 269 / 451 against 364 / 502;
+#   * from 512 rows on the two-step flow is faster: at 512 rows Q4_K 495 against 483 µs, Q6_K 821 against 496; Q5_K
+#     1.85 against 1.76 ms at 4096; at 8192 the tiled form wins only 5120 x 5120, by 5 % (Q4_K).
 # mode "fused" still takes the tiled form at any row count.
 FEW_ROWS = 64
-PANEL_ROWS = {12: 256, 13: 256, 14: 128}
+PANEL_ROWS = {12: 256, 13: 256, 14: 256}
 
 
 def prefer_fused(rows, qtype, n_out, k):

@@ -12,10 +12,10 @@ def test_prefer_fused_rule():
     for rows in (1, 16, 32, 64):
         assert fg.prefer_fused(rows, 12, 5120, 5120)
         assert fg.prefer_fused(rows, 14, 13824, 5120)
-    # medium rows: the panel form up to 256 rows for Q4_K / Q5_K, up to 128 for Q6_K
+    # medium rows: the panel form up to 256 rows
     for rows in (65, 128, 256):
-        assert fg.prefer_fused(rows, 12, 5120, 5120) and fg.prefer_fused(rows, 13, 13824, 5120)
-    assert fg.prefer_fused(128, 14, 5120, 5120) and not fg.prefer_fused(129, 14, 5120, 5120)
+        for q in (12, 13, 14):
+            assert fg.prefer_fused(rows, q, 5120, 5120) and fg.prefer_fused(rows, q, 13824, 5120)
     # from there on the two-step flow is faster for every format and shape
     for rows in (257, 512, 4096, 8192, 32768):
         for q in (12, 13, 14):
