@@ -386,10 +386,11 @@ class _ChunkState(_StreamState):
         views = (self.spares[self.u_spare[u]][2][t] if u in self.u_spare
                  else self.slot_type_views[u % self.n_chunk_slots][t])
         # Host-side fences in both directions (here, and on the slot-free event before a copy is issued), besides
-        # the stream waits: with the two stream waits alone, 40 Wan blocks streamed in 3 chunks each gave layers the
-        # wrong bytes from the third forward on in some processes (after other streams had been created and
-        # destroyed; never in the CPU protocol model, nor in block streaming). The host then runs at most the slots'
-        # depth ahead of the GPU; the copies stay ahead of the compute.
+        # the stream waits: with the two stream waits alone, 40 Wan blocks streamed in 3 chunks each gave layers
+        # wrong bytes on some machines (every forward on one, none on others), never with one hardware queue
+        # (GPU_MAX_HW_QUEUES=1, all commands in host order) and never in the CPU protocol model: the cross-queue
+        # ordering of a pending stream wait fails there. With the fences no cross-stream wait is ever pending. The
+        # host then runs at most the slots' depth ahead of the GPU; the copies stay ahead of the compute.
         if self.host_fence:
             self.unit_events[u].synchronize()
         _native.stream_wait(self.compute_stream(), self.unit_events[u])
