@@ -182,11 +182,11 @@ def fused_leg(torch, native):
                      "two_step_ms": round(tu, 3), "two_step_TFLOPS": round(flops / tu / 1e9, 1),
                      "flop": flops, "weight_bytes": wbytes}
     # few activation rows (128 and 32 tokens, and one token): the fused kernel's few-rows form streams each weight
-    # once, its panel form (65-512 rows) once per 128 rows. "cold": every call reads another copy of the weight, the
-    # copies of a layer spanning > 600 MB, so MI355X's 256 MB last-level cache cannot serve a call from the one
-    # before (a weight in a real forward was last read a step earlier); "warm": the same weight every call. One and
-    # 128 tokens go through fused_gguf.fused_linear, the drop-in's choice of form with its workspace (the panel form
-    # in K slices at 128 rows; few-rows at one row).
+    # once, its panel form once per 16 MT rows. "cold": every call reads another copy of the weight, the copies of a
+    # layer spanning > 600 MB, so MI355X's 256 MB last-level cache cannot serve a call from the one before (a weight
+    # in a real forward was last read a step earlier); "warm": the same weight every call. Every row count goes
+    # through fused_gguf.fused_linear, the drop-in's choice of form with its workspace: the panel form in K slices at
+    # 128 rows, and at 32 rows for Q6_K and the deep ffn_down (K >= 2 N); the few-rows form otherwise.
     fg = importlib.import_module(PKG + ".enhancers.fused_gguf")
     for rows in (128, 32, 1):
         for qt, name in ((12, "q4_k"), (13, "q5_k"), (14, "q6_k")):
@@ -202,11 +202,7 @@ def fused_leg(torch, native):
                 turn = [0]
 
                 def fused(r=raw):
-                    if rows == 1 or rows > 64:
-                        fg.fused_linear(x, r, qt, (N, K))
-                    else:
-                        lib.wf_linear_gguf(x.data_ptr(), rows, K, r.data_ptr(), r.numel(), qt, N, None, y.data_ptr(),
-                                           0, st)
+                    fg.fused_linear(x, r, qt, (N, K))
 
                 def fused_cold():
                     turn[0] += 1

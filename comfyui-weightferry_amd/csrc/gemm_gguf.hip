@@ -866,11 +866,12 @@ __global__ __launch_bounds__(64 * kSpWaves) void gemm_gguf_splitk(const uint16_t
     if (tid == 0) __hip_atomic_store(counters + tn, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// ------------------------------------------------------------------- medium row counts (64 < M <= kPanelMaxRows)
+// ----------------------------------------------------------------- medium row counts (16 < M <= kPanelMaxRows)
 // Between the few-rows kernel (every workgroup reads its activation fragments from L2: too much traffic beyond 64
-// rows) and the tiled kernel (256 x 320 output tiles: 16-128 workgroups on 256 CUs below 2048 rows), a workgroup
-// takes a panel: 128 weight rows (4 waves, each two 16-row groups as in the few-rows kernel) against BM = 16 MT
-// activation rows, over a slice of KS super-blocks of K. The activations stream through a two-buffer LDS ring, one
+// rows, and from 17-33 rows on the panel's split K already fills the chip better) and the tiled kernel (256 x 320
+// output tiles: 16-128 workgroups on 256 CUs below 2048 rows), a workgroup takes a panel: 128 weight rows (4 waves,
+// each two 16-row groups as in the few-rows kernel) against BM = 16 MT activation rows (MT = 2, 4 or 8), over a
+// slice of KS super-blocks of K. The activations stream through a two-buffer LDS ring, one
 // half super-block (BM rows x 256 bytes) per buffer -- 64 KiB at 128 rows, so two workgroups share a CU --, copied
 // by the load unit straight into LDS (buffer_load ... lds) one half ahead, 16-byte chunk c of row r at chunk
 // c ^ (r & 15) (the 16 rows of a fragment read fall in 16 different bank groups). The weight's raw bytes of the next
@@ -1193,14 +1194,26 @@ static int check_gguf(const char* who, const void* x_bf16, int64_t M, int64_t K,
     return WF_OK;
 }
 
-// Medium row counts: the panel kernel's plan. MT = 8 (128 activation rows per panel); slices S so that
-// NT x MTI x S >= 256 workgroups, at least two super-blocks each, and partial sums no larger than max_part bytes
-// (0: one slice, no workspace). Up to 512 rows it beats the tiled kernel (Wan block, Q4_K, one slice: 563 against
-// 856 us at 128 rows, 684 against 887 at 512); from 1024 rows the tiled kernel's 256 x 320 tiles, which dequantise
-// each weight value once per 256 rows instead of once per 128, are faster (909 against 1334 us).
+// Medium row counts: the panel kernel's plan. MT = 2 up to 32 rows, 4 up to 64, else 8 (128 activation rows per
+// panel); slices S so that NT x MTI x S >= 256 workgroups, at least two super-blocks each, and partial sums no larger
+// than max_part bytes (0: one slice, no workspace). Up to 512 rows it beats the tiled kernel (Wan block, Q4_K, one
+// slice: 563 against 856 us at 128 rows, 684 against 887 at 512); from 1024 rows the tiled kernel's 256 x 320 tiles,
+// which dequantise each weight value once per 256 rows instead of once per 128, are faster (909 against 1334 us).
 static constexpr int64_t kPanelMaxRows = 512;
+static constexpr int64_t kPanelMinRowsWs = 17;       // fewest rows the panel form takes with a workspace
 
+// Without a workspace (one slice) the panel form takes 65-512 rows.
 static bool panel_takes(int64_t M) { return M > 64 && M <= kPanelMaxRows; }
+
+// With a workspace (K in slices) it also takes 33-64 rows, and 17-32 rows of Q6_K or of a deep product (K >= 2 N),
+// where the few-rows kernel's one workgroup per 32 weight rows leaves CUs idle or runs long (measured on MI355X, Wan
+// shapes, warmed, with the workspace, per layer: Q4_K 5120 x 13824 at 32 rows 34.8 against 38.0 us, at 64 rows 45.1
+// against 70.0; Q6_K 5120 x 5120 at 17 rows 22.8 against 28.0; Q4_K 5120 x 5120 at 32 rows 17.0 against 16.5, so
+// shallow Q4_K / Q5_K products keep the few-rows kernel up to 32 rows).
+static bool panel_takes_ws(int64_t M, int64_t N, int64_t K, int qtype) {
+    if (M > 32) return M <= kPanelMaxRows;
+    return M >= kPanelMinRowsWs && (qtype == 14 || K >= 2 * N);
+}
 
 struct PanelPlan {
     int mt, mti, nt, ks, s;
@@ -1209,7 +1222,7 @@ struct PanelPlan {
 
 static PanelPlan panel_plan(int64_t M, int64_t N, int64_t K, int64_t max_part) {
     PanelPlan p{};
-    p.mt = 8;
+    p.mt = M <= 32 ? 2 : M <= 64 ? 4 : 8;
     p.mti = (int)((M + 16 * p.mt - 1) / (16 * p.mt));
     p.nt = (int)((N + kPnRows - 1) / kPnRows);
     const int nsb = (int)(K / 256);
@@ -1246,9 +1259,19 @@ static void launch_panel_mt(const uint16_t* X, const uint8_t* W, const uint16_t*
 template <int QT>
 static void launch_panel(int mid, const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M,
                          int N, int K, const PanelPlan& p, void* ws, hipStream_t st) {
-    if (mid == WF_F16) launch_panel_mt<QT, WF_F16, 8>(X, W, bias, Y, M, N, K, p, ws, st);
-    else if (mid == WF_BF16) launch_panel_mt<QT, WF_BF16, 8>(X, W, bias, Y, M, N, K, p, ws, st);
-    else launch_panel_mt<QT, WF_F32, 8>(X, W, bias, Y, M, N, K, p, ws, st);
+    if (p.mt == 2) {
+        if (mid == WF_F16) launch_panel_mt<QT, WF_F16, 2>(X, W, bias, Y, M, N, K, p, ws, st);
+        else if (mid == WF_BF16) launch_panel_mt<QT, WF_BF16, 2>(X, W, bias, Y, M, N, K, p, ws, st);
+        else launch_panel_mt<QT, WF_F32, 2>(X, W, bias, Y, M, N, K, p, ws, st);
+    } else if (p.mt == 4) {
+        if (mid == WF_F16) launch_panel_mt<QT, WF_F16, 4>(X, W, bias, Y, M, N, K, p, ws, st);
+        else if (mid == WF_BF16) launch_panel_mt<QT, WF_BF16, 4>(X, W, bias, Y, M, N, K, p, ws, st);
+        else launch_panel_mt<QT, WF_F32, 4>(X, W, bias, Y, M, N, K, p, ws, st);
+    } else {
+        if (mid == WF_F16) launch_panel_mt<QT, WF_F16, 8>(X, W, bias, Y, M, N, K, p, ws, st);
+        else if (mid == WF_BF16) launch_panel_mt<QT, WF_BF16, 8>(X, W, bias, Y, M, N, K, p, ws, st);
+        else launch_panel_mt<QT, WF_F32, 8>(X, W, bias, Y, M, N, K, p, ws, st);
+    }
 }
 
 static void run_gguf_panel(int qtype, int mid_dt, const void* x_bf16, const void* wq, const void* bias_bf16,
@@ -1305,8 +1328,9 @@ extern "C" int wf_linear_gguf_workspace(int64_t M, int64_t N, int64_t K, int64_t
     if (!bytes) { set_error("wf_linear_gguf_workspace: null out-pointer"); return WF_EINVAL; }
     *bytes = 0;
     if (M < 0 || N < 0 || K <= 0 || K % 256) { set_error("wf_linear_gguf_workspace: M, N, K"); return WF_EINVAL; }
+    // the format is not known here: the largest need over them (Q6_K takes the panel form from 17 rows)
     if (split_takes(M, N, K)) *bytes = split_plan(M, N, K).bytes();
-    else if (panel_takes(M)) *bytes = panel_plan(M, N, K, INT64_MAX).part_bytes;
+    else if (panel_takes_ws(M, N, K, 14)) *bytes = panel_plan(M, N, K, INT64_MAX).part_bytes;
     return WF_OK;
 }
 
@@ -1317,7 +1341,10 @@ extern "C" int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const
     const int rc = check_gguf("wf_linear_gguf_ws", x_bf16, M, K, wq, wq_bytes, qtype, N, bias_bf16, out_bf16, mid_dt);
     if (rc != WF_OK || M == 0 || N == 0) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (!split_takes(M, N, K) && panel_takes(M)) {
+    // up to 64 rows the panel form runs only in more than one slice (in one, the few-rows kernel is faster)
+    const bool panel = !split_takes(M, N, K) && panel_takes_ws(M, N, K, qtype) &&
+                       (panel_takes(M) || panel_plan(M, N, K, INT64_MAX).s > 1);
+    if (panel) {
         const PanelPlan p = panel_plan(M, N, K, INT64_MAX);
         if (p.part_bytes > 0 && (!workspace || !aligned(workspace, 256) || workspace_bytes < p.part_bytes)) {
             set_error("wf_linear_gguf_ws: a 256-byte aligned workspace of %lld bytes is needed (given %lld)",
@@ -1389,7 +1416,9 @@ extern "C" int wf_linear_gguf_noalloc(const void* x_bf16, int64_t M, int64_t K, 
                               mid_dt);
     if (rc != WF_OK || M == 0 || N == 0) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (!split_takes(M, N, K) && panel_takes(M)) {
+    // (up to 64 rows only when the scratch holds more than one slice: in one slice the few-rows kernel is faster)
+    if (!split_takes(M, N, K) && panel_takes_ws(M, N, K, qtype) &&
+        (panel_takes(M) || panel_plan(M, N, K, kScratchBytes).s > 1)) {
         // the panel form's partial sums in the scratch array, as many slices as fit there
         const PanelPlan p = panel_plan(M, N, K, kScratchBytes);
         void* ws = nullptr;

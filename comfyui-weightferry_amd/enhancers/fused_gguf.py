@@ -56,7 +56,7 @@ def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
                 y.data_ptr(), _MID[mid])
         need = ctypes.c_int64()
         _native.call("wf_linear_gguf_workspace", rows, n_out, k, ctypes.byref(need))
-        if need.value:              # the split form (few rows of a deep product) with its workspace
+        if need.value:              # the split or panel form (K in slices) with its workspace
             ws = _workspace(x.device, stream, need.value)
             rc = lib.wf_linear_gguf_ws(*args, ws.data_ptr(), ws.numel(), stream)
         else:
@@ -69,7 +69,8 @@ def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
 # Where the fused kernel beats the two-step flow (one dequantisation, then hipBLASLt), measured on MI355X over the
 # Wan-14B shapes (5120 x 5120, 13824 x 5120, 5120 x 13824), µs per block of six layers:
 #   * up to 64 rows, its few-rows form (the weight streamed through the chip once): 32 rows 124-134 µs against
-#     269-334 two-step (Q4_K);
+#     269-334 two-step (Q4_K); with the workspace the library runs the panel form in K slices from 33 rows, and from
+#     17 rows for Q6_K and deep products (K >= 2 N) (Wan shapes at 64 rows: 5120 x 13824 Q4_K 45 against 70 µs);
 #   * 65-256 rows, its panel form (128 x 128 panels, K in slices): Q4_K 183 against 367 µs at 128 rows, 290 against
 #     496 at 256; Q5_K 198 / 306 against 363 / 500; Q6_K 269 / 451 against 364 / 502;
 #   * from 512 rows on the two-step flow is faster: at 512 rows Q4_K 495 against 483 µs, Q6_K 821 against 496; Q5_K

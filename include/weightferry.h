@@ -109,11 +109,13 @@ int wf_linear_gguf(const void* x_bf16, int64_t M, int64_t K, const void* wq, int
  * last workgroup of each column tile adds them in a fixed order (the result is the same on every run). Workspace:
  * 256-byte aligned, at least the bytes wf_linear_gguf_workspace gives; its first 16 KiB are counters that must be
  * zero on entry and are zero again when the call has run, whatever its shape (a workspace cleared once can be reused
- * by later calls of any shape on the same stream; calls that overlap on one workspace race). With 65-512 rows
- * (at least four super-blocks of K) the panel form splits K into slices, enough to give the chip 256 workgroups:
- * each slice writes float32 partial sums into the workspace (S * M * N * 4 bytes, no counters) and a second kernel
- * adds them in slice order. Any other shape does not use the workspace (wf_linear_gguf_workspace gives 0; workspace
- * may be NULL) and is wf_linear_gguf. */
+ * by later calls of any shape on the same stream; calls that overlap on one workspace race). With 33-512 rows,
+ * and with 17-32 rows of Q6_K or of a deep product (K >= 2 N), the panel form splits K into slices (at least two
+ * super-blocks each), enough to give the chip 256 workgroups: each slice writes float32 partial sums into the
+ * workspace (S * M * N * 4 bytes, no counters) and a second kernel adds them in slice order; up to 64 rows only when
+ * K gives more than one slice. wf_linear_gguf_workspace does not know the format and gives the largest need over
+ * them (the panel form's bytes from 17 rows). Any other shape does not use the workspace (workspace may be NULL) and
+ * is wf_linear_gguf. */
 int wf_linear_gguf_workspace(int64_t M, int64_t N, int64_t K, int64_t* bytes);
 int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes, int qtype, int64_t N,
                       const void* bias_bf16, void* out_bf16, int mid_dt, void* workspace, int64_t workspace_bytes,
@@ -124,7 +126,8 @@ int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const void* wq, 
  * forbid hipMalloc). The split form's counters and partial sums live in a 16 MiB array the library holds on each GPU
  * it runs on until the process ends; the counters are cleared by a small kernel on `stream` at the start of each call
  * (no memset). A shape that needs more than 16 MiB there returns WF_EUNSUPPORTED with a message. The panel form
- * (65-512 rows) takes as many K slices as fit the array (one, and no scratch, at worst). Every call on a GPU shares
+ * (the rows of wf_linear_gguf_ws) takes as many K slices as fit the array (one, and no scratch, at worst; up to 64
+ * rows one slice leaves the call to the few-rows kernel). Every call on a GPU shares
  * that GPU's array: calls that overlap on one GPU (on different streams or threads) race. */
 int wf_linear_gguf_noalloc(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes, int qtype,
                            int64_t N, const void* bias_bf16, void* out_bf16, int mid_dt, void* stream);

@@ -52,7 +52,7 @@ def test_noalloc_equals_the_workspace_entry_point(native, qtype):
 
 def test_noalloc_without_split_is_the_plain_entry_point(native):
     g = torch.Generator().manual_seed(5)
-    M, N, K = 32, 5120, 5120
+    M, N, K = 16, 5120, 5120
     raw = torch.from_numpy(encode.random_blocks(12, N * K // 256, seed=9, family="normal")).cuda()
     x = torch.randn((M, K), generator=g).to(torch.bfloat16).cuda()
     assert _workspace(native, M, N, K)[0] == 0
