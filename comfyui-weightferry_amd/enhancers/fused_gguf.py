@@ -72,12 +72,15 @@ def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
 #     269-334 two-step (Q4_K); with the workspace the library runs the panel form in K slices from 33 rows, and from
 #     17 rows for Q6_K and deep products (K >= 2 N) (Wan shapes at 64 rows: 5120 x 13824 Q4_K 45 against 70 µs);
 #   * 65-256 rows, its panel form (128 x 128 panels, K in slices): Q4_K 183 against 367 µs at 128 rows, 290 against
-#     496 at 256; Q5_K 198 / 306 against 363 / 500; Q6_K 269 / 451 against 364 / 502;
-#   * from 512 rows on the two-step flow is faster: at 512 rows Q4_K 495 against 483 µs, Q6_K 821 against 496; Q5_K
-#     1.85 against 1.76 ms at 4096; at 8192 the tiled form wins only 5120 x 5120, by 5 % (Q4_K).
+#     496 at 256; Q5_K 198 / 306 against 363 / 500; Q6_K 269 / 451 against 364 / 502; and up to 384 rows for Q4_K /
+#     Q5_K (three 128-row panels): Q4_K 375 / 380 against 411 / 417 at 320 / 384 rows, Q5_K 408 / 412 against
+#     415 / 421 (Q6_K 607 against 413 at 320);
+#   * from 448 rows on the two-step flow is faster: Q4_K 487 against 465 µs at 448 rows, 495 against 483 at 512,
+#     Q6_K 821 against 496; Q5_K 1.80 against 1.72 ms at 4096; at 8192 the tiled form wins only 5120 x 5120, by
+#     5 % (Q4_K).
 # mode "fused" still takes the tiled form at any row count.
 FEW_ROWS = 64
-PANEL_ROWS = {12: 256, 13: 256, 14: 256}
+PANEL_ROWS = {12: 384, 13: 384, 14: 256}
 
 
 def prefer_fused(rows, qtype, n_out, k):

@@ -12,12 +12,16 @@ def test_prefer_fused_rule():
     for rows in (1, 16, 32, 64):
         assert fg.prefer_fused(rows, 12, 5120, 5120)
         assert fg.prefer_fused(rows, 14, 13824, 5120)
-    # medium rows: the panel form up to 256 rows
+    # medium rows: the panel form up to 256 rows, up to 384 for Q4_K / Q5_K
     for rows in (65, 128, 256):
         for q in (12, 13, 14):
             assert fg.prefer_fused(rows, q, 5120, 5120) and fg.prefer_fused(rows, q, 13824, 5120)
+    for rows in (257, 320, 384):
+        for q in (12, 13):
+            assert fg.prefer_fused(rows, q, 5120, 5120)
+        assert not fg.prefer_fused(rows, 14, 5120, 5120)
     # from there on the two-step flow is faster for every format and shape
-    for rows in (257, 512, 4096, 8192, 32768):
+    for rows in (385, 512, 4096, 8192, 32768):
         for q in (12, 13, 14):
             assert not fg.prefer_fused(rows, q, 5120, 5120) and not fg.prefer_fused(rows, q, 5120, 13824)
 
