@@ -74,7 +74,8 @@ def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
 #   * 65-256 rows, its panel form (128 x 128 panels, K in slices): Q4_K 183 against 367 µs at 128 rows, 290 against
 #     496 at 256; Q5_K 198 / 306 against 363 / 500; Q6_K 269 / 451 against 364 / 502; and up to 384 rows for Q4_K /
 #     Q5_K (three 128-row panels): Q4_K 375 / 380 against 411 / 417 at 320 / 384 rows, Q5_K 408 / 412 against
-#     415 / 421 (Q6_K 607 against 413 at 320);
+#     415 / 421 (Q6_K 607 against 413 at 320) -- except the wide ffn_up (n_out > k: 13824 x 5120, 102 against 85 µs
+#     at 320 rows, 324 panels on 256 CUs), which keeps the two-step flow above 256 rows;
 #   * from 448 rows on the two-step flow is faster: Q4_K 487 against 465 µs at 448 rows, 495 against 483 at 512,
 #     Q6_K 821 against 496; Q5_K 1.80 against 1.72 ms at 4096; at 8192 the tiled form wins only 5120 x 5120, by
 #     5 % (Q4_K).
@@ -85,7 +86,12 @@ PANEL_ROWS = {12: 384, 13: 384, 14: 256}
 
 def prefer_fused(rows, qtype, n_out, k):
     """mode "auto": True when the fused kernel is the faster way to compute this layer on MI355X."""
-    return rows <= FEW_ROWS or rows <= PANEL_ROWS.get(int(qtype), 0)
+    if rows <= FEW_ROWS:
+        return True
+    limit = PANEL_ROWS.get(int(qtype), 0)
+    if n_out > k:
+        limit = min(limit, 256)
+    return rows <= limit
 
 
 def linear(x, data, qtype, oshape, bias=None, mid_dtype=None, mode="auto"):

@@ -18,7 +18,8 @@ def test_prefer_fused_rule():
             assert fg.prefer_fused(rows, q, 5120, 5120) and fg.prefer_fused(rows, q, 13824, 5120)
     for rows in (257, 320, 384):
         for q in (12, 13):
-            assert fg.prefer_fused(rows, q, 5120, 5120)
+            assert fg.prefer_fused(rows, q, 5120, 5120) and fg.prefer_fused(rows, q, 5120, 13824)
+            assert not fg.prefer_fused(rows, q, 13824, 5120)            # wide outputs: two-step above 256 rows
         assert not fg.prefer_fused(rows, 14, 5120, 5120)
     # from there on the two-step flow is faster for every format and shape
     for rows in (385, 512, 4096, 8192, 32768):
