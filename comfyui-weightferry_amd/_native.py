@@ -185,7 +185,15 @@ def stream_wait(stream, event):
     call("wf_stream_wait_event", stream, event.handle)
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(device):
     """Raw hipStream_t of torch's current stream on ``device`` (the convention of the reference's int8 path,
-    enhancers/fused_int8.py:151)."""
+    enhancers/fused_int8.py:151). torch's raw-stream query when it has one (a fraction of the cost of building the
+    Stream object: this runs once per layer call)."""
+    if _raw_stream is not None:
+        if not isinstance(device, torch.device):
+            device = torch.device(device)
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream

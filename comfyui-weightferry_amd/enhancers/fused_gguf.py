@@ -17,6 +17,7 @@ from . import gguf_dequant
 _FUSED_TYPES = {12: 144, 13: 176, 14: 210}
 _MID = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 _workspaces = {}             # (device index, stream) -> uint8 workspace whose counter words are zero between calls
+_needs = {}                  # (rows, n_out, k) -> the workspace bytes wf_linear_gguf_workspace gives
 
 
 def _workspace(device, stream, nbytes):
@@ -31,6 +32,31 @@ def _workspace(device, stream, nbytes):
     return ws
 
 
+def _workspace_bytes(rows, n_out, k):
+    """wf_linear_gguf_workspace for this shape, asked once per shape (the answer depends on the shape only)."""
+    key = (rows, n_out, k)
+    need = _needs.get(key)
+    if need is None:
+        v = ctypes.c_int64()
+        _native.call("wf_linear_gguf_workspace", rows, n_out, k, ctypes.byref(v))
+        if len(_needs) > 4096:
+            _needs.clear()
+        need = _needs[key] = v.value
+    return need
+
+
+def _launch(x2, raw, q, n_out, k, b, y, mid):
+    rows = x2.shape[0]
+    stream = _native.stream_of(x2.device)
+    args = (x2.data_ptr(), rows, k, raw.data_ptr(), raw.numel(), q, n_out, b.data_ptr() if b is not None else None,
+            y.data_ptr(), mid)
+    need = _workspace_bytes(rows, n_out, k)
+    if need:                        # the split or panel form (K in slices) with its workspace
+        ws = _workspace(x2.device, stream, need)
+        return _native.lib().wf_linear_gguf_ws(*args, ws.data_ptr(), ws.numel(), stream)
+    return _native.lib().wf_linear_gguf(*args, stream)
+
+
 def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
     """y = x @ dequantize(W).T (+ bias) in one kernel, or None when this is not that case."""
     q = int(qtype) if qtype is not None else None
@@ -42,28 +68,23 @@ def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
     mid = torch.float16 if mid_dtype is None else mid_dtype
     if mid not in _MID:
         return None
-    raw = data.reshape(-1).view(torch.uint8) if data.is_contiguous() else None
-    if raw is None or raw.numel() != n_out * (k // 256) * _FUSED_TYPES[q]:
+    if not data.is_contiguous():
         return None
-    x2 = x.reshape(-1, k).contiguous()
-    rows = x2.shape[0]
-    y = torch.empty((rows, n_out), dtype=torch.bfloat16, device=x.device)
-    b = bias.contiguous() if bias is not None else None
-    lib = _native.lib()
-    with torch.cuda.device(x.device):
-        stream = _native.stream_of(x.device)
-        args = (x2.data_ptr(), rows, k, raw.data_ptr(), raw.numel(), q, n_out, b.data_ptr() if b is not None else None,
-                y.data_ptr(), _MID[mid])
-        need = ctypes.c_int64()
-        _native.call("wf_linear_gguf_workspace", rows, n_out, k, ctypes.byref(need))
-        if need.value:              # the split or panel form (K in slices) with its workspace
-            ws = _workspace(x.device, stream, need.value)
-            rc = lib.wf_linear_gguf_ws(*args, ws.data_ptr(), ws.numel(), stream)
-        else:
-            rc = lib.wf_linear_gguf(*args, stream)
+    # (the reshapes only where needed: this runs once per layer call, and with few rows its host time is the layer's)
+    raw = data if data.dim() == 1 and data.dtype == torch.uint8 else data.reshape(-1).view(torch.uint8)
+    if raw.numel() != n_out * (k // 256) * _FUSED_TYPES[q]:
+        return None
+    x2 = x if x.dim() == 2 and x.is_contiguous() else x.reshape(-1, k).contiguous()
+    y = torch.empty((x2.shape[0], n_out), dtype=torch.bfloat16, device=x.device)
+    b = bias if bias is None or bias.is_contiguous() else bias.contiguous()
+    if x.device.index == torch.cuda.current_device():
+        rc = _launch(x2, raw, q, n_out, k, b, y, _MID[mid])
+    else:                           # the kernels run on the current device: make it x's for the call
+        with torch.cuda.device(x.device):
+            rc = _launch(x2, raw, q, n_out, k, b, y, _MID[mid])
     if not _native.check(rc, "wf_linear_gguf"):
         return None
-    return y.reshape(*x.shape[:-1], n_out)
+    return y if x.dim() == 2 else y.reshape(*x.shape[:-1], n_out)
 
 
 # Where the fused kernel beats the two-step flow (one dequantisation, then hipBLASLt), measured on MI355X over the
