@@ -7,6 +7,7 @@ falls back to a CPU or torch computation of its own).
 torch is imported before the library is loaded so that the library binds to torch's HIP runtime (both carry the
 SONAME libamdhip64.so.7): one runtime per process, and torch's stream handles are valid in every call.
 """
+import contextlib
 import ctypes
 import os
 import threading
@@ -186,6 +187,15 @@ def stream_wait(stream, event):
 
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_no_guard = contextlib.nullcontext()
+
+
+def on_device(device):
+    """``torch.cuda.device(device)`` when ``device`` is not the current device, else a no-op context: the library's
+    kernels run on the current device, and the guard costs a few microseconds per call when it changes nothing."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return _no_guard
+    return torch.cuda.device(device)
 
 
 def stream_of(device):

@@ -77,11 +77,8 @@ def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
     x2 = x if x.dim() == 2 and x.is_contiguous() else x.reshape(-1, k).contiguous()
     y = torch.empty((x2.shape[0], n_out), dtype=torch.bfloat16, device=x.device)
     b = bias if bias is None or bias.is_contiguous() else bias.contiguous()
-    if x.device.index == torch.cuda.current_device():
+    with _native.on_device(x.device):
         rc = _launch(x2, raw, q, n_out, k, b, y, _MID[mid])
-    else:                           # the kernels run on the current device: make it x's for the call
-        with torch.cuda.device(x.device):
-            rc = _launch(x2, raw, q, n_out, k, b, y, _MID[mid])
     if not _native.check(rc, "wf_linear_gguf"):
         return None
     return y if x.dim() == 2 else y.reshape(*x.shape[:-1], n_out)

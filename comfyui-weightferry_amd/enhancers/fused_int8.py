@@ -53,7 +53,7 @@ def quantise_rows(x_2d, mode):
     dev = x_2d.device
     x_q = torch.empty((m, k), dtype=torch.int8, device=dev)
     x_s = torch.empty((m, 1), dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _native.on_device(dev):
         rc = _native.lib().wf_quant_rows_i8(x_2d.data_ptr(), m, k, mode, x_q.data_ptr(), x_s.data_ptr(), _stream(dev))
     return (x_q, x_s) if _native.check(rc, "wf_quant_rows_i8") else None
 
@@ -66,7 +66,7 @@ def gemm(x_q, x_s, w_q, ws, out_dtype=torch.bfloat16, bias=None):
     dev = x_q.device
     out = torch.empty((m, n), dtype=out_dtype, device=dev)
     code = 1 if out_dtype == torch.bfloat16 else 0
-    with torch.cuda.device(dev):
+    with _native.on_device(dev):
         rc = _native.lib().wf_linear_i8(x_q.data_ptr(), w_q.data_ptr(), x_s.data_ptr(), ws.data_ptr(),
                                         None if bias is None else bias.data_ptr(), out.data_ptr(), code, m, n, k,
                                         _stream(dev))
@@ -75,7 +75,7 @@ def gemm(x_q, x_s, w_q, ws, out_dtype=torch.bfloat16, bias=None):
 
 def _gemm_residual(q, gate_2d, resid_2d, out_2d, rows_per_gate):
     """wf_linear_i8_residual: out = bf16(resid + gate[row // rows_per_gate] * linear) over q's rows."""
-    with torch.cuda.device(q.device):
+    with _native.on_device(q.device):
         rc = _native.lib().wf_linear_i8_residual(q.x_q.data_ptr(), q.w_q.data_ptr(), q.x_s.data_ptr(),
                                                  q.ws.data_ptr(), gate_2d.data_ptr(), resid_2d.data_ptr(),
                                                  out_2d.data_ptr(), q.m, q.n, q.w_q.shape[1], rows_per_gate,
@@ -229,7 +229,7 @@ def quantise_pre(pre, x_2d):
         eps = float(pre.norm.eps) if code == PRE_LNMOD else 0.0
     x_q = torch.empty((m, k), dtype=torch.int8, device=dev)
     x_s = torch.empty((m, 1), dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _native.on_device(dev):
         rc = _native.lib().wf_quant_rows_i8_pre(x_2d.data_ptr(), m, k, code, table.data_ptr(),
                                                 None if shift is None else shift.data_ptr(), rows, eps,
                                                 x_q.data_ptr(), x_s.data_ptr(), _stream(dev))

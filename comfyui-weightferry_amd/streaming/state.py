@@ -65,7 +65,7 @@ class _StreamState:
         self.ssd_submitted = 0
 
     def compute_stream(self):
-        return torch.cuda.current_stream(self.device).cuda_stream
+        return _native.stream_of(self.device)
 
     def slot_of(self, s_idx):
         return s_idx % self.num_slots
