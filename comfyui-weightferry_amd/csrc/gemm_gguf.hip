@@ -1220,14 +1220,21 @@ struct PanelPlan {
     int64_t part_bytes;
 };
 
-static PanelPlan panel_plan(int64_t M, int64_t N, int64_t K, int64_t max_part) {
+// Workgroups the slices aim for: 256 (one per CU), or 512 (two per CU, which the 64 KiB ring allows) where that
+// measured faster on MI355X (Wan shapes, warmed, with the workspace): from 385 rows (Q4_K block at 512 rows 473
+// against 495 us, Q6_K 739 against 818) and for Q6_K up to 128 rows (254 against 268 at 128); elsewhere the extra
+// partial sums cost more than the second workgroup gains (Q4_K 303 against 289 at 256 rows).
+static int panel_target(int64_t M, int qtype) { return M > 384 || (qtype == 14 && M <= 128) ? 512 : 256; }
+
+static PanelPlan panel_plan(int64_t M, int64_t N, int64_t K, int64_t max_part, int qtype) {
     PanelPlan p{};
     p.mt = M <= 32 ? 2 : M <= 64 ? 4 : 8;
     p.mti = (int)((M + 16 * p.mt - 1) / (16 * p.mt));
     p.nt = (int)((N + kPnRows - 1) / kPnRows);
     const int nsb = (int)(K / 256);
     const int64_t tiles = (int64_t)p.nt * p.mti;
-    int s = (int)std::min<int64_t>((256 + tiles - 1) / tiles, std::max(1, nsb / 2));
+    const int64_t target = panel_target(M, qtype);
+    int s = (int)std::min<int64_t>((target + tiles - 1) / tiles, std::max(1, nsb / 2));
     while (s > 1 && (int64_t)s * M * N * 4 > max_part) s--;
     p.ks = (nsb + s - 1) / s;
     p.s = (nsb + p.ks - 1) / p.ks;
@@ -1292,7 +1299,8 @@ static void run_gguf(int qtype, int mid_dt, const void* x_bf16, const void* wq, 
     const uint16_t* B = static_cast<const uint16_t*>(bias_bf16);
     uint16_t* Y = static_cast<uint16_t*>(out_bf16);
     if (panel_takes(M)) {                             // without a workspace: one slice
-        run_gguf_panel(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, M, N, K, panel_plan(M, N, K, 0), nullptr, s);
+        run_gguf_panel(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, M, N, K, panel_plan(M, N, K, 0, qtype), nullptr,
+                       s);
         return;
     }
     if (qtype == 12) launch_mid<12>(mid_dt, X, W, B, Y, M, N, K, s);
@@ -1328,9 +1336,11 @@ extern "C" int wf_linear_gguf_workspace(int64_t M, int64_t N, int64_t K, int64_t
     if (!bytes) { set_error("wf_linear_gguf_workspace: null out-pointer"); return WF_EINVAL; }
     *bytes = 0;
     if (M < 0 || N < 0 || K <= 0 || K % 256) { set_error("wf_linear_gguf_workspace: M, N, K"); return WF_EINVAL; }
-    // the format is not known here: the largest need over them (Q6_K takes the panel form from 17 rows)
+    // the format is not known here: the largest need over them (Q6_K takes the panel form from 17 rows, and more
+    // slices up to 128 rows)
     if (split_takes(M, N, K)) *bytes = split_plan(M, N, K).bytes();
-    else if (panel_takes_ws(M, N, K, 14)) *bytes = panel_plan(M, N, K, INT64_MAX).part_bytes;
+    else if (panel_takes_ws(M, N, K, 14))
+        *bytes = std::max(panel_plan(M, N, K, INT64_MAX, 12).part_bytes, panel_plan(M, N, K, INT64_MAX, 14).part_bytes);
     return WF_OK;
 }
 
@@ -1343,9 +1353,9 @@ extern "C" int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const
     hipStream_t s = static_cast<hipStream_t>(stream);
     // up to 64 rows the panel form runs only in more than one slice (in one, the few-rows kernel is faster)
     const bool panel = !split_takes(M, N, K) && panel_takes_ws(M, N, K, qtype) &&
-                       (panel_takes(M) || panel_plan(M, N, K, INT64_MAX).s > 1);
+                       (panel_takes(M) || panel_plan(M, N, K, INT64_MAX, qtype).s > 1);
     if (panel) {
-        const PanelPlan p = panel_plan(M, N, K, INT64_MAX);
+        const PanelPlan p = panel_plan(M, N, K, INT64_MAX, qtype);
         if (p.part_bytes > 0 && (!workspace || !aligned(workspace, 256) || workspace_bytes < p.part_bytes)) {
             set_error("wf_linear_gguf_ws: a 256-byte aligned workspace of %lld bytes is needed (given %lld)",
                       (long long)p.part_bytes, (long long)workspace_bytes);
@@ -1418,9 +1428,9 @@ extern "C" int wf_linear_gguf_noalloc(const void* x_bf16, int64_t M, int64_t K, 
     hipStream_t s = static_cast<hipStream_t>(stream);
     // (up to 64 rows only when the scratch holds more than one slice: in one slice the few-rows kernel is faster)
     if (!split_takes(M, N, K) && panel_takes_ws(M, N, K, qtype) &&
-        (panel_takes(M) || panel_plan(M, N, K, kScratchBytes).s > 1)) {
+        (panel_takes(M) || panel_plan(M, N, K, kScratchBytes, qtype).s > 1)) {
         // the panel form's partial sums in the scratch array, as many slices as fit there
-        const PanelPlan p = panel_plan(M, N, K, kScratchBytes);
+        const PanelPlan p = panel_plan(M, N, K, kScratchBytes, qtype);
         void* ws = nullptr;
         if (p.part_bytes > 0) {
             const int src = scratch_address(&ws);

@@ -93,13 +93,14 @@ def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
 #     496 at 256; Q5_K 198 / 306 against 363 / 500; Q6_K 269 / 451 against 364 / 502; and up to 384 rows for Q4_K /
 #     Q5_K (three 128-row panels): Q4_K 375 / 380 against 411 / 417 at 320 / 384 rows, Q5_K 408 / 412 against
 #     415 / 421 (Q6_K 607 against 413 at 320) -- except the wide ffn_up (n_out > k: 13824 x 5120, 102 against 85 µs
-#     at 320 rows, 324 panels on 256 CUs), which keeps the two-step flow above 256 rows;
-#   * from 448 rows on the two-step flow is faster: Q4_K 487 against 465 µs at 448 rows, 495 against 483 at 512,
-#     Q6_K 821 against 496; Q5_K 1.80 against 1.72 ms at 4096; at 8192 the tiled form wins only 5120 x 5120, by
+#     at 320 rows, 324 panels on 256 CUs), which keeps the two-step flow above 256 rows; Q4_K up to 512 rows (with
+#     512 workgroups of K slices there): 5120 x 5120 58 against 61 µs at 512 rows, 5120 x 13824 122 against 137;
+#   * above that the two-step flow is faster: Q5_K 515 / 524 against 467 / 490 µs per block at 448 / 512 rows, Q6_K
+#     737 against 491 at 512; Q5_K 1.80 against 1.72 ms at 4096; at 8192 the tiled form wins only 5120 x 5120, by
 #     5 % (Q4_K).
 # mode "fused" still takes the tiled form at any row count.
 FEW_ROWS = 64
-PANEL_ROWS = {12: 384, 13: 384, 14: 256}
+PANEL_ROWS = {12: 512, 13: 384, 14: 256}
 
 
 def prefer_fused(rows, qtype, n_out, k):

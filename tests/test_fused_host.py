@@ -12,7 +12,7 @@ def test_prefer_fused_rule():
     for rows in (1, 16, 32, 64):
         assert fg.prefer_fused(rows, 12, 5120, 5120)
         assert fg.prefer_fused(rows, 14, 13824, 5120)
-    # medium rows: the panel form up to 256 rows, up to 384 for Q4_K / Q5_K
+    # medium rows: the panel form up to 256 rows, up to 384 for Q5_K and 512 for Q4_K
     for rows in (65, 128, 256):
         for q in (12, 13, 14):
             assert fg.prefer_fused(rows, q, 5120, 5120) and fg.prefer_fused(rows, q, 13824, 5120)
@@ -21,8 +21,12 @@ def test_prefer_fused_rule():
             assert fg.prefer_fused(rows, q, 5120, 5120) and fg.prefer_fused(rows, q, 5120, 13824)
             assert not fg.prefer_fused(rows, q, 13824, 5120)            # wide outputs: two-step above 256 rows
         assert not fg.prefer_fused(rows, 14, 5120, 5120)
+    for rows in (385, 448, 512):
+        assert fg.prefer_fused(rows, 12, 5120, 5120) and fg.prefer_fused(rows, 12, 5120, 13824)
+        assert not fg.prefer_fused(rows, 12, 13824, 5120)
+        assert not fg.prefer_fused(rows, 13, 5120, 5120) and not fg.prefer_fused(rows, 14, 5120, 5120)
     # from there on the two-step flow is faster for every format and shape
-    for rows in (385, 512, 4096, 8192, 32768):
+    for rows in (513, 1024, 4096, 8192, 32768):
         for q in (12, 13, 14):
             assert not fg.prefer_fused(rows, q, 5120, 5120) and not fg.prefer_fused(rows, q, 5120, 13824)
 
@@ -42,8 +46,8 @@ def test_auto_routes_by_rows(monkeypatch):
     monkeypatch.setattr(fg.gguf_dequant, "dequantize", fake_dequant)
     data = torch.zeros(16, dtype=torch.uint8)
     fg.linear(torch.zeros(2, 8, 256, dtype=torch.bfloat16), data, 12, (32, 256))           # 16 rows
-    fg.linear(torch.zeros(1, 512, 256, dtype=torch.bfloat16), data, 12, (32, 256))         # 512 rows
-    fg.linear(torch.zeros(1, 512, 256, dtype=torch.bfloat16), data, 12, (32, 256), mode="fused")
+    fg.linear(torch.zeros(1, 1024, 256, dtype=torch.bfloat16), data, 12, (32, 256))        # 1024 rows
+    fg.linear(torch.zeros(1, 1024, 256, dtype=torch.bfloat16), data, 12, (32, 256), mode="fused")
     fg.linear(torch.zeros(4, 256, dtype=torch.bfloat16), data, 12, (32, 256), mode="dequant")
     assert calls == ["fused", "dequant", "fused", "dequant"]
     layer = fg.GGUFLinear(256, 32, 12, bias=False)
