@@ -254,3 +254,37 @@ def test_panel_workspace_is_checked(native):
     st = native.stream_of(x.device)
     assert native.lib().wf_linear_gguf_ws(x.data_ptr(), M, K, w.data_ptr(), w.numel(), 12, N, None, y.data_ptr(), 0,
                                           ws.data_ptr(), need.value - 1, st) == native.EINVAL
+
+
+@pytest.mark.parametrize("qtype", [12, 14])
+@pytest.mark.parametrize("rows", [1, 40, 130])
+def test_fused_linear_input_layouts(native, qtype, rows):
+    # the drop-in takes the weight as ComfyUI-GGUF holds it (1-D or [N, bytes per row] uint8), activations of any
+    # leading shape or strides, and a strided bias: every layout gives the bits of the plain 2-D contiguous call,
+    # which is itself checked against float64 on the dequantised weight
+    fg = sub("enhancers.fused_gguf")
+    N, K = 384, 1024
+    raw = encode.random_blocks(qtype, N * K // 256, seed=rows + qtype, family="normal")
+    g = torch.Generator().manual_seed(rows)
+    x = torch.randn((rows, K), generator=g).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16)
+    rd, xd, bd = torch.from_numpy(raw).cuda(), x.cuda(), bias.cuda()
+    print(f"case fused_linear layouts qtype={qtype} rows={rows}", flush=True)
+    ref = fg.fused_linear(xd, rd, qtype, (N, K), bias=bd)
+    torch.cuda.synchronize()
+    check(ref.cpu(), x, weight_bf16(raw, qtype, 0, N, K), bias=bias)
+    bits = ref.view(torch.int16)
+    as_rows = rd.view(N, -1)                                            # [N, bytes per row]
+    x3 = xd.view(1, rows, K)
+    x_strided = torch.empty((rows, 2 * K), dtype=torch.bfloat16, device="cuda")[:, ::2]
+    x_strided.copy_(xd)
+    b_strided = torch.empty(2 * N, dtype=torch.bfloat16, device="cuda")[::2]
+    b_strided.copy_(bd)
+    for what, y in (("2-D weight", fg.fused_linear(xd, as_rows, qtype, (N, K), bias=bd)),
+                    ("3-D activations", fg.fused_linear(x3, rd, qtype, (N, K), bias=bd)),
+                    ("strided activations", fg.fused_linear(x_strided, rd, qtype, (N, K), bias=bd)),
+                    ("strided bias", fg.fused_linear(xd, rd, qtype, (N, K), bias=b_strided))):
+        torch.cuda.synchronize()
+        assert y is not None, what
+        assert torch.equal(y.reshape(rows, N).view(torch.int16), bits), what
+    assert fg.fused_linear(x3, rd, qtype, (N, K), bias=bd).shape == (1, rows, N)
