@@ -531,6 +531,38 @@ __device__ __forceinline__ void sk_load(const uint8_t* b, int kq, SkRaw<QT>& w) 
     }
 }
 
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+
+// Q6_K's raw bytes of K-quarter kq through a buffer resource over the workgroup's weight rows, b = the super-block's
+// byte offset in it (2-byte aligned: 210-byte blocks). Each 8-byte piece is one 12-byte load from its aligned-down
+// dword, the 16 scale bytes one 16- and one 4-byte load (the 4 bytes are used only when the block starts 2 bytes
+// past a dword, and then end with it), d one 2-byte load at its place: the buffer's range check works per dword,
+// so a wider load of the last block's last bytes would read as zeros. Fewer load instructions than sk_load<14>,
+// whose many narrow loads (each touching 16 rows) kept the few-rows kernel's Q6_K waves waiting on the address unit.
+// Rows past N (past the resource's end) read as zeros.
+__device__ __forceinline__ uint2 ld8_rs(__amdgpu_buffer_rsrc_t r, uint32_t o) {
+    const uint32_t a = o & ~3u;
+    const u32x3 v = __builtin_bit_cast(u32x3, __builtin_amdgcn_raw_buffer_load_b96(r, a, 0, 0));
+    return funnel8(v[0], v[1], v[2], (o & 3u) * 8u);
+}
+
+__device__ __forceinline__ void sk_load_q6(__amdgpu_buffer_rsrc_t r, uint32_t b, int kq, SkRaw<14>& w) {
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int gp = 0; gp < 2; gp++) w.ql[2 * h + gp] = ld8_rs(r, b + 64 * h + 32 * gp + 8 * kq);
+#pragma unroll
+    for (int h = 0; h < 2; h++) w.qh[h] = ld8_rs(r, b + 128 + 32 * h + 8 * kq);
+    const uint32_t a = (b + 192) & ~3u, sh = ((b + 192) & 3u) * 8u;
+    const uint4 v = ld128(r, a);
+    const uint32_t t = ld32(r, a + 16);
+    w.sc[0] = __builtin_amdgcn_alignbit(v.y, v.x, sh);
+    w.sc[1] = __builtin_amdgcn_alignbit(v.z, v.y, sh);
+    w.sc[2] = __builtin_amdgcn_alignbit(v.w, v.z, sh);
+    w.sc[3] = __builtin_amdgcn_alignbit(t, v.w, sh);
+    w.d = __builtin_amdgcn_raw_buffer_load_b16(r, b + 208, 0, 0);
+}
+
 // the 8 values of stage g as a bf16x8 B fragment, the reference's rounding chain in MID
 template <int QT, int MID, int g>
 __device__ __forceinline__ bf16x8 sk_dequant(const SkRaw<QT>& w, int kq) {
@@ -619,6 +651,11 @@ __global__ __launch_bounds__(64 * NW) void gemm_gguf_skinny(const uint16_t* __re
     const uint8_t* wrow[NR];
 #pragma unroll
     for (int nr = 0; nr < NR; nr++) wrow[nr] = W + (int64_t)min(n0 + 16 * nr + r, N - 1) * row_bytes;
+    // Q6_K: the workgroup's rows through a buffer resource (rows past N read as zeros; their sums are not stored)
+    const __amdgpu_buffer_rsrc_t rw = tile_rsrc(W + (int64_t)n0 * row_bytes, (int64_t)min(16 * NR, N - n0) * row_bytes);
+    uint32_t rofs[NR];
+#pragma unroll
+    for (int nr = 0; nr < NR; nr++) rofs[nr] = (uint32_t)((16 * nr + r) * row_bytes);
     const uint16_t* xrow[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) xrow[mt] = X + (int64_t)min(16 * mt + r, M - 1) * K + 8 * kq;
@@ -630,7 +667,10 @@ __global__ __launch_bounds__(64 * NW) void gemm_gguf_skinny(const uint16_t* __re
     const int nsb = K / 256;
     auto load = [&](SkRaw<QT> (&w)[NR], int sb) {
 #pragma unroll
-        for (int nr = 0; nr < NR; nr++) sk_load<QT>(wrow[nr] + (int64_t)sb * TS, kq, w[nr]);
+        for (int nr = 0; nr < NR; nr++) {
+            if constexpr (QT == 14) sk_load_q6(rw, rofs[nr] + (uint32_t)sb * TS, kq, w[nr]);
+            else sk_load<QT>(wrow[nr] + (int64_t)sb * TS, kq, w[nr]);
+        }
     };
     // NR groups of 16 weight rows share each activation fragment (NR MFMAs per activation load)
     auto mfmas = [&](const bf16x8 (&bw)[NR], const bf16x8& ax, int mt) {
@@ -1133,12 +1173,12 @@ static void launch(const uint16_t* X, const uint8_t* W, const uint16_t* bias, ui
                    hipStream_t s) {
     // few rows: 32 weight rows per workgroup (two 16-row groups sharing each activation fragment)
     // Up to 8 rows the activations go one super-block ahead: 10-22 % faster than the per-stage reads (Wan shapes,
-    // cold weights); from 9 rows on, their 16 distinct rows per fragment make it slower. Q6_K's dequantisation takes
-    // more registers: its 16-row, 4-wave workgroups (twice as many) run 5-20 % faster than 32 rows over 8 waves on
-    // the Wan shapes, and twice as fast on 2048-4096 x 13824, where 32-row workgroups leave CUs idle.
-    if (M <= 8) {
-        if constexpr (QT == 14) launch_skinny<QT, MID, 1, 1, 4, true>(X, W, bias, Y, M, N, K, s);
-        else launch_skinny<QT, MID, 1, 2, 8, true>(X, W, bias, Y, M, N, K, s);
+    // cold weights); from 9 rows on, their 16 distinct rows per fragment make it slower. Q6_K keeps the per-stage
+    // reads at every row count: with its raw bytes through sk_load_q6 the 32-row, 8-wave form is the fastest one
+    // (Wan shapes at 1-8 rows, per layer: 18.4 / 34.8 / 39.1 us against 20.3 / 37.2 / 47.4 for the 16-row, 4-wave
+    // workgroups with activations ahead and the narrow loads).
+    if (M <= 8 && QT != 14) {
+        launch_skinny<QT, MID, 1, 2, 8, true>(X, W, bias, Y, M, N, K, s);
         return;
     }
     if (M <= 16) { launch_skinny<QT, MID, 1, 2, 8>(X, W, bias, Y, M, N, K, s); return; }

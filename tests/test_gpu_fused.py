@@ -99,11 +99,13 @@ def test_wan_block_shapes_sampled_rows(native, qtype, N, K):
 @pytest.mark.parametrize("mid", [0, 2])
 @pytest.mark.parametrize("M,N,K,with_bias", [(1, 300, 256, True), (5, 5120, 5120, False), (16, 61, 512, True),
                                              (17, 1000, 1024, False), (33, 300, 2048, True), (64, 5120, 512, False),
-                                             (48, 777, 1280, True), (65, 256, 768, False)])
+                                             (48, 777, 1280, True), (65, 256, 768, False),
+                                             (4, 777, 1280, False), (12, 777, 1280, True)])
 def test_few_rows_whole_output(native, qtype, mid, M, N, K, with_bias):
-    # up to 64 activation rows take the few-rows kernel (16 weight rows per workgroup, K split over its 8 waves,
+    # up to 64 activation rows take the few-rows kernel (32 weight rows per workgroup, K split over its 8 waves,
     # 1 to 4 row tiles of 16; K = 256 and 512 leave waves with no super-block); 65 rows the panel kernel: ragged M
-    # and N, every output element checked
+    # and N, every output element checked. 777 x 1280: the last workgroup's last weight row ends with a Q6_K block
+    # that starts on a dword (the buffer range check ends at that row)
     raw = encode.random_blocks(qtype, N * K // 256, seed=qtype * 7 + M, family="normal")
     g = torch.Generator().manual_seed(M * 31 + N)
     x = torch.randn((M, K), generator=g).to(torch.bfloat16)
