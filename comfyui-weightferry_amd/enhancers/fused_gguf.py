@@ -60,7 +60,9 @@ def _launch(x2, raw, q, n_out, k, b, y, mid):
 def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
     """y = x @ dequantize(W).T (+ bias) in one kernel, or None when this is not that case."""
     q = int(qtype) if qtype is not None else None
-    if q not in _FUSED_TYPES or not x.is_cuda or not data.is_cuda or x.dtype != torch.bfloat16:
+    if q not in _FUSED_TYPES or not x.is_cuda or data.device != x.device or x.dtype != torch.bfloat16:
+        return None                 # (one device: the kernel reads every operand on x's device)
+    if bias is not None and bias.device != x.device:
         return None
     n_out, k = int(oshape[0]), int(oshape[1])
     if x.shape[-1] != k or k % 256 or (bias is not None and (bias.dtype != torch.bfloat16 or bias.numel() != n_out)):

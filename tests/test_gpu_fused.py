@@ -290,3 +290,6 @@ def test_fused_linear_input_layouts(native, qtype, rows):
         assert y is not None, what
         assert torch.equal(y.reshape(rows, N).view(torch.int16), bits), what
     assert fg.fused_linear(x3, rd, qtype, (N, K), bias=bd).shape == (1, rows, N)
+    # operands off x's device are not the kernel's case (the two-step flow takes them)
+    assert fg.fused_linear(xd, rd, qtype, (N, K), bias=bias) is None
+    assert fg.fused_linear(xd, torch.from_numpy(raw), qtype, (N, K), bias=bd) is None
