@@ -94,7 +94,9 @@ def int8_linear(x, w_q, w_scale, bias=None, convrot=False):
     """The W8A8 linear of bf16 activations x [..., k]: dynamic per-row int8 activations (plain, or ConvRot),
     weight w_q int8 [n, k] with a float32 per-channel (or per-tensor) scale, exact int32 sums, output bf16
     [..., n]. None when this is not the kernels' case."""
-    if not x.is_cuda or x.dtype != torch.bfloat16 or w_q.dtype != torch.int8:
+    if not x.is_cuda or x.dtype != torch.bfloat16 or w_q.dtype != torch.int8 or w_q.device != x.device:
+        return None
+    if bias is not None and bias.device != x.device:
         return None
     k = x.shape[-1]
     mode = QUANT_MODES["convrot" if convrot else "plain"]
@@ -309,6 +311,8 @@ def _eligible_weight(x, weight, bias, cache):
         return None
     if not _CONVROT_GROUP <= k <= _QUANT_MAX_K[QUANT_MODES["convrot"]] or w_q.shape[1] != k:
         return None
+    if w_q.device != x.device:
+        return None                 # the kernels read the weight on x's device (the scales are moved there)
     return plain
 
 
