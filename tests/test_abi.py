@@ -94,3 +94,30 @@ def test_probe_is_a_separate_library_with_its_own_checks():
     assert probe.wfp_hbm_stream(p16 + 4, p16, 4, 1, 2, None) == -1
     assert probe.wfp_hbm_stream(p16, p16, 4, 3, 5, None) == -2
     assert b"3:5" in probe.wfp_last_error()
+
+
+def test_fused_gemm_workspace_sizes_without_gpu():
+    # wf_linear_gguf_workspace is host logic: which form takes a shape with a workspace, and how many float32 partial
+    # sums (or split counters) it needs -- the rules the library's header states
+    import ctypes as ct
+    native = sub("_native")
+    lib = native.lib()
+
+    def need(M, N, K):
+        v = ct.c_int64(-1)
+        assert lib.wf_linear_gguf_workspace(M, N, K, ct.byref(v)) == native.OK
+        return v.value
+    # 1-16 rows of a shallow or wide product: the few-rows kernel, no workspace
+    for M in (1, 8, 16):
+        assert need(M, 5120, 5120) == 0 and need(M, 13824, 5120) == 0
+    # up to 8 rows of a narrow deep product: the split form (16 KiB of counters, then the partial sums)
+    assert need(1, 2048, 8192) > 16384 and need(8, 2048, 8192) > need(1, 2048, 8192)
+    # 17-512 rows: the panel form's slices, S * M * N * 4 bytes with S >= 2 (the largest need over the formats)
+    for M, N, K in ((17, 5120, 5120), (32, 13824, 5120), (64, 5120, 13824), (128, 5120, 5120), (512, 13824, 5120)):
+        n = need(M, N, K)
+        assert n > 0 and n % (M * N * 4) == 0 and n // (M * N * 4) >= 2, (M, N, K, n)
+    # too shallow for two slices of two super-blocks, or past the panel form: nothing
+    assert need(128, 5120, 768) == 0 and need(513, 5120, 5120) == 0 and need(4096, 5120, 5120) == 0
+    # bad shapes are refused
+    v = ct.c_int64()
+    assert lib.wf_linear_gguf_workspace(4, 64, 300, ct.byref(v)) == native.EINVAL
