@@ -8,8 +8,8 @@
 // Two kernels:
 //  * gemm_i8_dl (K % 64 == 0, the workload): 256 x 320, 256 x 256, 256 x 128 or 128 x 160 tiles (chosen per
 //    shape, see launch_dl), operands streamed global -> LDS by the load unit (no register staging) through a
-//    4-stage ring of 64-byte K stages, and an epilogue that stages the rounded tile in LDS and stores whole 16-byte
-//    runs of output rows.
+//    4-stage ring of 64-byte K stages (128-byte for 128 x 160 tiles), and an epilogue that stages the rounded
+//    tile in LDS and stores whole 16-byte runs of output rows.
 //  * gemm_i8 (K % 16 == 0 otherwise): 2 x 2 waves, predicated loads staged through registers into a
 //    double-buffered LDS tile of 128-byte K stages. Rows are 8 chunks of 16 bytes; chunk c of row r sits at slot
 //    c ^ (((r >> 1) ^ ((r & 1) << 2)) & 7), conflict-free for stage writes and fragment reads.
@@ -183,7 +183,7 @@ __global__ __launch_bounds__(256) void gemm_i8(const int8_t* __restrict__ A, con
 }
 
 // ------------------------------------------------------------------------- K % 64 == 0: direct-to-LDS ring
-// VM x VN waves of WM x WN MFMA tiles, the operands streamed through a 4-stage LDS ring of 64-byte K stages. The
+// VM x VN waves of WM x WN MFMA tiles, the operands streamed through a 4-stage LDS ring of BK-byte K stages. The
 // loads go from global memory straight into LDS (buffer_load_dwordx4 ... lds: lane l of an instruction writes the 16
 // bytes at LDS slot l of a 1 KiB run, so the swizzle is applied on the global side -- lane l loads the chunk that
 // belongs in slot l), with no register staging and no LDS write instructions; rows past M or N read as zeros. When
@@ -191,11 +191,26 @@ __global__ __launch_bounds__(256) void gemm_i8(const int8_t* __restrict__ A, con
 // pad slots after the stage, so every wave issues (and waits for) the same count. Stage kt + 3 is issued
 // while stage kt is computed. The barrier at the top of stage kt certifies that stage kt + 1 has landed (every wave
 // waited for its own loads) and that stage kt - 1 is no longer read, so the wave can prefetch stage kt + 1's first
-// fragments during stage kt and never waits on LDS right after a barrier. Rows are 64 bytes = 4 chunks; chunk c
-// of row r sits at slot c ^ ((r >> 2) & 3), conflict-free for the 16 lanes that read 16 rows' same chunk.
+// fragments during stage kt and never waits on LDS right after a barrier. A stage row is BK bytes = BK / 16 chunks,
+// swizzled by row_swz so that the 16 lanes that read 16 rows' same chunk hit 16 different bank groups.
+//
+// BK = 64 (16 rows per load instruction) for every tiling; BK = 128 (8 rows of one whole 128-byte line each) for
+// the 128 x 160 tiling, whose 4 stages of 36 KiB fit the LDS. The vector memory return path (TD) pays per cache line
+// touched, so half-line row segments cost it as much as whole lines: at 1024 x 5120 it was 69 % busy at 26 % MFMA
+// busy with 64-byte stages, and 128-byte stages take that product from 39.3 to 33.3 us. The larger tilings hold 72
+// or 64 KiB per 128-byte stage, which leaves room for 2 stages only, and lost more to the shallower ring than they
+// gained (2048 x 5120: 62.3 against 73.0 us).
 constexpr int kDlBK = 64;
 
-template <int VM, int VN, int WM, int WN, int OUT, bool BIAS, bool RESID>
+// slot of chunk c in a stage row r of CH chunks: 4 chunks (64 bytes) c ^ ((r >> 2) & 3); 8 chunks (128 bytes) swz
+template <int CH>
+__device__ __forceinline__ int row_swz(int row, int chunk) {
+    static_assert(CH == 4 || CH == 8, "64- or 128-byte stage rows");
+    if constexpr (CH == 4) return swz4(row, chunk);
+    else return swz(row, chunk);
+}
+
+template <int VM, int VN, int WM, int WN, int OUT, bool BIAS, bool RESID, int BK>
 __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
                                                            const float* __restrict__ xs,
                                                            const float* __restrict__ ws,
@@ -203,7 +218,8 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
                                                            int M, int N, int K, Residual res) {
     constexpr int NT = 64 * VM * VN, NW = NT / 64;
     constexpr int BM = VM * WM * 32, BN = VN * WN * 32;
-    constexpr int AI = BM / 16, BI = BN / 16;             // 1 KiB load instructions per stage (16 rows each)
+    constexpr int CH = BK / 16, RPI = 64 / CH, KS = BK / 32;   // 16-byte chunks per row, rows per load, K steps
+    constexpr int AI = BM / RPI, BI = BN / RPI;           // 1 KiB load instructions per stage (RPI rows each)
     constexpr int IPW = (AI + BI + NW - 1) / NW;          // per wave; spare issues of the last waves fill pad slots
     constexpr int SLOTS = NW * IPW * 64;                  // 16-byte slots per stage, pad slots after the B rows
     static_assert(4 * SLOTS * 16 <= 160 * 1024, "the ring fits the LDS");
@@ -215,7 +231,7 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);     // wave-uniform: scalar load bases
     const int wm = wave / VN, wn = wave % VN;
-    const int nk = K / kDlBK;
+    const int nk = K / BK;
     const __amdgpu_buffer_rsrc_t ra = tile_rsrc(A + (int64_t)m0 * K, (int64_t)(M - m0) * K);
     const __amdgpu_buffer_rsrc_t rb = tile_rsrc(B + (int64_t)n0 * K, (int64_t)(N - n0) * K);
     // this wave's load instructions: global chunk run gi = wave * IPW + q (A rows for gi < AI, then B rows)
@@ -223,11 +239,11 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
 #pragma unroll
     for (int q = 0; q < IPW; q++) {
         const int gi = min(wave * IPW + q, AI + BI - 1);  // a pad issue repeats the last B run into its pad slot
-        const int r = (gi < AI ? gi : gi - AI) * 16 + (lane >> 2);
-        voff[q] = (uint32_t)(r * K + 16 * swz4(r, lane & 3));
+        const int r = (gi < AI ? gi : gi - AI) * RPI + lane / CH;
+        voff[q] = (uint32_t)(r * K + 16 * row_swz<CH>(r, lane % CH));
     }
     auto issue = [&](i32x4* st, int kt) {
-        const int k0 = kt * kDlBK;
+        const int k0 = kt * BK;
 #pragma unroll
         for (int q = 0; q < IPW; q++) {
             const int gi = wave * IPW + q;
@@ -235,18 +251,18 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
         }
     };
     const int lr = lane & 31, lk = lane >> 5;
-    int aslot[WM][2], bslot[WN][2];
+    int aslot[WM][KS], bslot[WN][KS];
 #pragma unroll
     for (int i = 0; i < WM; i++) {
         const int row = wm * WM * 32 + i * 32 + lr;
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) aslot[i][ks] = row * 4 + swz4(row, 2 * ks + lk);
+        for (int ks = 0; ks < KS; ks++) aslot[i][ks] = row * CH + row_swz<CH>(row, 2 * ks + lk);
     }
 #pragma unroll
     for (int j = 0; j < WN; j++) {
         const int row = wn * WN * 32 + j * 32 + lr;
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) bslot[j][ks] = BM * 4 + row * 4 + swz4(row, 2 * ks + lk);
+        for (int ks = 0; ks < KS; ks++) bslot[j][ks] = BM * CH + row * CH + row_swz<CH>(row, 2 * ks + lk);
     }
     i32x4 fa[2][WM], fb[2][WN];
     auto fread = [&](const i32x4* st, int ks, int set) {
@@ -283,10 +299,12 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
         wait_vm<IPW>();                                          // stage kt + 1 landed (kt + 2 may be in flight)
         wave_barrier_sync();
         issue(free_, kt + 3);
-        fread(cur, 1, 1);
-        mfmas(0);
-        fread(nxt, 0, 0);
-        mfmas(1);
+        static_for<KS>([&](auto ksc) {                          // K step ks computes from fragment set ks & 1
+            constexpr int ks = decltype(ksc)::value;
+            if constexpr (ks + 1 < KS) fread(cur, ks + 1, (ks + 1) & 1);
+            else fread(nxt, 0, 0);
+            mfmas(ks & 1);
+        });
     };
     int kt = 0;
     for (; kt + 4 <= nk; kt += 4) {
@@ -400,15 +418,16 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
 //   256 x 256: 8 waves of 4 x 2 MFMA tiles (128 x 64).
 //   256 x 128: 4 waves of 4 x 2 MFMA tiles, one per SIMD: more workgroups for small outputs.
 //   128 x 160: 4 waves of 1 x 5 MFMA tiles: 1024 x 5120 outputs make exactly 256 tiles (1.2 LDS fragment reads per
-//              MFMA against 0.75 for 4 x 2, but every CU busy: 42.7 against 50.9 us for the 256 x 128 tiling).
-template <int VM, int VN, int WM, int WN, int OUT>
+//              MFMA against 0.75 for 4 x 2, but every CU busy: 42.7 against 50.9 us for the 256 x 128 tiling);
+//              128-byte K stages where K % 128 == 0.
+template <int VM, int VN, int WM, int WN, int OUT, int BK = kDlBK>
 static void launch_dl_shape(const int8_t* A, const int8_t* B, const float* xs, const float* ws, const void* bias,
                             void* out, int M, int N, int K, Residual r, bool resid, hipStream_t s) {
     constexpr int BM = VM * WM * 32, BN = VN * WN * 32, NT = 64 * VM * VN;
     const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    if (resid) gemm_i8_dl<VM, VN, WM, WN, OUT, false, true><<<dim3(tiles), NT, 0, s>>>(A, B, xs, ws, nullptr, out, M, N, K, r);
-    else if (bias) gemm_i8_dl<VM, VN, WM, WN, OUT, true, false><<<dim3(tiles), NT, 0, s>>>(A, B, xs, ws, bias, out, M, N, K, r);
-    else gemm_i8_dl<VM, VN, WM, WN, OUT, false, false><<<dim3(tiles), NT, 0, s>>>(A, B, xs, ws, bias, out, M, N, K, r);
+    if (resid) gemm_i8_dl<VM, VN, WM, WN, OUT, false, true, BK><<<dim3(tiles), NT, 0, s>>>(A, B, xs, ws, nullptr, out, M, N, K, r);
+    else if (bias) gemm_i8_dl<VM, VN, WM, WN, OUT, true, false, BK><<<dim3(tiles), NT, 0, s>>>(A, B, xs, ws, bias, out, M, N, K, r);
+    else gemm_i8_dl<VM, VN, WM, WN, OUT, false, false, BK><<<dim3(tiles), NT, 0, s>>>(A, B, xs, ws, bias, out, M, N, K, r);
 }
 
 // modelled time of a tiling: whole rounds of 256 workgroups x tile area / relative efficiency (per mille)
@@ -423,7 +442,8 @@ static void launch_dl(const int8_t* A, const int8_t* B, const float* xs, const f
     const int64_t c320 = dl_cost(M, N, 256, 320, 1030), c256 = dl_cost(M, N, 256, 256, 1000);
     const int64_t c128 = dl_cost(M, N, 256, 128, 780), c160 = dl_cost(M, N, 128, 160, 581);
     const int64_t best = std::min(std::min(c320, c256), std::min(c128, c160));
-    if (c160 == best) launch_dl_shape<4, 1, 1, 5, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
+    if (c160 == best && K % 128 == 0) launch_dl_shape<4, 1, 1, 5, OUT, 128>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
+    else if (c160 == best) launch_dl_shape<4, 1, 1, 5, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
     else if (c128 == best) launch_dl_shape<2, 2, 4, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
     else if (c256 == best) launch_dl_shape<2, 4, 4, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
     else launch_dl_shape<4, 2, 2, 5, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
