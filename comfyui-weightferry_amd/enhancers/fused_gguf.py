@@ -60,7 +60,7 @@ def _launch(x2, raw, q, n_out, k, b, y, mid):
 def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
     """y = x @ dequantize(W).T (+ bias) in one kernel, or None when this is not that case."""
     q = int(qtype) if qtype is not None else None
-    if q not in _FUSED_TYPES or not x.is_cuda or data.device != x.device or x.dtype != torch.bfloat16:
+    if q not in _FUSED_TYPES or not x.is_cuda or x.dim() == 0 or data.device != x.device or x.dtype != torch.bfloat16:
         return None                 # (one device: the kernel reads every operand on x's device)
     if bias is not None and bias.device != x.device:
         return None

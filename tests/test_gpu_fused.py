@@ -293,3 +293,5 @@ def test_fused_linear_input_layouts(native, qtype, rows):
     # operands off x's device are not the kernel's case (the two-step flow takes them)
     assert fg.fused_linear(xd, rd, qtype, (N, K), bias=bias) is None
     assert fg.fused_linear(xd, torch.from_numpy(raw), qtype, (N, K), bias=bd) is None
+    # nor is a 0-dimensional x (no row of K values)
+    assert fg.fused_linear(xd[0, 0], rd, qtype, (N, K)) is None
