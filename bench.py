@@ -541,6 +541,42 @@ def formats_leg(torch, native, encode, steps, warmup):
     return res
 
 
+def _cpu_host(torch):
+    """Threads for the CPU legs and what the host is: torch takes every CPU this process may use -- os.cpu_count(),
+    bounded by the process's CPU affinity, its cgroup CPU quota and OMP_NUM_THREADS where the host sets one (a
+    shared host's statement of this process's CPU share; more threads than that share only contend). Returns the
+    fields each cpu_baseline record carries."""
+    nproc = os.cpu_count() or 1
+    share, why = nproc, ["os.cpu_count()"]
+    try:
+        aff = len(os.sched_getaffinity(0))
+        if aff < share:
+            share, why = aff, ["CPU affinity"]
+    except (AttributeError, OSError):
+        pass
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            q = max(1, -(-int(quota) // int(period)))
+            if q < share:
+                share, why = q, ["cgroup cpu.max"]
+    except (OSError, ValueError):
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and 0 < int(omp) < share:
+        share, why = int(omp), ["OMP_NUM_THREADS"]
+    torch.set_num_threads(share)
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cores": torch.get_num_threads(), "nproc": nproc, "threads_bound_by": why[0], "cpu_model": model}
+
+
 def cpu_baseline_dequant(torch, raw, qtype, rows, cols, budget_s=12.0):
     """The reference's CPU path (ComfyUI-GGUF's torch op chain, restated in oracle.torch_chain) on the first
     `rows` rows of one weight; GB/s with the same byte accounting as the GPU leg."""
@@ -549,8 +585,7 @@ def cpu_baseline_dequant(torch, raw, qtype, rows, cols, budget_s=12.0):
     per = torch_chain.BLOCK_SIZE[qtype]
     nbytes = rows * cols // per * ts
     sample = torch.from_numpy(raw[:nbytes].copy())
-    cores = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(cores)
+    host = _cpu_host(torch)
     for _ in range(2):
         torch_chain.dequantize(sample, qtype, (rows, cols), torch.float16, torch.bfloat16)
     times = []
@@ -562,10 +597,11 @@ def cpu_baseline_dequant(torch, raw, qtype, rows, cols, budget_s=12.0):
     times.sort()
     med = times[len(times) // 2]
     algo = nbytes + rows * cols * 2
-    return {"value": round(algo / med / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+    return {"value": round(algo / med / 1e9, 3), "unit": "GB/s", **host, "kind": "port",
             "sample": f"ComfyUI-GGUF torch op chain (oracle/torch_chain.py) on CPU, Q4_K -> bf16 (MID f16), "
-                      f"first {rows} rows of the 13824x5120 weight, median of {len(times)} runs"}
+                      f"first {rows} of the 13824 rows of the 13824x5120 weight ({nbytes} bytes in, "
+                      f"{rows * cols * 2} out; GB/s is size-independent for this streaming op), median of "
+                      f"{len(times)} runs"}
 
 
 def _cpu_median(fn, budget_s, runs=10):
@@ -586,14 +622,13 @@ def cpu_baselines(torch, encode):
     torch._int_mm with the scale epilogue for the int8 linear; the streamed forward has no CPU path in the reference,
     so its baseline is the CPU dequantisation + linear of one Wan block, extrapolated to 4096 tokens x 40 blocks."""
     from oracle import torch_chain
-    cores = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(cores)
+    host = _cpu_host(torch)
     res = {}
     # Q8_0, first 512 rows of the 5120 x 5120 weight
     raw = encode.encode_q8_0(encode.weights((512, 5120), seed=1234))
     t8 = torch.from_numpy(raw)
     med, n = _cpu_median(lambda: torch_chain.dequantize(t8, 8, (512, 5120), torch.float16, torch.bfloat16), 6.0)
-    res["q8_0_dequant"] = {"value": round((raw.size + 512 * 5120 * 2) / med / 1e9, 3), "unit": "GB/s", "cores": cores,
+    res["q8_0_dequant"] = {"value": round((raw.size + 512 * 5120 * 2) / med / 1e9, 3), "unit": "GB/s", **host,
                            "kind": "port", "sample": f"Q8_0 -> bf16 (MID f16), 512 rows x 5120, median of {n}"}
     # fused-GEMM row: Q5_K dequantisation of one 5120 x 5120 layer + bf16 F.linear at 64 tokens
     raw5 = torch.from_numpy(encode.random_blocks(13, 5120 * 5120 // 256, seed=1234))
@@ -604,7 +639,7 @@ def cpu_baselines(torch, encode):
         return torch_chain.linear_bf16(x, w)
     med, n = _cpu_median(layer, 8.0, 5)
     res["q5_k_dequant_plus_linear"] = {"value": round(2 * 64 * 5120 * 5120 / med / 1e12, 4), "unit": "TFLOPS",
-                                       "cores": cores, "kind": "port", "ms_per_layer": round(med * 1e3, 1),
+                                       **host, "kind": "port", "ms_per_layer": round(med * 1e3, 1),
                                        "sample": f"Q5_K 5120x5120 dequant + bf16 linear, 64 tokens, median of {n}"}
     # int8 W8A8 row: torch._int_mm + (acc * xs) * ws epilogue, 256 x 5120 by 5120 x 5120
     xq = torch.randint(-127, 128, (256, 5120), dtype=torch.int8)
@@ -616,7 +651,7 @@ def cpu_baselines(torch, encode):
         acc = torch._int_mm(xq, wqt)
         return ((acc.float() * xs[:, None]) * ws[None, :]).to(torch.bfloat16)
     med, n = _cpu_median(i8, 6.0)
-    res["int8_linear"] = {"value": round(2 * 256 * 5120 * 5120 / med / 1e12, 4), "unit": "TOPS", "cores": cores,
+    res["int8_linear"] = {"value": round(2 * 256 * 5120 * 5120 / med / 1e12, 4), "unit": "TOPS", **host,
                           "kind": "port", "sample": f"torch._int_mm 256x5120 by 5120x5120 + scale epilogue, median of {n}"}
     # streamed row: one Wan block's linears (Q4_K) on the CPU at 64 tokens -- eight 5120 x 5120 layers and two of
     # 13824 x 5120 elements (ffn up / down), timed once per shape on random blocks; the dequantisations (per call,
@@ -632,7 +667,7 @@ def cpu_baselines(torch, encode):
         t_mm += count * mm
     block_s = t_deq + t_mm * 4096 / 64
     res["streamed_block_linears"] = {"value": round(40 * block_s * 1e3, 0), "unit": "ms/step (extrapolated)",
-                                     "cores": cores, "kind": "port",
+                                     **host, "kind": "port",
                                      "sample": "one Wan block's 10 Q4_K linears on the CPU: dequantisation "
                                                f"{t_deq * 1e3:.0f} ms + bf16 GEMMs at 64 tokens {t_mm * 1e3:.0f} ms "
                                                "scaled to 4096 tokens, x 40 blocks (linears only; attention "

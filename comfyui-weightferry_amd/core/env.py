@@ -30,7 +30,8 @@ DEFAULTS = {
     "WEIGHTFERRY_CHUNK_BLOCK0": "1",       # "0": block 0 stays resident in chunk mode
     "WEIGHTFERRY_CHUNK_RECALIBRATE": None,  # "1": learn the call order again on every load
     "WEIGHTFERRY_CHUNK_LOG": None,         # "1": a log line per chunked forward
-    "WEIGHTFERRY_CHUNK_HOST_FENCE": "1",   # "0": chunk copies ordered by stream waits alone (no host-side waits)
+    # "0" is refused: chunk streaming always keeps its host-side fences (streaming/chunk_state.py)
+    "WEIGHTFERRY_CHUNK_HOST_FENCE": "1",
     "WEIGHTFERRY_OUTSIDE_LEAF": "1",       # "0": a layer called before any block starts the chunk pipeline
 }
 

@@ -191,6 +191,7 @@ class PersistentEntry:
         self.n_blocks, self.block_bytes = int(n_blocks), int(block_bytes)
         self.bin = os.path.join(directory, f"{_ENTRY_PREFIX}{self.key}.bin")
         self.json = self.bin[:-4] + ".json"
+        self._store = None
 
     def complete(self):
         """The metadata names this key and layout, and the data file holds every block (the last one's padding may
@@ -217,19 +218,24 @@ class PersistentEntry:
         return FileBlockSource(self.bin, [(i * stride, self.block_bytes) for i in range(self.n_blocks)])
 
     def open_store(self):
-        """A store writing the entry's data file; the old metadata goes first, so a write that stops part way
-        leaves an entry that is never read."""
+        """A store writing the entry's data under a name of its own (<data file>.<pid>_<n>.tmp). The committed data
+        file is never written in place: a process reading the entry meanwhile keeps its bytes, and two processes
+        writing the same entry each write their own file. A write that stops part way leaves its temporary file,
+        removed when the store is deleted (or, if the process died, by the next enforce_cap)."""
         os.makedirs(self.directory, exist_ok=True)
-        try:
-            os.remove(self.json)
-        except OSError:
-            pass
-        return DiskBlockStore(self.directory, self.block_bytes, self.n_blocks, path=self.bin, keep=True)
+        self._store = DiskBlockStore(self.directory, self.block_bytes, self.n_blocks,
+                                     path=f"{self.bin}.{os.getpid()}_{next(_COUNTER)}.tmp")
+        return self._store
 
     def commit(self, cap_bytes):
-        """Metadata last (the entry is complete from here on), then older entries beyond ``cap_bytes`` removed.
-        Returns the bytes removed."""
-        tmp = self.json + ".tmp"
+        """The written data file renamed over the entry's (atomic: readers see the old file or the new one, whole),
+        the metadata last (the entry is complete from here on), then older entries beyond ``cap_bytes`` removed.
+        The store then refers to the entry's data file and leaves it on the drive. Returns the bytes removed."""
+        store = self._store
+        store.finalize()
+        os.replace(store.path, self.bin)
+        store.path, store.keep = self.bin, True
+        tmp = f"{self.json}.{os.getpid()}_{next(_COUNTER)}.tmp"
         with open(tmp, "w", encoding="utf-8") as f:
             json.dump({"key": self.key, "blocks": self.n_blocks, "block_bytes": self.block_bytes,
                        "created": time.time()}, f)
@@ -250,6 +256,19 @@ def enforce_cap(directory, cap_bytes, keep_key=None):
     entries = {}
     for name in names:
         if not name.startswith(_ENTRY_PREFIX):
+            continue
+        if name.endswith(".tmp"):
+            # an entry being written (<name>.<pid>_<n>.tmp): its writer renames or removes it; one left by a process
+            # that no longer runs is removed here
+            try:
+                pid = int(name.rsplit(".", 2)[-2].split("_")[0])
+            except ValueError:
+                continue
+            if pid != os.getpid() and not _pid_alive(pid):
+                try:
+                    os.remove(os.path.join(directory, name))
+                except OSError:
+                    pass
             continue
         key = name[len(_ENTRY_PREFIX):].split(".", 1)[0]
         path = os.path.join(directory, name)

@@ -454,7 +454,7 @@ __global__ __launch_bounds__(512) void gemm_gguf_dl(const uint16_t* __restrict__
                 }
         }
         const int mp = mw + p * PR;
-        if ((N & 7) == 0) {
+        if ((N & 7) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0) {   // whole aligned 16-byte runs
 #pragma unroll
             for (int it = 0; it < PR * RUNS / 64; it++) {
                 const int q = it * 64 + lane, r = q / RUNS, c = q % RUNS;
@@ -1043,7 +1043,9 @@ __global__ __launch_bounds__(256) void gguf_panel_sum(const float* __restrict__ 
     const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i0 >= MN) return;
     float t[4];
-    if ((N & 3) == 0) {                               // then MN % 4 == 0 and every slice starts 16-byte aligned
+    // N % 4 == 0: MN % 4 == 0 and every slice starts 16-byte aligned; the four outputs go as one 8-byte store only
+    // when Y itself is 8-byte aligned (a caller's view may start at any element)
+    if ((N & 3) == 0 && (reinterpret_cast<uintptr_t>(Y) & 7) == 0) {
         float4 v = *reinterpret_cast<const float4*>(part + i0);
         t[0] = v.x; t[1] = v.y; t[2] = v.z; t[3] = v.w;
         for (int q = 1; q < S; q++) {
@@ -1379,8 +1381,11 @@ extern "C" int wf_linear_gguf_workspace(int64_t M, int64_t N, int64_t K, int64_t
     // the format is not known here: the largest need over them (Q6_K takes the panel form from 17 rows, and more
     // slices up to 128 rows)
     if (split_takes(M, N, K)) *bytes = split_plan(M, N, K).bytes();
-    else if (panel_takes_ws(M, N, K, 14))
-        *bytes = std::max(panel_plan(M, N, K, INT64_MAX, 12).part_bytes, panel_plan(M, N, K, INT64_MAX, 14).part_bytes);
+    else if (panel_takes_ws(M, N, K, 14)) {
+        const int64_t part = std::max(panel_plan(M, N, K, INT64_MAX, 12).part_bytes,
+                                      panel_plan(M, N, K, INT64_MAX, 14).part_bytes);
+        if (part > 0) *bytes = kSplitCounterBytes + part;   // the split form's counters stay untouched
+    }
     return WF_OK;
 }
 
@@ -1395,13 +1400,20 @@ extern "C" int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const
     const bool panel = !split_takes(M, N, K) && panel_takes_ws(M, N, K, qtype) &&
                        (panel_takes(M) || panel_plan(M, N, K, INT64_MAX, qtype).s > 1);
     if (panel) {
+        // the panel form's partial sums go past the split form's counters, which must stay zero between calls (one
+        // workspace serves calls of every shape and form on a stream)
         const PanelPlan p = panel_plan(M, N, K, INT64_MAX, qtype);
-        if (p.part_bytes > 0 && (!workspace || !aligned(workspace, 256) || workspace_bytes < p.part_bytes)) {
-            set_error("wf_linear_gguf_ws: a 256-byte aligned workspace of %lld bytes is needed (given %lld)",
-                      (long long)p.part_bytes, (long long)workspace_bytes);
-            return WF_EINVAL;
+        void* part = nullptr;
+        if (p.part_bytes > 0) {
+            const int64_t need = kSplitCounterBytes + p.part_bytes;
+            if (!workspace || !aligned(workspace, 256) || workspace_bytes < need) {
+                set_error("wf_linear_gguf_ws: a 256-byte aligned workspace of %lld bytes is needed (given %lld)",
+                          (long long)need, (long long)workspace_bytes);
+                return WF_EINVAL;
+            }
+            part = static_cast<uint8_t*>(workspace) + kSplitCounterBytes;
         }
-        run_gguf_panel(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, p, workspace, s);
+        run_gguf_panel(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, p, part, s);
     } else if (!split_takes(M, N, K)) {
         run_gguf(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, s);
     } else {
@@ -1468,15 +1480,17 @@ extern "C" int wf_linear_gguf_noalloc(const void* x_bf16, int64_t M, int64_t K, 
     hipStream_t s = static_cast<hipStream_t>(stream);
     // (up to 64 rows only when the scratch holds more than one slice: in one slice the few-rows kernel is faster)
     if (!split_takes(M, N, K) && panel_takes_ws(M, N, K, qtype) &&
-        (panel_takes(M) || panel_plan(M, N, K, kScratchBytes, qtype).s > 1)) {
+        (panel_takes(M) || panel_plan(M, N, K, kScratchBytes - kSplitCounterBytes, qtype).s > 1)) {
         // the panel form's partial sums in the scratch array, as many slices as fit there
-        const PanelPlan p = panel_plan(M, N, K, kScratchBytes, qtype);
-        void* ws = nullptr;
+        const PanelPlan p = panel_plan(M, N, K, kScratchBytes - kSplitCounterBytes, qtype);
+        void* part = nullptr;
         if (p.part_bytes > 0) {
+            void* ws = nullptr;
             const int src = scratch_address(&ws);
             if (src != WF_OK) return src;
+            part = static_cast<uint8_t*>(ws) + kSplitCounterBytes;
         }
-        run_gguf_panel(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, p, ws, s);
+        run_gguf_panel(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, p, part, s);
     } else if (!split_takes(M, N, K)) {
         run_gguf(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, s);
     } else {

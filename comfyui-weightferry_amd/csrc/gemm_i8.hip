@@ -358,7 +358,7 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
         const uint4* ov = reinterpret_cast<const uint4*>(ot);
         constexpr int RUNS = TC / 8;                       // 16-byte runs per row
         uint16_t* Y = static_cast<uint16_t*>(out);
-        if ((N & 7) == 0) {
+        if ((N & 7) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0) {   // whole aligned 16-byte runs
 #pragma unroll
             for (int it = 0; it < TR * RUNS / 64; it++) {
                 const int q = it * 64 + lane, r = q / RUNS, c = q % RUNS;

@@ -61,8 +61,39 @@ def _runs(js, specs, offsets):
     return runs, where, base
 
 
+def _pack(order, size_of, limit):
+    """Chunk types: ``order`` cut into consecutive runs of leaves, each run closed before the leaf that would take it
+    past ``limit`` bytes (a leaf larger than ``limit`` makes a run of its own)."""
+    cuts, filled = [0], 0
+    for i, leaf in enumerate(order):
+        if i > cuts[-1] and filled + size_of[leaf] > limit:
+            cuts.append(i)
+            filled = 0
+        filled += size_of[leaf]
+    cuts.append(len(order))
+    return [list(order[a:b]) for a, b in zip(cuts, cuts[1:])]
+
+
+def _stored_order(order_cache, leaves):
+    """The leaf call order an earlier load kept in ``order_cache``, when there is one that names only these blocks'
+    leaves and WEIGHTFERRY_CHUNK_RECALIBRATE=1 does not ask to learn it again; else None."""
+    if order_cache is None or _env.get("WEIGHTFERRY_CHUNK_RECALIBRATE") == "1":
+        return None
+    kept = order_cache.get("order") or ()
+    if not kept or any(leaf not in leaves for leaf in kept):
+        return None
+    return list(kept)
+
+
 class _ChunkState(_StreamState):
     """Per-model chunk streaming state (double-buffered, RAM tier)."""
+
+    # The host waits for the slot-free event before a unit's copy is issued and for the unit's copy event before its
+    # first leaf runs, besides the two stream waits. Required: with the stream waits alone, 40 Wan blocks streamed in
+    # 3 chunks each gave layers wrong bytes on MI355X (every forward on one machine, none on others), never with one
+    # hardware queue (GPU_MAX_HW_QUEUES=1) and never in the CPU model of the queues. The cause is not known. Only that
+    # CPU model (tests) clears this flag, to check the stream-wait ordering of the protocol by itself.
+    host_fence = True
 
     def __init__(self, owner, device, streaming_blocks, host_flats, host_views, rest, specs, offsets, chunk_bytes,
                  num_slots, order_cache=None, ring=None, disk_index=None, source=None):
@@ -103,11 +134,15 @@ class _ChunkState(_StreamState):
         self.blocks_started = 0
         self._fwd = None
         self._retired = []                # unit events replaced in this forward (closed once it has run)
-        # host-side fences on both cross-stream dependencies (see leaf_pre); WEIGHTFERRY_CHUNK_HOST_FENCE=0 leaves
-        # them to the stream waits alone
-        self.host_fence = _env.get("WEIGHTFERRY_CHUNK_HOST_FENCE") != "0"
-        if order_cache is not None:
-            self.use_learned_order(order_cache)
+        if _env.get("WEIGHTFERRY_CHUNK_HOST_FENCE") == "0":
+            raise ValueError("WEIGHTFERRY_CHUNK_HOST_FENCE=0 is not supported: chunk copies ordered by stream waits "
+                             "alone gave layers wrong bytes on MI355X, so the host-side fences always stay on")
+        kept = _stored_order(order_cache, self.leaf_params)
+        if kept is not None:
+            self.order = kept
+            self.finish_calibration()
+            log_info(f"DiT Layer Streaming [chunks]: {len(kept)} leaves in the stored call order; chunked from the "
+                     f"first forward.")
 
     # ---- helpers
     def _views(self, buf, where):
@@ -205,33 +240,14 @@ class _ChunkState(_StreamState):
             self._copy(s, self.leaf_plan[leaf][0], self.scratch, compute)
         self._bind(s, self.scratch_views[leaf])
 
-    def use_learned_order(self, order_cache):
-        """Take the call order an earlier load learned (order_cache["order"]): chunk types now, no calibration."""
-        order = order_cache.get("order")
-        if (not order or _env.get("WEIGHTFERRY_CHUNK_RECALIBRATE") == "1"
-                or not set(order) <= set(self.leaf_params)):
-            return False
-        self.order = list(order)
-        self.finish_calibration()
-        log_info("DiT Layer Streaming [chunks]: call order of an earlier load reused (no calibration pass).")
-        return True
-
     def finish_calibration(self):
         """Chunk types from the learned order (leaves never called go last, in registration order), their copy
-        plans, the slots and the events."""
-        if self.order_cache is not None and self.order:
+        plans, the slots and the events; the order is kept in ``order_cache`` for later loads."""
+        if self.order and self.order_cache is not None:
             self.order_cache["order"] = list(self.order)
-        order = list(self.order) + [leaf for leaf in self.leaf_params if leaf not in self.order]
-        types, cur, cur_bytes = [], [], 0
-        for leaf in order:
-            nb = self.leaf_bytes[leaf]
-            if cur and cur_bytes + nb > self.chunk_bytes:
-                types.append(cur)
-                cur, cur_bytes = [], 0
-            cur.append(leaf)
-            cur_bytes += nb
-        if cur:
-            types.append(cur)
+        called = set(self.order)
+        types = _pack(list(self.order) + [leaf for leaf in self.leaf_params if leaf not in called], self.leaf_bytes,
+                      self.chunk_bytes)
         self.types = types
         self.n_types = len(types)
         self.type_of_leaf = {leaf: t for t, leaves in enumerate(types) for leaf in leaves}
@@ -385,12 +401,8 @@ class _ChunkState(_StreamState):
             self._fwd["spares"] += 1
         views = (self.spares[self.u_spare[u]][2][t] if u in self.u_spare
                  else self.slot_type_views[u % self.n_chunk_slots][t])
-        # Host-side fences in both directions (here, and on the slot-free event before a copy is issued), besides
-        # the stream waits: with the two stream waits alone, 40 Wan blocks streamed in 3 chunks each gave layers
-        # wrong bytes on some machines (every forward on one, none on others), never with one hardware queue
-        # (GPU_MAX_HW_QUEUES=1, all commands in host order) and never in the CPU protocol model: the cross-queue
-        # ordering of a pending stream wait fails there. With the fences no cross-stream wait is ever pending. The
-        # host then runs at most the slots' depth ahead of the GPU; the copies stay ahead of the compute.
+        # the host-side fence on the copy (see host_fence): no cross-stream wait is ever pending when the compute
+        # stream waits; the host runs at most the slots' depth ahead of the GPU, and the copies stay ahead of compute
         if self.host_fence:
             self.unit_events[u].synchronize()
         _native.stream_wait(self.compute_stream(), self.unit_events[u])

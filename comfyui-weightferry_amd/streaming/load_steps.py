@@ -2,10 +2,12 @@
 slots and the state, and the forward hooks -- the reference's streaming/load_steps.py on the direct path
 (_capture_streamed_blocks :1152-1274, _build_state :719-766, _install_first_block_hook :315-337,
 _install_block_stream_hooks :451-522)."""
+import functools
 import time
 
 import torch
 
+from .. import _native
 from ..core import env as _env
 from ..core.tiers.pinned import PinnedHost
 from ..utils.logging import log_info
@@ -220,67 +222,80 @@ def _install_first_block_hook(dit, first_block, state, owner):
     state.handles.append(first_block.register_forward_pre_hook(first_block_pre_hook))
 
 
+class _SlotHooks:
+    """The per-block side of double buffering. Before streamed block s runs, the compute stream must not start it
+    until its bytes are in its slot: reissue its copy if a skipped block broke the chain of prefetches, wait for the
+    copy's event (on the host too, see ``_StreamState.host_fence``, then on the compute stream) and point the
+    block's parameters at the slot. After it runs, the slot is free once the compute stream passes this point: record
+    that, and start the copy of the block that takes the slot next (in this forward, or the next forward's first
+    blocks when this was the slot's last one). The single-buffer mode copies on the compute stream instead."""
+
+    def __init__(self, dit, state, owner):
+        self.dit, self.state, self.owner = dit, state, owner
+
+    def _ours(self):
+        return getattr(self.dit, _ACTIVE_ATTR, None) is self.owner
+
+    def _await_copy(self, s, compute, prof):
+        st = self.state
+        if not st.issued[s]:
+            st.issue_prefetch(s)
+        st.wait_transfer(s)
+        landed = st.transferred_events[s]
+        if prof is not None:
+            prof.record(s, "wait0", compute)     # before the host fence: the GPU's idle time counts as stall
+        if st.host_fence:
+            landed.synchronize()
+        _native.stream_wait(compute, landed)
+
+    def before(self, s, module, args):
+        if not self._ours():
+            return
+        st = self.state
+        tic = time.perf_counter()
+        prof, compute = st.profiler, st.compute_stream()
+        if prof is not None:
+            prof.mark(s, "cpu_pre_hook")
+        if st.is_double:
+            self._await_copy(s, compute, prof)
+        else:
+            if prof is not None:
+                prof.record(s, "wait0", compute)
+            st.materialize(s, 0, compute)
+        if prof is not None:
+            prof.record(s, "start", compute)
+        for param, view in zip(module.parameters(), st.slot_views[st.slot_of(s)]):
+            param.data = view
+        if prof is not None:
+            prof.add_cpu(time.perf_counter() - tic)
+
+    def after(self, s, module, args, output):
+        if not self._ours():
+            return
+        st = self.state
+        prof, compute = st.profiler, st.compute_stream()
+        if prof is not None:
+            prof.record(s, "end", compute)
+        if not st.is_double:
+            return
+        tic = time.perf_counter()
+        slot = st.slot_of(s)
+        st.computed_events[slot].record(compute)
+        heir = s + st.num_slots                  # the next block to use this slot
+        if heir >= st.num_stream:
+            st.wrap_prefetch(slot)
+        elif not st.issued[heir]:
+            st.issue_prefetch(heir)
+        if prof is not None:
+            prof.add_cpu(time.perf_counter() - tic)
+
+
 def _install_block_stream_hooks(dit, state, owner):
-    """Per streamed block a pre-hook (wait for its copy, bind the slot) and a post-hook (free the slot, issue the
-    copy of the block that takes it next)."""
-    def make_pre_hook(cur_s):
-        def stream_pre_hook(module, args):
-            if getattr(dit, _ACTIVE_ATTR, None) is not owner:
-                return
-            t0 = time.perf_counter()
-            prof = state.profiler
-            if prof is not None:
-                prof.mark(cur_s, "cpu_pre_hook")
-            compute = state.compute_stream()
-            slot_idx = state.slot_of(cur_s)
-            if state.is_double:
-                if not state.issued[cur_s]:
-                    state.issue_prefetch(cur_s)      # the prefetch chain was broken (a block was skipped)
-                state.wait_transfer(cur_s)
-                if prof is not None:
-                    prof.record(cur_s, "wait0", compute)   # before the host fence: the GPU's idle time counts as stall
-                if state.host_fence:
-                    state.transferred_events[cur_s].synchronize()
-                from .. import _native
-                _native.stream_wait(compute, state.transferred_events[cur_s])
-            else:
-                if prof is not None:
-                    prof.record(cur_s, "wait0", compute)
-                state.materialize(cur_s, 0, compute)
-            if prof is not None:
-                prof.record(cur_s, "start", compute)
-            for p, sv in zip(module.parameters(), state.slot_views[slot_idx]):
-                p.data = sv
-            if prof is not None:
-                prof.add_cpu(time.perf_counter() - t0)
-        return stream_pre_hook
-
-    def make_post_hook(cur_s):
-        def stream_post_hook(module, args, output):
-            if getattr(dit, _ACTIVE_ATTR, None) is not owner:
-                return
-            prof = state.profiler
-            compute = state.compute_stream()
-            if prof is not None:
-                prof.record(cur_s, "end", compute)
-            if not state.is_double:
-                return
-            t0 = time.perf_counter()
-            slot_idx = state.slot_of(cur_s)
-            state.computed_events[slot_idx].record(compute)
-            next_s = cur_s + state.num_slots
-            if next_s < state.num_stream:
-                if not state.issued[next_s]:
-                    state.issue_prefetch(next_s)
-            else:
-                state.wrap_prefetch(slot_idx)    # the slot's last block of this forward: the next forward's block
-            if prof is not None:
-                prof.add_cpu(time.perf_counter() - t0)
-        return stream_post_hook
-
-    for s_idx, blk in enumerate(state.streaming_blocks):
-        state.handles.append(blk.register_forward_pre_hook(make_pre_hook(s_idx)))
-        state.handles.append(blk.register_forward_hook(make_post_hook(s_idx)))
+    """Registers _SlotHooks.before / after on every streamed block."""
+    hooks = _SlotHooks(dit, state, owner)
+    for s, blk in enumerate(state.streaming_blocks):
+        state.handles.append(blk.register_forward_pre_hook(functools.partial(hooks.before, s)))
+        state.handles.append(blk.register_forward_hook(functools.partial(hooks.after, s)))
 
 
 def _install_resident_profile_hooks(dit, blocks, resident_idx, state, owner):

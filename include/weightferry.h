@@ -112,7 +112,8 @@ int wf_linear_gguf(const void* x_bf16, int64_t M, int64_t K, const void* wq, int
  * by later calls of any shape on the same stream; calls that overlap on one workspace race). With 33-512 rows,
  * and with 17-32 rows of Q6_K or of a deep product (K >= 2 N), the panel form splits K into slices (at least two
  * super-blocks each), enough to give the chip 256 workgroups: each slice writes float32 partial sums into the
- * workspace (S * M * N * 4 bytes, no counters) and a second kernel adds them in slice order; up to 64 rows only when
+ * workspace past the split form's 16 KiB of counters, which it leaves untouched (16 KiB + S * M * N * 4 bytes), and a
+ * second kernel adds them in slice order; up to 64 rows only when
  * K gives more than one slice. wf_linear_gguf_workspace does not know the format and gives the largest need over
  * them (the panel form's bytes from 17 rows). Any other shape does not use the workspace (workspace may be NULL) and
  * is wf_linear_gguf. */
@@ -126,7 +127,8 @@ int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const void* wq, 
  * forbid hipMalloc). The split form's counters and partial sums live in a 16 MiB array the library holds on each GPU
  * it runs on until the process ends; the counters are cleared by a small kernel on `stream` at the start of each call
  * (no memset). A shape that needs more than 16 MiB there returns WF_EUNSUPPORTED with a message. The panel form
- * (the rows of wf_linear_gguf_ws) takes as many K slices as fit the array (one, and no scratch, at worst; up to 64
+ * (the rows of wf_linear_gguf_ws) takes as many K slices as fit the array past the counters (one, and no scratch, at
+ * worst; up to 64
  * rows one slice leaves the call to the few-rows kernel). Every call on a GPU shares
  * that GPU's array: calls that overlap on one GPU (on different streams or threads) race. */
 int wf_linear_gguf_noalloc(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes, int qtype,

@@ -197,6 +197,17 @@ def test_order_cache_skips_calibration(fake, monkeypatch):
     assert sm3.state.calibrating
 
 
+def test_stream_waits_alone_are_refused(fake, monkeypatch):
+    # the host-side fences are part of the design: the setting that turned them off is refused, not obeyed
+    dn = sub("streaming.dit_node")
+    monkeypatch.setenv("WEIGHTFERRY_CHUNK_HOST_FENCE", "0")
+    with pytest.raises(ValueError, match="HOST_FENCE"):
+        dn.apply_streaming(Model(3, []), device="cpu", pin_memory=False, chunk=True, chunk_bytes=512, chunk_slots=2)
+    monkeypatch.setenv("WEIGHTFERRY_CHUNK_HOST_FENCE", "1")
+    sm = dn.apply_streaming(Model(3, []), device="cpu", pin_memory=False, chunk=True, chunk_bytes=512, chunk_slots=2)
+    assert sm.state.host_fence
+
+
 def test_chunk_types_cut_by_bytes():
     chunk = sub("streaming.chunk_state")
     specs = [((64,), torch.float32)] * 3 + [((1000,), torch.float32)]
@@ -282,7 +293,7 @@ def test_ssd_tier_chunks_come_out_of_the_ring(ring, monkeypatch, tmp_path, fence
     # 6 streamed blocks, some on the SSD tier (a cache file of their captured bytes): the calibration forward and
     # the chunked ones copy their units out of the ring's buffers; every layer sees its own bytes, with or without
     # the host fences, and the ring serves each SSD-tier block once per forward
-    monkeypatch.setenv("WEIGHTFERRY_CHUNK_HOST_FENCE", fence)
+    monkeypatch.setattr(sub("streaming.chunk_state")._ChunkState, "host_fence", fence == "1")
     dn = sub("streaming.dit_node")
     seen = []
     model = Model(6, seen)
@@ -408,7 +419,7 @@ def test_host_far_ahead_of_the_gpu(monkeypatch, tmp_path, blocks, slots, chunk_k
     # the whole forward is enqueued before anything runs (without the host fences: nothing runs until the forward's
     # end); every layer must still read its own bytes -- with SSD-tier blocks too, whose ring buffers are refilled
     # as soon as the copies queued out of them have run
-    monkeypatch.setenv("WEIGHTFERRY_CHUNK_HOST_FENCE", fence)
+    monkeypatch.setattr(sub("streaming.chunk_state")._ChunkState, "host_fence", fence == "1")
     fn = DeferredFake()
     FakeRing.fn, FakeRing.made = fn, []
     monkeypatch.setattr(sub("core.tiers.sources"), "DiskRing", FakeRing)

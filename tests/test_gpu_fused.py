@@ -234,14 +234,35 @@ def test_panel_whole_output(native, qtype, M, N, K, with_bias, mid):
     check(y2, x, w, bias=bias)
     nsb = K // 256
     assert (need > 0) == (nsb >= 4)                  # two super-blocks per slice at least
-    if need:
-        assert need % (M * N * 4) == 0 and need // (M * N * 4) >= 2
+    if need:                                         # the split form's 16 KiB of counters, then the slices
+        part = need - 16384
+        assert part % (M * N * 4) == 0 and part // (M * N * 4) >= 2
     if not need or (M <= 32 and qtype != 14 and K < 2 * N):
         assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))     # the same form, the same slices
     y3 = noalloc(native, xd, rd, qtype, N, bias=bd, mid=mid)
     if need <= 16 << 20:
         assert torch.equal(y3.view(torch.int16), y2.view(torch.int16))
     check(y3, x, w, bias=bias)
+
+
+def test_panel_then_split_share_one_workspace(native):
+    # one workspace per stream serves every shape: a panel call in K slices leaves the split form's counters at zero,
+    # so a split call after it on the same workspace still finds its last workgroup and writes every output
+    qtype = 12
+    g = torch.Generator().manual_seed(11)
+    xp = torch.randn((128, 2048), generator=g).to(torch.bfloat16)
+    rp = encode.random_blocks(qtype, 256 * 2048 // 256, seed=5, family="normal")
+    xs = torch.randn((4, 8192), generator=g).to(torch.bfloat16)
+    rs = encode.random_blocks(qtype, 512 * 8192 // 256, seed=6, family="normal")
+    ws = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    yp, ws, need_p = fused_ws(native, xp.cuda(), torch.from_numpy(rp).cuda(), qtype, 256, ws=ws)
+    assert need_p > 16384                            # the panel form in slices, with partial sums
+    assert not ws[:16384].any()
+    ys, ws, need_s = fused_ws(native, xs.cuda(), torch.from_numpy(rs).cuda(), qtype, 512, ws=ws)
+    assert need_s > 0                                # the split form
+    check(yp, xp, weight_bf16(rp, qtype, 0, 256, 2048))
+    check(ys, xs, weight_bf16(rs, qtype, 0, 512, 8192))
+    assert not ws[:16384].any()
 
 
 def test_panel_workspace_is_checked(native):

@@ -119,10 +119,47 @@ def test_persistent_entry_is_complete_only_after_commit(tmp_path):
     with open(e.bin, "r+b") as f:                                                # a data file cut short
         f.truncate(2 * 8192)
     assert not e.complete()
-    # opening the store again removes the metadata first
+    # a rewrite goes to a file of its own: the committed data file is not cut while another process may read it, and
+    # a rewrite abandoned part way removes its file and leaves the entry as it was
     e2 = cf.PersistentEntry(str(tmp_path), "k1", 3, 5000)
-    e2.open_store().delete()
-    assert not os.path.exists(e2.json)
+    size = os.path.getsize(e.bin)
+    st2 = e2.open_store()
+    assert st2.path != e.bin and os.path.getsize(e.bin) == size
+    st2.write_block(0, torch.full((5000,), 9, dtype=torch.uint8))
+    tmp_file = st2.path
+    st2.delete()
+    assert not os.path.exists(tmp_file) and os.path.getsize(e.bin) == size and os.path.exists(e.json)
+
+
+def test_two_writers_of_one_entry(tmp_path):
+    # two loads miss the same entry and both write it: each writes its own file and renames it into place, so a
+    # reader that opened the first commit's file keeps whole bytes, and the entry is complete after either commit
+    a = cf.PersistentEntry(str(tmp_path), "k2", 2, 5000)
+    b = cf.PersistentEntry(str(tmp_path), "k2", 2, 5000)
+    sa, sb = a.open_store(), b.open_store()
+    for st in (sa, sb):
+        for i in range(2):
+            st.write_block(i, torch.full((5000,), i + 1, dtype=torch.uint8))
+    a.commit(cap_bytes=1 << 30)
+    assert a.complete() and sa.path == a.bin
+    reader = open(a.bin, "rb")
+    b.commit(cap_bytes=1 << 30)
+    assert b.complete()
+    reader.seek(8192)                                                            # block 1 (4 KiB stride)
+    assert reader.read(5000) == bytes([2]) * 5000
+    reader.close()
+    sa.delete()
+    sb.delete()
+    assert os.path.exists(a.bin) and not [n for n in os.listdir(tmp_path) if n.endswith(".tmp")]
+
+
+def test_cap_removes_a_dead_writers_file(tmp_path):
+    live = tmp_path / f"dit_persist_k3.bin.{os.getpid()}_0.tmp"
+    dead = tmp_path / "dit_persist_k4.bin.999999999_0.tmp"
+    for f in (live, dead):
+        f.write_bytes(b"\0" * 100)
+    cf.enforce_cap(str(tmp_path), 0)
+    assert live.exists() and not dead.exists()
 
 
 def _entry(d, key, nbytes, used):
