@@ -1,299 +1,301 @@
 """The int8 path's caller inside ComfyUI's Cosmos-Predict2 / Anima DiT block (comfy/ldm/cosmos/predict2.py).
 
-With int8 ConvRot weights, a block's three sub-layers (self-attention, cross-attention, MLP) each start from
-``LayerNorm(x) * (1 + scale) + shift`` and end with ``x + gate * out``. ComfyUI writes every one of those
-intermediate tensors and then quantises the projections' inputs one projection at a time. Installed, this module
-replaces ``Block.forward``, ``Attention.compute_qkv`` and ``GPT2FeedForward.forward`` with versions that route the
-block's int8 linears through ``fused_int8``:
+ComfyUI's ``Block.forward`` runs three sub-layers (self-attention, cross-attention, MLP). Each one reads
+``LayerNorm(x) * (1 + scale) + shift`` and adds ``gate * out`` to the residual stream ``x``; every intermediate is a
+tensor in HBM, and each int8 projection quantises its own input. Installed, this module replaces ``Block.forward``,
+``Attention.compute_qkv`` and ``GPT2FeedForward.forward`` so that the block's int8 linears go through ``fused_int8``
+with these parts (``WEIGHTFERRY_FUSED_BLOCK``: "1" all, "0" none, or a comma-separated list):
 
-* ``qkv``  -- the self-attention's q, k and v projections quantise their common input once;
-* ``modq`` -- the scale-and-shift is left pending and the input projections' quantiser applies it;
-* ``ln``   -- the LayerNorm before it as well (widths that are powers of two and multiples of 512);
-* ``gelu`` -- the MLP's GELU is left pending for its second layer's quantiser;
+* ``qkv``  -- q, k and v of the self-attention share one quantisation of their common input;
+* ``modq`` -- the scale-and-shift is not computed: the input projections' quantiser applies it;
+* ``ln``   -- the LayerNorm before it is not computed either (needs ``modq``; widths that are powers of two and
+  multiples of 512);
+* ``gelu`` -- the MLP's GELU is applied by its second layer's quantiser;
 * ``res``  -- ``x + gate * out`` is computed in the output projection's GEMM epilogue.
 
-Every part checks its preconditions per call and otherwise leaves ComfyUI's computation in place: a pending
-operation no layer took is computed the plain way, a residual no epilogue added is added with ``torch.addcmul``.
-The parts and their order of operations are those of the reference's fused block (enhancers/fused_block.py:
-320-345,424-524,589-700); its element-wise Triton kernels, SageAttention and TaylorSeer parts are not part of this
-path. ``WEIGHTFERRY_FUSED_BLOCK`` selects the parts ("1": all, "0": none, or a comma-separated list).
+Every part is checked per call and steps aside when its case is not met, so the block then computes what ComfyUI
+computes: an input no projection took is computed the plain way and the sub-layer is run again on it, a residual no
+epilogue added is added with ComfyUI's ``torch.addcmul``. The reference's fused block
+(enhancers/fused_block.py:424-735) has the same parts for this path; its Triton element-wise kernels,
+SageAttention and TaylorSeer parts are outside it.
 """
+import weakref
+from collections import namedtuple
+
 import torch
 
 from ..core import env as _env
 from ..utils.logging import log_info, log_warn
-from .fused_int8 import (_clear_pre, _int8_proj_ok, _materialise, _Overrides, _residual_forward, _set_pre)
+from .fused_int8 import _clear_pre, _int8_proj_ok, _Overrides, _residual_forward, _set_pre
 from .fused_state import _count, _state, _tls
 
 PARTS = ("qkv", "modq", "ln", "gelu", "res")
-_MERGE_GATES = None   # None: WEIGHTFERRY_CFG_RESID_MERGE decides per block; True / False force it
+_MERGE_GATES = None   # None: WEIGHTFERRY_CFG_RESID_MERGE decides per forward; True / False force it
+_PENDING_PART = {"lnmod": "ln", "mod": "modq", "gelu": "gelu"}
 
 
 def wanted_parts():
-    """The parts WEIGHTFERRY_FUSED_BLOCK asks for: all for "1" / "on" / "all" / unset, none for "0" / "off",
-    else the listed ones."""
+    """The parts WEIGHTFERRY_FUSED_BLOCK names: every part for "1" / "on" / "true" / "all" or when unset, none for
+    "0" / "off" / "false", else the listed ones (in PARTS order; unknown names are ignored)."""
     flag = (_env.get("WEIGHTFERRY_FUSED_BLOCK") or "1").strip().lower()
     if flag in ("", "0", "off", "false"):
         return ()
     if flag in ("1", "on", "true", "all"):
         return PARTS
-    asked = [p.strip() for p in flag.split(",")]
-    return tuple(p for p in PARTS if p in asked)
+    named = {p.strip() for p in flag.split(",")}
+    return tuple(p for p in PARTS if p in named)
 
 
-def _on(part):
-    return part in _state["parts"]
+def _on(*parts):
+    return all(p in _state["parts"] for p in parts)
+
+
+# ------------------------------------------------------------------------------------------ eligibility
+def _unpatched(module, *methods):
+    """No instance-level override of ``methods`` on ``module`` (another node's patch would see our tensors)."""
+    return not any(m in module.__dict__ for m in methods)
+
+
+def _bf16_cuda(t):
+    return t.dtype == torch.bfloat16 and t.is_cuda and t.is_contiguous()
+
+
+def _plain_layernorm(norm, width):
+    """ComfyUI's LayerNorm over the last dimension with no affine parameters and nothing for its cast path to apply,
+    at a width the quantiser's LayerNorm splits into rows as PyTorch's kernel does (a power of two, a multiple of
+    512)."""
+    return (isinstance(norm, torch.nn.LayerNorm) and _unpatched(norm, "forward")
+            and norm.weight is None and norm.bias is None and tuple(norm.normalized_shape) == (width,)
+            and width % 512 == 0 and width & (width - 1) == 0
+            and not getattr(norm, "weight_function", ()) and not getattr(norm, "bias_function", ()))
+
+
+class _BlockCall:
+    """What one call of the block may fuse, settled once per call. A pending input needs the qkv and modq parts, no
+    transformer patches (they would see the normalised input), a bf16 block, ComfyUI's own attention and MLP
+    methods, and every input projection -- self-attention q / k / v, cross-attention q, MLP layer1 -- a plain int8
+    linear; the same facts decide the residual epilogue's part of it."""
+
+    def __init__(self, block, transformer_options, compute_dtype, residual_dtype):
+        self.patched = bool((transformer_options or {}).get("patches"))
+        self.compute_dtype, self.residual_dtype = compute_dtype, residual_dtype
+        sa, ca, mlp = block.self_attn, block.cross_attn, block.mlp
+        self.pending = (_on("qkv", "modq") and not self.patched and compute_dtype == torch.bfloat16
+                        and _unpatched(sa, "forward", "compute_qkv") and _unpatched(ca, "forward", "compute_qkv")
+                        and _unpatched(mlp, "forward")
+                        and all(_int8_proj_ok(p) for p in (sa.q_proj, sa.k_proj, sa.v_proj, ca.q_proj, mlp.layer1)))
+        self.same_gate = False
+
+    def input_forms(self, norm, x, scale, shift):
+        """The sub-layer's input in the forms to try, best first, as (pending kind or None, tensor the module
+        receives): x with LayerNorm and scale-and-shift pending, norm(x) with the scale-and-shift pending, and the
+        real input. norm(x) is computed only when the first form is not taken."""
+        if self.pending and _on("ln") and _bf16_cuda(x) and _plain_layernorm(norm, x.shape[-1]):
+            yield "lnmod", x
+        normed = norm(x)
+        if self.pending and _bf16_cuda(normed):
+            yield "mod", normed
+        yield None, normed * (1 + scale) + shift
+
+    def epilogue_ok(self, out_proj, x):
+        return (_on("res") and not self.patched and out_proj is not None and _int8_proj_ok(out_proj)
+                and x.dtype == self.compute_dtype)
 
 
 # -------------------------------------------------------------------------------------------- sub-layers
-class _Call:
-    """Facts of one block call that every sub-layer consults."""
-
-    def __init__(self, block, transformer_options, compute_dtype, residual_dtype):
-        self.block = block
-        self.patched = bool((transformer_options or {}).get("patches"))
-        self.compute_dtype = compute_dtype
-        self.residual_dtype = residual_dtype
-
-    def pending_allowed(self, tensor):
-        """An input projection may take a pending scale-and-shift: modq and qkv on, no patches that would see
-        the normalised input, bf16 all through, and every input projection of the block a plain int8 linear
-        (enhancers/fused_block.py:489-502)."""
-        if not (_on("modq") and _on("qkv")) or self.patched:
-            return False
-        if tensor.dtype != torch.bfloat16 or self.compute_dtype != torch.bfloat16:
-            return False
-        if not (tensor.is_cuda and tensor.is_contiguous()):
-            return False
-        blk = self.block
-        sa, ca, mlp = blk.self_attn, blk.cross_attn, blk.mlp
-        if any("forward" in m.__dict__ or "compute_qkv" in m.__dict__ for m in (sa, ca)) or "forward" in mlp.__dict__:
-            return False
-        return all(_int8_proj_ok(lin) for lin in (sa.q_proj, sa.k_proj, sa.v_proj, ca.q_proj, mlp.layer1))
-
-    def norm_allowed(self, norm, x):
-        """The LayerNorm may go into the quantiser: ComfyUI's LayerNorm without affine parameters and without
-        cast functions, over the last dimension of a contiguous bf16 CUDA input whose width is a multiple of 512
-        and a power of two (enhancers/fused_block.py:505-520)."""
-        width = x.shape[-1]
-        return (_on("ln") and isinstance(norm, torch.nn.LayerNorm) and "forward" not in norm.__dict__
-                and norm.weight is None and norm.bias is None and len(norm.normalized_shape) == 1
-                and width == norm.normalized_shape[0] and width % 512 == 0 and not width & (width - 1)
-                and x.dtype == torch.bfloat16 and x.is_cuda and x.is_contiguous()
-                and not getattr(norm, "weight_function", ()) and not getattr(norm, "bias_function", ()))
+# One sub-layer of the block as data: its LayerNorm and modulation, ``run`` (the module on an input, reshaped back
+# to the residual's layout), the projection that may add the residual, and input projections outside
+# compute_qkv's shared quantisation that should take the pending input.
+_Sub = namedtuple("_Sub", "module norm shift scale gate run out_proj shared")
 
 
-def _modulate(normed, scale, shift):
-    """ComfyUI's scale-and-shift of a normalised input: normed * (1 + scale) + shift."""
-    return normed * (1 + scale) + shift
+def _with_epilogue(call, sub, x, inp):
+    """sub.run(inp) with the sub's int8 projections computing through fused_int8, and ``x + gate * out`` left
+    pending for the output projection's epilogue when allowed. Returns (out, whether the residual was added)."""
+    res = None
+    layers = list(sub.shared)
+    if call.epilogue_ok(sub.out_proj, x):
+        res = {"x": x, "gate": sub.gate, "done": False, "same": call.same_gate}
+        layers.append((sub.out_proj, _residual_forward))
+    _tls.res = res
+    try:
+        with _Overrides(layers):
+            out = sub.run(inp)
+    finally:
+        _tls.res = None
+    return out, res is not None and res["done"]
 
 
-def _run_sublayer(call, module, norm_and_x, scale, shift, fn, x_res, gate, out_layer, overrides=()):
-    """fn(input) for one sub-layer whose input is ``norm(x) * (1 + scale) + shift`` (norm_and_x = (norm, x)):
-    with that input left pending for the input projections' quantiser when allowed (LayerNorm included when
-    allowed), and with ``x_res + gate * out`` inside out_layer's GEMM when allowed. Returns (out, residual added).
-    A pending input no layer took is computed the plain way and the sub-layer runs again on it
-    (enhancers/fused_block.py:523-567)."""
-    with_res = (_on("res") and out_layer is not None and _int8_proj_ok(out_layer) and x_res is not None
-                and x_res.dtype == call.compute_dtype and not call.patched)
-
-    def run(inp):
-        res = {"x": x_res, "gate": gate, "done": False, "same": getattr(_tls, "same_gate", False)} if with_res \
-            else None
-        _tls.res = res
+def _step(call, sub, x):
+    """The residual stream after one sub-layer: the first input form some projection takes (an untaken pending
+    form is counted as a fallback of its part and the next form tried), then the residual added in the epilogue
+    or by ComfyUI's addcmul."""
+    for kind, inp in call.input_forms(sub.norm, x, sub.scale, sub.shift):
+        if kind is None:
+            out, added = _with_epilogue(call, sub, x, inp)
+            break
+        pend = _set_pre(inp, kind, sub.scale, sub.shift, norm=sub.norm if kind == "lnmod" else None)
         try:
-            with _Overrides(list(overrides) + ([(out_layer, _residual_forward)] if with_res else [])):
-                out = fn(inp)
-        finally:
-            _tls.res = None
-        return out, bool(res is not None and res["done"])
-
-    norm, x = norm_and_x
-    if call.norm_allowed(norm, x) and call.pending_allowed(x):
-        pre = _set_pre(x, "lnmod", scale, shift, norm=norm)
-        try:
-            got = run(x)
+            out, added = _with_epilogue(call, sub, x, inp)
         finally:
             _clear_pre()
-        if pre.used:
-            return got
-        _count("ln", False, f"{type(module).__name__} did not take the pending input")
-    normed = norm(x)
-    if call.pending_allowed(normed):
-        pre = _set_pre(normed, "mod", scale, shift)
-        try:
-            got = run(normed)
-        finally:
-            _clear_pre()
-        if pre.used:
-            return got
-        _count("modq", False, f"{type(module).__name__} did not take the pending input")
-    return run(_modulate(normed, scale, shift))
-
-
-def _join_residual(x_res, gate, out, added, residual_dtype):
-    """The residual stream after a sub-layer: ``out`` itself when its GEMM already added x_res + gate * out,
-    else ComfyUI's addcmul."""
+        if pend.used:
+            break
+        _count(_PENDING_PART[kind], False, f"{type(sub.module).__name__} did not take the pending input")
     if added:
         return out
-    return torch.addcmul(x_res, gate.to(residual_dtype), out.to(residual_dtype))
+    rd = call.residual_dtype
+    return torch.addcmul(x, sub.gate.to(rd), out.to(rd))
 
 
-def _gates_equal(emb, lora):
-    """Whether every (batch, frame) row of the block's modulation input is the same (classifier-free guidance
-    batches share the timestep), so every gate row is: the residual epilogue then runs once over all rows with
-    one gate row. One host sync per forward; cached on the embedding, which every block of a forward receives."""
-    hit = getattr(emb, "_weightferry_rows_same", None)
-    if hit is not None and hit[0] is lora:
-        return hit[1]
+def _equal_gate_rows(emb, lora):
+    """WEIGHTFERRY_CFG_RESID_MERGE: whether every (batch, frame) row of the modulation input -- timestep embedding
+    and AdaLN-LoRA term -- is the same, so that every gate row is (classifier-free guidance batches share the
+    timestep) and the residual epilogue can run once over all rows with one gate row. One device-to-host sync per
+    forward: the answer is kept for the embedding object ComfyUI hands to every block, through weak references, so
+    a later tensor at the same address is never taken for it."""
+    memo = getattr(_tls, "gate_rows", None)
+    if memo is not None and memo[0]() is emb and (memo[1]() if memo[1] is not None else None) is lora:
+        return memo[2]
 
-    def rows_equal(t):
-        return t is None or (t.dim() == 3 and bool(torch.equal(t, t[:1, :1].expand_as(t))))
-    same = emb.dim() == 3 and emb.shape[0] * emb.shape[1] > 1 and rows_equal(emb) and rows_equal(lora)
-    try:
-        emb._weightferry_rows_same = (lora, same)
-    except Exception:  # noqa: BLE001 -- an object that takes no attributes: checked again next block
-        pass
+    def uniform(t):
+        if t is None:
+            return True
+        return t.dim() == 3 and bool((t == t[:1, :1]).all())
+    same = emb.dim() == 3 and emb.shape[0] * emb.shape[1] > 1 and uniform(emb) and uniform(lora)
+    _tls.gate_rows = (weakref.ref(emb), weakref.ref(lora) if lora is not None else None, same)
     return same
 
 
-# ------------------------------------------------------------------------------------------- the patched methods
+# ------------------------------------------------------------------------------------- the patched methods
 def _block_forward(self, x_B_T_H_W_D, emb_B_T_D, crossattn_emb, rope_emb_L_1_1_D=None, adaln_lora_B_T_3D=None,
                    extra_per_block_pos_emb=None, transformer_options={}):
-    """ComfyUI's Block.forward with its three sub-layers run through ``_run_sublayer``: the same operations in the
-    same order wherever a part does not apply."""
+    """ComfyUI's Block.forward (same signature), its three sub-layers run by ``_step``."""
+    x, emb, lora = x_B_T_H_W_D, emb_B_T_D, adaln_lora_B_T_3D
+    call = _BlockCall(self, transformer_options, emb.dtype, x.dtype)
     merge = _MERGE_GATES if _MERGE_GATES is not None else _env.get("WEIGHTFERRY_CFG_RESID_MERGE") == "1"
-    _tls.same_gate = bool(merge and _on("res") and _gates_equal(emb_B_T_D, adaln_lora_B_T_3D))
-    try:
-        return _block_body(self, x_B_T_H_W_D, emb_B_T_D, crossattn_emb, rope_emb_L_1_1_D, adaln_lora_B_T_3D,
-                           extra_per_block_pos_emb, transformer_options)
-    finally:
-        _tls.same_gate = False
-
-
-def _modulation(block, emb, lora):
-    """(shift, scale, gate) of each sub-layer as (B, T, 1, 1, D) tensors, from the block's AdaLN modulations."""
-    out = []
-    for layer in (block.adaln_modulation_self_attn, block.adaln_modulation_cross_attn, block.adaln_modulation_mlp):
-        m = layer(emb)
-        if block.use_adaln_lora:
+    call.same_gate = bool(merge and _on("res") and _equal_gate_rows(emb, lora))
+    if extra_per_block_pos_emb is not None:
+        x = x + extra_per_block_pos_emb
+    # (shift, scale, gate) of each sub-layer, (B, T, 1, 1, D)
+    mods = []
+    for adaln in (self.adaln_modulation_self_attn, self.adaln_modulation_cross_attn, self.adaln_modulation_mlp):
+        m = adaln(emb)
+        if self.use_adaln_lora:
             m = m + lora
-        out.append(tuple(t.unsqueeze(2).unsqueeze(2) for t in m.chunk(3, dim=-1)))
-    return out
-
-
-def _block_body(self, x, emb, crossattn_emb, rope_emb, adaln_lora, extra_pos, transformer_options):
-    call = _Call(self, transformer_options, emb.dtype, x.dtype)
-    if extra_pos is not None:
-        x = x + extra_pos
-    (sh_sa, sc_sa, g_sa), (sh_ca, sc_ca, g_ca), (sh_mlp, sc_mlp, g_mlp) = _modulation(self, emb, adaln_lora)
+        mods.append([c[:, :, None, None, :] for c in m.chunk(3, dim=-1)])
     B, T, H, W, D = x.shape
+    cd = call.compute_dtype
 
-    def tokens(n):                      # (B, T, H, W, D) -> (B, T H W, D), the attention's layout
-        return n.to(call.compute_dtype).reshape(B, T * H * W, D)
+    def attention(attn, context):
+        def run(n):
+            out = attn(n.to(cd).reshape(B, T * H * W, D), context, rope_emb=rope_emb_L_1_1_D,
+                       transformer_options=transformer_options)
+            return out.reshape(B, T, H, W, D)
+        return run
 
-    def grid(r):
-        return r.reshape(B, T, H, W, D)
-
-    out, added = _run_sublayer(
-        call, self.self_attn, (self.layer_norm_self_attn, x), sc_sa, sh_sa,
-        lambda n: self.self_attn(tokens(n), None, rope_emb=rope_emb, transformer_options=transformer_options),
-        x, g_sa, self.self_attn.output_proj)
-    x = _join_residual(x, g_sa, grid(out), added, call.residual_dtype)
-
-    out, added = _run_sublayer(
-        call, self.cross_attn, (self.layer_norm_cross_attn, x), sc_ca, sh_ca,
-        lambda n: self.cross_attn(tokens(n), crossattn_emb, rope_emb=rope_emb,
-                                  transformer_options=transformer_options),
-        x, g_ca, self.cross_attn.output_proj, overrides=(self.cross_attn.q_proj,))
-    x = _join_residual(x, g_ca, grid(out), added, call.residual_dtype)
-
+    sa, ca = self.self_attn, self.cross_attn
+    x = _step(call, _Sub(sa, self.layer_norm_self_attn, *mods[0], attention(sa, None), sa.output_proj, ()), x)
+    x = _step(call, _Sub(ca, self.layer_norm_cross_attn, *mods[1], attention(ca, crossattn_emb), ca.output_proj,
+                         (ca.q_proj,)), x)
+    shift, scale, gate = mods[2]
     patches = (transformer_options or {}).get("patches", {})
-    if "mlp_patch" in patches:
-        normed = _modulate(self.layer_norm_mlp(x), sc_mlp, sh_mlp).to(call.compute_dtype)
-        args = {"x": normed, "transformer_options": transformer_options}
-        for patch in patches["mlp_patch"]:
-            args = patch(args)
-        out, added = self.mlp(args["x"]), False
-    else:
-        out, added = _run_sublayer(call, self.mlp, (self.layer_norm_mlp, x), sc_mlp, sh_mlp,
-                                   lambda n: self.mlp(n.to(call.compute_dtype)), x, g_mlp, self.mlp.layer2)
-    return _join_residual(x, g_mlp, out, added, call.residual_dtype)
+    if "mlp_patch" not in patches:
+        return _step(call, _Sub(self.mlp, self.layer_norm_mlp, shift, scale, gate, lambda n: self.mlp(n.to(cd)),
+                                self.mlp.layer2, ()), x)
+    # ComfyUI's MLP patches see the real input: nothing pending, no epilogue
+    args = {"x": (self.layer_norm_mlp(x) * (1 + scale) + shift).to(cd), "transformer_options": transformer_options}
+    for patch in patches["mlp_patch"]:
+        args = patch(args)
+    out = self.mlp(args["x"])
+    rd = call.residual_dtype
+    return torch.addcmul(x, gate.to(rd), out.to(rd))
 
 
 def _compute_qkv(self, x, context=None, rope_emb=None, transformer_options={}):
-    """ComfyUI's Attention.compute_qkv with the self-attention's three projections under one ``_Overrides``, so
-    their common input is quantised once (and a pending input applied once)."""
+    """ComfyUI's Attention.compute_qkv; for the self-attention, its q / k / v projections compute through
+    fused_int8 together, so their common input (or the pending one) is quantised once."""
     orig = _state["orig"]["compute_qkv"]
-    if (context is not None or not getattr(self, "is_selfattn", False) or not _on("qkv")
-            or "attn1_patch" in (transformer_options or {}).get("patches", {})):
-        return orig(self, x, context, rope_emb=rope_emb, transformer_options=transformer_options)
-    projs = [p for p in (self.q_proj, self.k_proj, self.v_proj) if hasattr(p, "_forward")]
-    if len(projs) != 3:
+    shared = (context is None and getattr(self, "is_selfattn", False) and _on("qkv")
+              and "attn1_patch" not in (transformer_options or {}).get("patches", {}))
+    if shared:
+        projs = [p for p in (self.q_proj, self.k_proj, self.v_proj) if hasattr(p, "_forward")]
+        if len(projs) == 3:
+            with _Overrides(projs):
+                return orig(self, x, context, rope_emb=rope_emb, transformer_options=transformer_options)
         _count("qkv", False, "projections without _forward")
-        return orig(self, x, context, rope_emb=rope_emb, transformer_options=transformer_options)
-    with _Overrides(projs):
-        return orig(self, x, context, rope_emb=rope_emb, transformer_options=transformer_options)
+    return orig(self, x, context, rope_emb=rope_emb, transformer_options=transformer_options)
 
 
 def _mlp_forward(self, x):
-    """ComfyUI's GPT2FeedForward.forward (layer1, GELU, layer2) with a pending input taken by layer1 and the GELU
-    left pending for layer2's quantiser."""
+    """ComfyUI's GPT2FeedForward.forward (layer1, activation, layer2). layer1 takes the block's pending input, when
+    there is one; with the gelu part, torch's exact GELU is left pending for layer2's quantiser. A pending input a
+    layer did not take is computed the plain way and that layer run again on it."""
     orig = _state["orig"]["mlp_forward"]
     act = getattr(self, "activation", None)
-    gelu_ok = (_on("gelu") and type(act) is torch.nn.GELU and getattr(act, "approximate", "none") == "none"
-               and _int8_proj_ok(self.layer2))
-    pre = getattr(_tls, "pre", None)
-    if not gelu_ok and pre is None:
+    gelu = (_on("gelu") and type(act) is torch.nn.GELU and getattr(act, "approximate", "none") == "none"
+            and _int8_proj_ok(self.layer2))
+    inherited = getattr(_tls, "pre", None)          # the block's pending input for layer1
+    if inherited is None and not gelu:
         return orig(self, x)
     with _Overrides([self.layer1, self.layer2]):
         h = self.layer1(x)
-        if pre is not None:
-            _clear_pre()
-            if not pre.used:            # layer1 did not take the pending input: run it on the real one
+        if inherited is not None:
+            _clear_pre()                            # the block's pending input ends at layer1
+            if not inherited.used:
                 _count("modq", False, "mlp.layer1 did not take the pending input")
-                h = self.layer1(_materialise(pre).view(x.shape))
-        if not (gelu_ok and h.dtype == torch.bfloat16 and h.is_cuda and h.is_contiguous()):
+                h = self.layer1(inherited.real().view(x.shape))
+        if not (gelu and _bf16_cuda(h)):
             return self.layer2(self.activation(h))
-        gelu = _set_pre(h, "gelu")
+        pend = _set_pre(h, "gelu")
         try:
             out = self.layer2(h)
         finally:
             _clear_pre()
-        if not gelu.used:
-            _count("gelu", False, "mlp.layer2 did not take the pending input")
-            out = self.layer2(self.activation(h))
-        return out
+        if pend.used:
+            return out
+        _count("gelu", False, "mlp.layer2 did not take the pending input")
+        return self.layer2(self.activation(h))
 
 
 # ------------------------------------------------------------------------------------------------ install
+# (class, method, replacement, the parts any of which needs it)
+_METHODS = (("Block", "forward", _block_forward, PARTS),
+            ("Attention", "compute_qkv", _compute_qkv, ("qkv",)),
+            ("GPT2FeedForward", "forward", _mlp_forward, ("gelu", "modq")))
+_ORIG_KEY = {("Block", "forward"): "forward", ("Attention", "compute_qkv"): "compute_qkv",
+             ("GPT2FeedForward", "forward"): "mlp_forward"}
+
+
 def _cosmos_module():
     import comfy.ldm.cosmos.predict2 as p2
     return p2
 
 
 def install(parts=None, module=None):
-    """Put the adapter on ``module``'s Block / Attention / GPT2FeedForward classes (default: ComfyUI's
-    comfy.ldm.cosmos.predict2) for ``parts`` (default: WEIGHTFERRY_FUSED_BLOCK). install(()) gives ComfyUI's
-    methods back. Returns the parts in effect."""
+    """Replace the methods of ``module``'s Block / Attention / GPT2FeedForward (default: ComfyUI's
+    comfy.ldm.cosmos.predict2) that ``parts`` (default: WEIGHTFERRY_FUSED_BLOCK) need, and give ComfyUI's back to
+    the others; install(()) restores all three. Returns the parts in effect ("ln" only with "modq", which carries
+    it)."""
     if module is None:
         try:
             module = _cosmos_module()
         except Exception as exc:  # noqa: BLE001 -- no ComfyUI Cosmos model: nothing to patch
             log_warn(f"int8 block: ComfyUI's Cosmos model not found ({exc}); not installed.")
             return ()
-    parts = tuple(p for p in (wanted_parts() if parts is None else parts) if p in PARTS)
-    if "ln" in parts and "modq" not in parts:
-        parts = tuple(p for p in parts if p != "ln")     # the LayerNorm travels with the pending scale-and-shift
+    chosen = set(wanted_parts() if parts is None else parts)
+    if "modq" not in chosen:
+        chosen.discard("ln")
+    parts = tuple(p for p in PARTS if p in chosen)
     orig = _state.get("orig")
     if orig is None or orig.get("module") is not module:
-        orig = _state["orig"] = {"module": module, "forward": module.Block.forward,
-                                 "compute_qkv": module.Attention.compute_qkv,
-                                 "mlp_forward": module.GPT2FeedForward.forward}
+        orig = {"module": module}
+        for cls, meth, _fn, _needs in _METHODS:
+            orig[_ORIG_KEY[(cls, meth)]] = getattr(getattr(module, cls), meth)
+        _state["orig"] = orig
     _state["parts"] = parts
-    module.Block.forward = _block_forward if parts else orig["forward"]
-    module.Attention.compute_qkv = _compute_qkv if "qkv" in parts else orig["compute_qkv"]
-    module.GPT2FeedForward.forward = _mlp_forward if ("gelu" in parts or "modq" in parts) else orig["mlp_forward"]
+    for cls, meth, fn, needs in _METHODS:
+        setattr(getattr(module, cls), meth, fn if set(parts) & set(needs) else orig[_ORIG_KEY[(cls, meth)]])
     if parts:
         log_info(f"int8 block: {', '.join(parts)} (WEIGHTFERRY_FUSED_BLOCK).")
     return parts

@@ -95,6 +95,29 @@ def test_wan_block_shapes_sampled_rows(native, qtype, N, K):
     check(y, x, weight_bf16(raw, qtype, 0, N, K), rows=rows)
 
 
+@pytest.mark.parametrize("qtype,N,K", [(13, 5120, 5120), (14, 5120, 5120), (13, 5120, 13824), (14, 13824, 5120),
+                                        (12, 5120, 13824)])
+def test_wan_block_shapes_whole_output(native, qtype, N, K):
+    # every one of the 4096 x N outputs of a Wan block layer at full K (random blocks of realistic scales), against a
+    # float32 GEMM on the GPU of the same bf16 activations with the oracle's dequantised bf16 weight; the same bounds
+    # as check()
+    M = 4096
+    raw = encode.random_blocks(qtype, N * K // 256, seed=N + K + qtype, family="normal")
+    g = torch.Generator().manual_seed(99)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16).cuda()
+    print(f"case wan whole output qtype={qtype} M={M} N={N} K={K}", flush=True)
+    y = fused(native, x, torch.from_numpy(raw).cuda(), qtype, N)
+    w = weight_bf16(raw, qtype, 0, N, K).cuda()
+    torch.backends.cuda.matmul.allow_tf32 = False
+    ref = x.float() @ w.T
+    del w
+    scale = ref.abs().max().item()
+    err = (y.float() - ref).abs()
+    assert err.max().item() / scale <= 1e-2
+    over = err - (ref.abs() * 2.0 ** -8 + 1e-3 * scale)
+    assert over.max().item() <= 0, (over.max().item(), torch.nonzero(over > 0)[:4].tolist())
+
+
 @pytest.mark.parametrize("qtype", [12, 13, 14])
 @pytest.mark.parametrize("mid", [0, 2])
 @pytest.mark.parametrize("M,N,K,with_bias", [(1, 300, 256, True), (5, 5120, 5120, False), (16, 61, 512, True),
