@@ -30,7 +30,7 @@ typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 constexpr int kBK = 128;        // K bytes per stage of gemm_i8
 constexpr int kGroupM = 8;      // tile-rows per group of the tile order
 
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ (((row >> 1) ^ ((row & 1) << 2)) & 7); }
+__device__ __forceinline__ int swz(int row, int chunk) { return swz8(row, chunk); }
 
 __device__ __forceinline__ float to_f32_out(const void* p, int64_t i, int dt) {
     if (dt == WF_BF16) return __uint_as_float((uint32_t)static_cast<const uint16_t*>(p)[i] << 16);

@@ -20,6 +20,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, in
 // of 16 consecutive rows hit 16 different 16-byte bank groups
 __device__ __forceinline__ int swz4(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
 
+// chunk c (16 bytes) of a 128-byte LDS row r sits at slot c ^ (((r >> 1) ^ ((r & 1) << 2)) & 7): conflict-free for
+// the fragment reads of one chunk of consecutive rows and for whole-row writes
+__device__ __forceinline__ int swz8(int row, int chunk) { return chunk ^ (((row >> 1) ^ ((row & 1) << 2)) & 7); }
+
 // 16 bytes per lane from buffer r at voffset into LDS slot `lane` of the 1 KiB run at lds (wave-uniform); the byte
 // offset is in voffset so that the buffer's range check covers it. The address-space cast is device code only; the
 // host pass never sees it.

@@ -118,6 +118,44 @@ def test_wan_block_shapes_whole_output(native, qtype, N, K):
     assert over.max().item() <= 0, (over.max().item(), torch.nonzero(over > 0)[:4].tolist())
 
 
+def check_gpu(y, x, w, bias=None):
+    """check()'s bounds against a float32 GEMM on the GPU (for outputs too large for a CPU float64 reference)"""
+    torch.backends.cuda.matmul.allow_tf32 = False
+    ref = x.float() @ w.cuda().T
+    if bias is not None:
+        ref = ref + bias.float()[None, :]
+    scale = ref.abs().max().item()
+    err = (y.float() - ref).abs()
+    assert err.max().item() / scale <= 1e-2
+    over = err - (ref.abs() * 2.0 ** -8 + 1e-3 * scale)
+    assert over.max().item() <= 0, (over.max().item(), torch.nonzero(over > 0)[:4].tolist())
+
+
+@pytest.mark.parametrize("M,N,K,with_bias,mid,offset", [(2048, 8999, 768, False, 0, 0), (2100, 8000, 256, True, 2, 0),
+                                                        (4100, 8000, 512, True, 1, 1), (3333, 5120, 1280, False, 0, 0),
+                                                        (4096, 5120, 512, False, 0, 1)])
+def test_q6k_tall_form_whole_output(native, M, N, K, with_bias, mid, offset):
+    # Q6_K from 1024 rows, where 512 x 160 tiles take no more modelled rounds than 256-row tiles, goes to the tall form
+    # (each dequantised weight value feeds 512 rows; activations as whole 128-byte lines): ragged M past a 512-row
+    # tile, ragged N past a 160-row tile and N % 8 != 0 (element stores), bias, every MID, and an output view one
+    # element past an aligned start (element stores); every output element checked
+    qtype = 14
+    raw = encode.random_blocks(qtype, N * K // 256, seed=M + N + K, family="normal")
+    g = torch.Generator().manual_seed(M * 3 + N)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16).cuda()
+    bias = torch.randn(N, generator=g).to(torch.bfloat16).cuda() if with_bias else None
+    flat = torch.empty(M * N + 8, dtype=torch.bfloat16, device="cuda")
+    y = flat[offset:offset + M * N].view(M, N)
+    print(f"case tall qtype=14 M={M} N={N} K={K} mid={mid} offset={offset}", flush=True)
+    rd = torch.from_numpy(raw).cuda()
+    rc = native.lib().wf_linear_gguf(x.data_ptr(), M, K, rd.data_ptr(), rd.numel(), qtype, N,
+                                     bias.data_ptr() if bias is not None else None, y.data_ptr(), mid,
+                                     native.stream_of(x.device))
+    assert rc == 0, native.last_error()
+    torch.cuda.synchronize()
+    check_gpu(y, x, weight_bf16(raw, qtype, mid, N, K), bias=bias)
+
+
 @pytest.mark.parametrize("qtype", [12, 13, 14])
 @pytest.mark.parametrize("mid", [0, 2])
 @pytest.mark.parametrize("M,N,K,with_bias", [(1, 300, 256, True), (5, 5120, 5120, False), (16, 61, 512, True),
