@@ -921,6 +921,11 @@ static void launch_splitk_mid(int mid, const uint16_t* X, const uint8_t* W, cons
     else launch_splitk<QT, WF_F32>(X, W, bias, Y, M, N, K, p, ws, st);
 }
 
+#ifndef WF_SKINNY_NR1_MAX_N
+#define WF_SKINNY_NR1_MAX_N 8191
+#endif
+static constexpr int kSkinnyNr1MaxN = WF_SKINNY_NR1_MAX_N;
+
 template <int QT, int MID, int MT, int NR, int NW, bool AHEAD = false>
 static void launch_skinny(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
                           hipStream_t s) {
@@ -971,11 +976,19 @@ static void launch(const uint16_t* X, const uint8_t* W, const uint16_t* bias, ui
     // reads at every row count: with its raw bytes through sk_load_q6 the 32-row, 8-wave form is the fastest one
     // (Wan shapes at 1-8 rows, per layer: 18.4 / 34.8 / 39.1 us against 20.3 / 37.2 / 47.4 for the 16-row, 4-wave
     // workgroups with activations ahead and the narrow loads).
+    // Up to 16 rows of a Q6_K product narrower than 256 workgroups of 32 rows, 16 weight rows per workgroup (NR = 1):
+    // more CUs wait on Q6_K's slower raw loads (Wan block at one row 129 against 147 us, cold weights, MI355X). For
+    // Q4_K / Q5_K the 64 CUs that then hold two workgroups set the time (88 against 82 us): their few-rows kernel is
+    // bound by the dequantisation's VALU work per CU, which the split does not shrink.
     if (M <= 8 && QT != 14) {
         launch_skinny<QT, MID, 1, 2, 8, true>(X, W, bias, Y, M, N, K, s);
         return;
     }
-    if (M <= 16) { launch_skinny<QT, MID, 1, 2, 8>(X, W, bias, Y, M, N, K, s); return; }
+    if (M <= 16) {
+        if (QT == 14 && N <= kSkinnyNr1MaxN) launch_skinny<QT, MID, 1, 1, 8>(X, W, bias, Y, M, N, K, s);
+        else launch_skinny<QT, MID, 1, 2, 8>(X, W, bias, Y, M, N, K, s);
+        return;
+    }
     if (M <= 32) { launch_skinny<QT, MID, 2, 2, 8>(X, W, bias, Y, M, N, K, s); return; }
     if (M <= 64) { launch_skinny<QT, MID, 4, 2, 8>(X, W, bias, Y, M, N, K, s); return; }
     auto cost = [&](int bn) {
