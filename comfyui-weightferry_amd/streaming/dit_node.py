@@ -7,20 +7,60 @@ application is not part of this path, so here they are plain calls: ``apply_stre
 installs the hooks, ``StreamedModel.__call__`` runs one forward with streaming active, ``teardown`` undoes it."""
 import torch
 
-from .common import _ACTIVE_ATTR, _STATE_ATTR, _blocks
+from .common import _ACTIVE_ATTR, _STATE_ATTR, _blocks, _flat_layout, _specs, _views
 from .load_steps import (_build_chunk_state, _build_state, _install_block_stream_hooks, _install_chunk_hooks,
                          _install_first_block_hook, _install_resident_profile_hooks)
+
+
+class _ResidentBuffers:
+    """Self-managed resident blocks (the reference's resident_mode "Self-managed", streaming/state.py:91-106): each
+    block's parameters are copied once into a GPU buffer of its own, in the streamed blocks' 256-byte aligned flat
+    layout, and bound to it for each forward only; between forwards the parameters hold their own tensors again
+    (``rest``). The host application's memory manager can then move, offload or rewrite those tensors without
+    touching what the forwards read."""
+
+    def __init__(self, blocks, device):
+        self.blocks = list(blocks)
+        self.rest = [[p.data for p in b.parameters()] for b in self.blocks]
+        self.flats, self.views = [], []
+        for b in self.blocks:
+            specs = _specs(b)
+            offsets, total = _flat_layout(specs)
+            flat = torch.empty(total, dtype=torch.uint8, device=device)
+            views = _views(flat, specs, offsets)
+            for p, v in zip(b.parameters(), views):
+                v.copy_(p.data)
+            self.flats.append(flat)
+            self.views.append(views)
+
+    def bind(self):
+        for b, views in zip(self.blocks, self.views):
+            for p, v in zip(b.parameters(), views):
+                p.data = v
+
+    def unbind(self):
+        for b, rest in zip(self.blocks, self.rest):
+            for p, r in zip(b.parameters(), rest):
+                p.data = r
+
+    def release(self, device=None):
+        """The parameters get their own tensors back (moved to ``device`` when given); the buffers are freed."""
+        for b, rest in zip(self.blocks, self.rest):
+            for p, r in zip(b.parameters(), rest):
+                p.data = r if device is None else r.to(device)
+        self.flats, self.views = [], []
 
 
 class StreamedModel:
     """A model whose blocks stream from pinned host memory through GPU slots."""
 
-    def __init__(self, dit, state, resident_idx, stream_idx, owner):
+    def __init__(self, dit, state, resident_idx, stream_idx, owner, residents=None):
         self.dit = dit
         self.state = state
         self.resident_idx = resident_idx
         self.stream_idx = stream_idx
         self.owner = owner
+        self.residents = residents            # _ResidentBuffers of self-managed resident blocks, or None
 
     def __call__(self, *args, **kwargs):
         """One forward of the model with streaming active."""
@@ -35,6 +75,8 @@ class StreamedModel:
         prof = state.profiler
         try:
             state.begin_forward()
+            if self.residents is not None:
+                self.residents.bind()
             if prof is not None:
                 prof.begin_forward(state.compute_stream())
             return fn(*args, **kwargs)
@@ -42,6 +84,8 @@ class StreamedModel:
             if prof is not None:
                 prof.end_forward(state.compute_stream())
             setattr(dit, _ACTIVE_ATTR, None)
+            if self.residents is not None:
+                self.residents.unbind()
             state.restore_rest_binding()
             state.end_forward()
 
@@ -53,6 +97,9 @@ class StreamedModel:
         buffers and slots."""
         state = self.state
         dev = torch.device(device) if device is not None else state.device
+        if self.residents is not None:
+            self.residents.release(dev)
+            self.residents = None
         state.close()
         for blk in state.streaming_blocks:
             for p in blk.parameters():
@@ -68,10 +115,12 @@ class StreamedModel:
 def apply_streaming(dit, device="cuda", resident_blocks=0, prefetch_slots=2, pin_memory=True, profile=None,
                     model_file=None, ram_blocks=None, ssd_layout=None, ring_depth=2, ring_threads=1, direct_io=True,
                     tensor_name=None, double_buffer=True, ssd_dir=None, chunk=False, chunk_bytes=None,
-                    chunk_slots=None, order_cache=None):
+                    chunk_slots=None, order_cache=None, self_resident=False):
     """Stream all but the first ``resident_blocks`` blocks of ``dit`` (which stay where they are, on ``device``)
     through ``prefetch_slots`` (>= 2) GPU slots. The reference keeps block 0 resident by default
-    (streaming/dit_node.py:237-267); here resident_blocks = 0 streams every block.
+    (streaming/dit_node.py:237-267); here resident_blocks = 0 streams every block. ``self_resident``: the resident
+    blocks are copied into GPU buffers of their own and bound to them for each forward only (_ResidentBuffers)
+    instead of being moved to ``device``.
 
     SSD tier: with ``ram_blocks`` below the number of streamed blocks, only ``ram_blocks`` blocks are captured into
     pinned RAM; the others (spread by ``ssd_layout``, see core.tiers.plan.ssd_positions) are read from disk on every
@@ -95,8 +144,12 @@ def apply_streaming(dit, device="cuda", resident_blocks=0, prefetch_slots=2, pin
     stream_idx = list(range(len(resident_idx), len(blocks)))
     if not stream_idx:
         raise ValueError("no block left to stream")
-    for i in resident_idx:
-        blocks[i].to(device)
+    residents = None
+    if self_resident and resident_idx:
+        residents = _ResidentBuffers([blocks[i] for i in resident_idx], device)
+    else:
+        for i in resident_idx:
+            blocks[i].to(device)
     owner = object()
     ssd = _ssd_tier(dit, blocks, stream_idx, model_file, ram_blocks, ssd_layout, ring_depth, ring_threads, direct_io,
                     tensor_name, ssd_dir)
@@ -108,14 +161,14 @@ def apply_streaming(dit, device="cuda", resident_blocks=0, prefetch_slots=2, pin
         _install_first_block_hook(dit, blocks[0], state, owner)
         _install_chunk_hooks(dit, state, owner)
         setattr(dit, _STATE_ATTR, state)
-        return StreamedModel(dit, state, resident_idx, stream_idx, owner)
+        return StreamedModel(dit, state, resident_idx, stream_idx, owner, residents)
     state = _build_state(owner, device, [blocks[i] for i in stream_idx], prefetch_slots, pin_memory, profile, ssd,
                          double_buffer)
     _install_first_block_hook(dit, blocks[0], state, owner)
     _install_block_stream_hooks(dit, state, owner)
     _install_resident_profile_hooks(dit, blocks, resident_idx, state, owner)
     setattr(dit, _STATE_ATTR, state)
-    return StreamedModel(dit, state, resident_idx, stream_idx, owner)
+    return StreamedModel(dit, state, resident_idx, stream_idx, owner, residents)
 
 
 def _ssd_tier(dit, blocks, stream_idx, model_file, ram_blocks, ssd_layout, ring_depth, ring_threads, direct_io,

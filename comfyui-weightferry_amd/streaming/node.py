@@ -21,9 +21,10 @@ WEIGHTFERRY_RAM_MARGIN_GB, see core.tiers.plan.plan_tiers) on the SSD tier:
 read straight from the GGUF model file named by WEIGHTFERRY_MODEL_FILE (ComfyUI-GGUF's loaded tensors do not carry
 their file's path), or else from a cache file of their captured bytes (WEIGHTFERRY_CACHE_DIR; kept for later runs
 with WEIGHTFERRY_PERSIST_GB > 0). The ring's depth and reader threads follow the drive's measured read rate
-(core.tiers.disk_io.probe_disk, remembered for a week). Options of the reference that belong to other paths -- SageAttention, fp8 storage format,
-self-managed residents, auto-configuration, the VRAM budget -- are accepted and logged as not applied; the node
-then streams as with their defaults."""
+(core.tiers.disk_io.probe_disk, remembered for a week). resident_mode "Self-managed" keeps the resident blocks in GPU
+buffers of the node's own, bound for each forward (dit_node._ResidentBuffers). Options of the reference that belong to
+other paths -- SageAttention, fp8 storage format, auto-configuration, the VRAM budget -- are accepted and logged as not
+applied; the node then streams as with their defaults."""
 import math
 import os
 
@@ -104,7 +105,7 @@ class WeightFerryDiT:
         not_applied = [name for name, on in (
             ("sage_attention", sage_attention), ("sage_pv_fp16", sage_pv_fp16),
             ("host_format=storage", host_format == HOST_FORMAT_STORAGE),
-            ("resident_mode=self-managed", resident_mode == RESIDENT_MODE_SELF), ("auto_config", auto_config),
+            ("auto_config", auto_config),
             ("vram_budget_gb", bool(vram_budget_gb)), ("text encoder streaming", _text_encoder)) if on]
         if not_applied:
             log_info(f"DiT Layer Streaming: not part of this package, not applied: {', '.join(not_applied)}.")
@@ -173,7 +174,8 @@ class WeightFerryDiT:
                                           pin_memory=pin_memory, model_file=model_file or None, ram_blocks=ram_blocks,
                                           double_buffer=double or (ram_blocks is not None and ram_blocks < num_stream),
                                           ring_depth=depth, ring_threads=threads, chunk=chunk,
-                                          order_cache=order_cache if chunk else None)
+                                          order_cache=order_cache if chunk else None,
+                                          self_resident=resident_mode == RESIDENT_MODE_SELF)
             sm.owner_node = owner
             setattr(dit, _NODE_ATTR, sm)
             n_ssd = len(sm.state.disk_index)

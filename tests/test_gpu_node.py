@@ -72,6 +72,27 @@ def test_load_forward_detach(native, comfy, reference, buffer_mode, slots):
     assert all(p.device.type == "cpu" for b in model.blocks[1:] for p in b.parameters())
 
 
+def test_self_managed_residents(native, comfy, reference):
+    # resident_mode "Self-managed": the two resident blocks run on the node's own GPU copies, bound for each forward
+    # only; a write-back into the blocks' own tensors between forwards does not change the output
+    x, ctx, ref = reference
+    node = sub("streaming.node")
+    model = _stack()
+    mp = node.WeightFerryDiT().apply_streaming(fake_comfy.FakeModelPatcher(model), resident_blocks=2,
+                                               resident_mode=node.RESIDENT_MODE_SELF, prefetch_slots=2)[0]
+    model.blocks[0].cuda()
+    model.blocks[1].cuda()
+    mp.load()
+    sm = getattr(model, node._NODE_ATTR)
+    assert sm.residents is not None and len(sm.stream_idx) == 4
+    _check(mp, x, ctx, ref, times=1)
+    for p in model.blocks[1].parameters():
+        p.data.zero_()
+    _check(mp, x, ctx, ref, times=2)
+    mp.detach()
+    assert all(p.device.type == "cpu" for b in model.blocks for p in b.parameters())
+
+
 def test_skipped_on_load_captures_lazily(native, comfy, reference):
     x, ctx, ref = reference
     node = sub("streaming.node")

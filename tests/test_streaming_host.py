@@ -181,6 +181,33 @@ def test_hook_protocol_binds_the_right_bytes(fake, slots, skip):
     assert sm.state.num_slots == slots
 
 
+def test_self_managed_residents(fake):
+    # resident_mode "Self-managed": the resident blocks run on copies of their own, bound for each forward only --
+    # what the host application's memory manager then does to the blocks' tensors (a write-back overwriting them)
+    # does not reach the forward, and between forwards the parameters hold those tensors again
+    dn = sub("streaming.dit_node")
+    seen = []
+    model = Stack(6, seen)
+    own = [[p.data for p in model.blocks[i].parameters()] for i in range(2)]
+    sm = dn.apply_streaming(model, device="cpu", resident_blocks=2, prefetch_slots=2, pin_memory=False,
+                            profile=False, self_resident=True)
+    assert sm.stream_idx == [2, 3, 4, 5]
+    for t in own[0] + own[1]:
+        t.zero_()                                          # the host application rewrites the blocks' tensors
+    for _ in range(2):
+        seen.clear()
+        sm(torch.zeros(1))
+        fake.run_all()
+        assert [s[0] for s in seen] == [1, 2, 3, 4, 5, 6]
+        for tag, w0, w1, b0 in seen:
+            assert (w0, w1, b0) == (tag, tag, 2 * tag), seen
+        for i in range(2):
+            assert all(p.data_ptr() == t.data_ptr() for p, t in zip(model.blocks[i].parameters(), own[i]))
+    sm.teardown(device="cpu")
+    assert sm.residents is None
+    assert all(p.data_ptr() == t.data_ptr() for p, t in zip(model.blocks[0].parameters(), own[0]))
+
+
 def test_every_copy_waits_for_the_slots_last_reader(fake):
     dn = sub("streaming.dit_node")
     seen = []
