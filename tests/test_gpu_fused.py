@@ -1,7 +1,7 @@
 """GPU check of wf_linear_gguf (fused K-quant dequant + bf16 MFMA GEMM) through the C ABI.
 
 Reference: a float64 GEMM of the same bf16 activations with the oracle's bit-exact dequantised bf16 weight (the
-reference path: dequantize, then F.linear in bf16). The tolerance is the north-star bound, max relative error
+reference path: dequantize, then F.linear in bf16). The tolerance is the task's bound for bf16 GEMMs, max relative error
 <= 1e-2 (max |y - ref| / max |ref|); each element is also held to |y - ref| <= 2^-8 |ref| + 1e-3 max |ref|, which
 only a correct weight meets (float32 accumulation order and the final bf16 rounding stay well inside it)."""
 import numpy as np
