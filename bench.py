@@ -149,7 +149,8 @@ WAN_LINEARS = [("q", 5120, 5120), ("k", 5120, 5120), ("v", 5120, 5120), ("o", 51
 
 def fused_leg(torch, native):
     """One Wan-14B block's linears at 4096 tokens with Q5_K / Q6_K weights: the fused kernel and the two-step
-    flow (wf_dequant to bf16, then torch's bf16 GEMM)."""
+    flow (wf_dequant to bf16, then a bf16 GEMM: torch's, hipBLASLt, and the library's wf_linear_bf16, which the
+    GGUF linear's two-step flow takes at this row count)."""
     sys.path.insert(0, ROOT)
     encode = importlib.import_module(PKG + ".gguf_encode")
     lib = native.lib()
@@ -158,7 +159,7 @@ def fused_leg(torch, native):
     M = 4096
     res = {}
     for qt, name in ((13, "q5_k"), (14, "q6_k")):
-        tf = tu = 0.0
+        tf = tu = th = 0.0
         flops = wbytes = 0
         for lname, N, K in WAN_LINEARS:
             raw = torch.from_numpy(encode.encode(encode.weights((N, K), seed=N + K), qt)).to(dev)
@@ -172,14 +173,20 @@ def fused_leg(torch, native):
             def two_step():
                 lib.wf_dequant(raw.data_ptr(), raw.numel(), qt, 0, 1, w.data_ptr(), N * K, st)
                 torch.matmul(x, w.t(), out=y)
+
+            def two_step_hand():
+                lib.wf_dequant(raw.data_ptr(), raw.numel(), qt, 0, 1, w.data_ptr(), N * K, st)
+                lib.wf_linear_bf16(x.data_ptr(), w.data_ptr(), None, y.data_ptr(), M, N, K, st)
             tf += _timed(torch, fused, 10, 2)
             tu += _timed(torch, two_step, 10, 2)
+            th += _timed(torch, two_step_hand, 10, 2)
             flops += 2 * M * N * K
             wbytes += raw.numel()
             del raw, x, y, w
         res[name] = {"fused_ms": round(tf, 3), "fused_TFLOPS": round(flops / tf / 1e9, 1),
                      "fused_frac_of_2500": round(flops / tf / 1e9 / 2500, 3),
                      "two_step_ms": round(tu, 3), "two_step_TFLOPS": round(flops / tu / 1e9, 1),
+                     "two_step_hand_ms": round(th, 3), "two_step_hand_TFLOPS": round(flops / th / 1e9, 1),
                      "flop": flops, "weight_bytes": wbytes}
     # few activation rows (128 and 32 tokens, and one token): the fused kernel's few-rows form streams each weight
     # once, its panel form once per 16 MT rows. "cold": every call reads another copy of the weight, the copies of a

@@ -30,6 +30,7 @@ EXPORTS = {
     "wf_quant_rows_i8": (_int, [_p, _i64, _i64, _int, _p, _p, _p]),
     "wf_quant_rows_i8_pre": (_int, [_p, _i64, _i64, _int, _p, _p, _i64, ctypes.c_float, _p, _p, _p]),
     "wf_linear_i8": (_int, [_p, _p, _p, _p, _p, _p, _int, _i64, _i64, _i64, _p]),
+    "wf_linear_bf16": (_int, [_p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "wf_linear_i8_residual": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "wf_linear_gguf": (_int, [_p, _i64, _i64, _p, _i64, _int, _i64, _p, _p, _int, _p]),
     "wf_linear_gguf_workspace": (_int, [_i64, _i64, _i64, ctypes.POINTER(_i64)]),

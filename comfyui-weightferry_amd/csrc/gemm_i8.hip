@@ -21,6 +21,7 @@
 #include <algorithm>
 
 #include "lds_ring.h"
+#include "wl_ring.h"
 
 namespace wf {
 
@@ -28,7 +29,6 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBK = 128;        // K bytes per stage of gemm_i8
-constexpr int kGroupM = 8;      // tile-rows per group of the tile order
 
 __device__ __forceinline__ int swz(int row, int chunk) { return swz8(row, chunk); }
 
@@ -36,19 +36,6 @@ __device__ __forceinline__ float to_f32_out(const void* p, int64_t i, int dt) {
     if (dt == WF_BF16) return __uint_as_float((uint32_t)static_cast<const uint16_t*>(p)[i] << 16);
     if (dt == WF_F16) return (float)__builtin_bit_cast(_Float16, static_cast<const uint16_t*>(p)[i]);
     return static_cast<const float*>(p)[i];
-}
-
-// tile index of workgroup w among T tiles (XCD-aware), then grouped row-major order over (tm, tn)
-__device__ __forceinline__ void tile_of(int w, int T, int ntm, int ntn, int& tm, int& tn) {
-    int L = w;
-    if ((T & 7) == 0) L = (w & 7) * (T >> 3) + (w >> 3);
-    const int per_group = kGroupM * ntn;
-    const int group = L / per_group;
-    const int first_m = group * kGroupM;
-    const int gm = min(ntm - first_m, kGroupM);
-    const int in = L - group * per_group;
-    tm = first_m + in % gm;
-    tn = in / gm;
 }
 
 // Epilogue operands of the residual variant: out = bf16(resid + gate[m / rows_per_group] * bf16(t)), t the plain
@@ -71,7 +58,7 @@ __global__ __launch_bounds__(256) void gemm_i8(const int8_t* __restrict__ A, con
     __shared__ uint4 lds[2][(BM + BN) * 8];
     const int ntm = (M + BM - 1) / BM, ntn = (N + BN - 1) / BN;
     int tm, tn;
-    tile_of(blockIdx.x, ntm * ntn, ntm, ntn, tm, tn);
+    tile_order(blockIdx.x, ntm * ntn, ntm, ntn, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -194,12 +181,12 @@ __global__ __launch_bounds__(256) void gemm_i8(const int8_t* __restrict__ A, con
 // fragments during stage kt and never waits on LDS right after a barrier. A stage row is BK bytes = BK / 16 chunks,
 // swizzled by row_swz so that the 16 lanes that read 16 rows' same chunk hit 16 different bank groups.
 //
-// BK = 64 (16 rows per load instruction) for every tiling; BK = 128 (8 rows of one whole 128-byte line each) for
-// the 128 x 160 tiling, whose 4 stages of 36 KiB fit the LDS. The vector memory return path (TD) pays per cache line
-// touched, so half-line row segments cost it as much as whole lines: at 1024 x 5120 it was 69 % busy at 26 % MFMA
-// busy with 64-byte stages, and 128-byte stages take that product from 39.3 to 33.3 us. The larger tilings hold 72
-// or 64 KiB per 128-byte stage, which leaves room for 2 stages only, and lost more to the shallower ring than they
-// gained (2048 x 5120: 62.3 against 73.0 us).
+// BK = 64 (16 rows per load instruction); BK = 128 (8 rows of one whole 128-byte line each) for the 128 x 160
+// tiling, whose 4 stages of 36 KiB fit the LDS. The vector memory return path (TD) pays per cache line touched, so
+// half-line row segments cost it as much as whole lines: at 1024 x 5120 it was 69 % busy at 26 % MFMA busy with
+// 64-byte stages, and 128-byte stages take that product from 39.3 to 33.3 us. The larger tilings hold 72 or 64 KiB
+// per 128-byte stage, room for two stage buffers only: they run gemm_i8_wl below when K % 128 == 0, this ring
+// otherwise.
 constexpr int kDlBK = 64;
 
 // slot of chunk c in a stage row r of CH chunks: 4 chunks (64 bytes) c ^ ((r >> 2) & 3); 8 chunks (128 bytes) swz
@@ -226,7 +213,7 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
     __shared__ i32x4 st0[SLOTS], st1[SLOTS], st2[SLOTS], st3[SLOTS];
     const int ntm = (M + BM - 1) / BM, ntn = (N + BN - 1) / BN;
     int tm, tn;
-    tile_of(blockIdx.x, ntm * ntn, ntm, ntn, tm, tn);
+    tile_order(blockIdx.x, ntm * ntn, ntm, ntn, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);     // wave-uniform: scalar load bases
@@ -411,6 +398,89 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
     }
 }
 
+// K % 128 == 0, the 256-row tilings: whole 128-byte lines through two stage buffers (wl_ring.h), whose barrier sits
+// before the last K step's MFMAs and whose loads leave right after it (16384 x 13824 x 5120: 1049 against 1137 us
+// for the 64-byte ring, 4096 x 5120 x 5120: 100.1 against 105.4 us). The 128 x 160 tiling keeps the 4-stage ring of
+// 128-byte stages (1024 x 5120 x 5120: 35.5 against 38.3 us on two buffers). Epilogue as above; the residual form
+// stores single elements.
+template <typename S, int OUT, bool BIAS, bool RESID>
+__global__ __launch_bounds__(S::NT) void gemm_i8_wl(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
+                                                    const float* __restrict__ xs, const float* __restrict__ ws,
+                                                    const void* __restrict__ bias, void* __restrict__ out, int M,
+                                                    int N, int K, Residual res) {
+    constexpr int WM = S::WM, WN = S::WN;
+    __shared__ wl_frag sb0[S::SLOTS], sb1[S::SLOTS];
+    const int ntm = (M + S::BM - 1) / S::BM, ntn = (N + S::BN - 1) / S::BN;
+    int tm, tn;
+    tile_order(blockIdx.x, ntm * ntn, ntm, ntn, tm, tn);
+    const int m0 = __builtin_amdgcn_readfirstlane(tm * S::BM), n0 = __builtin_amdgcn_readfirstlane(tn * S::BN);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const __amdgpu_buffer_rsrc_t ra = tile_rsrc(A + (int64_t)m0 * K, (int64_t)(M - m0) * K);
+    const __amdgpu_buffer_rsrc_t rb = tile_rsrc(B + (int64_t)n0 * K, (int64_t)(N - n0) * K);
+    i32x16 acc[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int j = 0; j < WN; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0;
+    wl_mainloop<S>(ra, rb, (uint32_t)K, K / 128, wave, lane, sb0, sb1, acc,
+                   [](const i32x16& c, const wl_frag& a, const wl_frag& b) {
+                       return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+                   });
+    const int wm = wave / S::VN, wn = wave % S::VN;
+    const int mw = m0 + wm * WM * 32, nw = n0 + wn * WN * 32;
+    const int lr = lane & 31, lk = lane >> 5;
+    float wsn[WN], bn[WN];
+#pragma unroll
+    for (int j = 0; j < WN; j++) {
+        const int n = nw + j * 32 + lr;
+        wsn[j] = n < N ? ws[n] : 0.0f;
+        bn[j] = BIAS && n < N ? to_f32_out(bias, n, OUT) : 0.0f;
+    }
+    if constexpr (!RESID) {
+        wl_store_tile<WM, WN>(wl_out_region<S>(sb0, sb1, wave), static_cast<uint16_t*>(out), M, N, mw, nw, lane,
+                              [&](int i, int j, int e) {
+                                  const int m = mw + i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
+                                  const float xm = m < M ? xs[m] : 0.0f;
+                                  float t = ((float)acc[i][j][e] * xm) * wsn[j];
+                                  if (BIAS) t = t + bn[j];
+                                  return OUT == WF_BF16 ? __builtin_bit_cast(uint16_t, (__bf16)t)
+                                                        : __builtin_bit_cast(uint16_t, (_Float16)t);
+                              });
+    } else {
+#pragma unroll
+        for (int j = 0; j < WN; j++) {
+            const int n = nw + j * 32 + lr;
+            if (n >= N) continue;
+#pragma unroll
+            for (int i = 0; i < WM; i++) {
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int m = mw + i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
+                    if (m >= M) continue;
+                    const float t = ((float)acc[i][j][e] * xs[m]) * wsn[j];
+                    const int64_t o = (int64_t)m * N + n;
+                    const float g = __uint_as_float((uint32_t)res.gate[(int64_t)(m / res.rows_per_group) * N + n] << 16);
+                    const float r = __uint_as_float((uint32_t)res.resid[o] << 16);
+                    static_cast<__bf16*>(out)[o] = (__bf16)(r + g * (float)(__bf16)t);
+                }
+            }
+        }
+    }
+}
+
+template <int VM, int VN, int WM, int WN, int OUT>
+static void launch_wl_shape(const int8_t* A, const int8_t* B, const float* xs, const float* ws, const void* bias,
+                            void* out, int M, int N, int K, Residual r, bool resid, hipStream_t s) {
+    using S = WlShape<VM, VN, WM, WN>;
+    const int tiles = ((M + S::BM - 1) / S::BM) * ((N + S::BN - 1) / S::BN);
+    if (resid) gemm_i8_wl<S, OUT, false, true><<<dim3(tiles), S::NT, 0, s>>>(A, B, xs, ws, nullptr, out, M, N, K, r);
+    else if (bias) gemm_i8_wl<S, OUT, true, false><<<dim3(tiles), S::NT, 0, s>>>(A, B, xs, ws, bias, out, M, N, K, r);
+    else gemm_i8_wl<S, OUT, false, false><<<dim3(tiles), S::NT, 0, s>>>(A, B, xs, ws, bias, out, M, N, K, r);
+}
+
 // K % 64 == 0: the direct-to-LDS kernel in one of three tilings, chosen by the modelled time: rounds of 256 workgroups
 // (one per CU) times the tile's area, over the tiling's measured MFMA efficiency.
 //   256 x 320: 8 waves of 2 x 5 MFMA tiles (64 x 160); fewest LDS fragment reads per MFMA, and 4096 x 5120 outputs
@@ -443,7 +513,11 @@ static void launch_dl(const int8_t* A, const int8_t* B, const float* xs, const f
     const int64_t c128 = dl_cost(M, N, 256, 128, 780), c160 = dl_cost(M, N, 128, 160, 581);
     const int64_t best = std::min(std::min(c320, c256), std::min(c128, c160));
     if (c160 == best && K % 128 == 0) launch_dl_shape<4, 1, 1, 5, OUT, 128>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
-    else if (c160 == best) launch_dl_shape<4, 1, 1, 5, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
+    else if (K % 128 == 0) {
+        if (c128 == best) launch_wl_shape<2, 2, 4, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
+        else if (c256 == best) launch_wl_shape<2, 4, 4, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
+        else launch_wl_shape<4, 2, 2, 5, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
+    } else if (c160 == best) launch_dl_shape<4, 1, 1, 5, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
     else if (c128 == best) launch_dl_shape<2, 2, 4, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
     else if (c256 == best) launch_dl_shape<2, 4, 4, 2, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);
     else launch_dl_shape<4, 2, 2, 5, OUT>(A, B, xs, ws, bias, out, M, N, K, r, resid, s);

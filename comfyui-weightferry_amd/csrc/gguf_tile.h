@@ -1,5 +1,5 @@
-// Device helpers of the fused K-quant dequant + bf16 GEMM kernels (gemm_gguf.hip, gemm_gguf_tall.hip): the tile
-// order, the raw weight bytes of one dequantisation task of a 32-value stage (16, 8 or 4 values) through a buffer
+// Device helpers of the fused K-quant dequant + bf16 GEMM kernels (gemm_gguf.hip, gemm_gguf_tall.hip): the raw
+// weight bytes of one dequantisation task of a 32-value stage (16, 8 or 4 values) through a buffer
 // resource, and their dequantisation with the reference's rounding chain (MID, then bf16 -- enhancers/
 // gguf_dequant.py:195-224,250) into packed bf16 pairs.
 #pragma once
@@ -15,22 +15,6 @@ namespace wf {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-constexpr int kGroupMG = 8;
-
-// tile index of workgroup w among T tiles: XCD-aware (workgroup w runs on XCD w % 8, so one XCD's workgroups take
-// consecutive tiles and share their activation / weight rows in its L2), then groups of kGroupMG tile-rows
-__device__ __forceinline__ void tile_order(int w, int T, int ntm, int ntn, int& tm, int& tn) {
-    int L = w;
-    if ((T & 7) == 0) L = (w & 7) * (T >> 3) + (w >> 3);
-    const int per_group = kGroupMG * ntn;
-    const int group = L / per_group;
-    const int first_m = group * kGroupMG;
-    const int gm = min(ntm - first_m, kGroupMG);
-    const int in = L - group * per_group;
-    tm = first_m + in % gm;
-    tn = in / gm;
-}
 
 template <int QT>
 struct GGUFTs { static constexpr int TS = QT == 12 ? 144 : QT == 13 ? 176 : 210; };

@@ -1,6 +1,6 @@
 // Helpers of the GEMM kernels that stream operands global -> LDS with the load unit (buffer_load ... lds) through a
-// ring of LDS stages: buffer resources with zero fill past the end, the 16-byte LDS DMA, the 4-chunk row swizzle, a
-// barrier without the workgroup fence, and a compile-time loop.
+// ring of LDS stages: buffer resources with zero fill past the end, the 16-byte LDS DMA, the row swizzles, a barrier
+// without the workgroup fence, the XCD-aware tile order and a compile-time loop.
 #pragma once
 
 #include <type_traits>
@@ -65,6 +65,21 @@ template <int N>
 __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// tile index of workgroup w among T tiles: XCD-aware (workgroup w runs on XCD w % 8, so one XCD's workgroups take
+// consecutive tiles and share their operand rows in its L2), then groups of 8 tile-rows, column by column
+__device__ __forceinline__ void tile_order(int w, int T, int ntm, int ntn, int& tm, int& tn) {
+    constexpr int kGroupRows = 8;
+    int L = w;
+    if ((T & 7) == 0) L = (w & 7) * (T >> 3) + (w >> 3);
+    const int per_group = kGroupRows * ntn;
+    const int group = L / per_group;
+    const int first_m = group * kGroupRows;
+    const int gm = min(ntm - first_m, kGroupRows);
+    const int in = L - group * per_group;
+    tm = first_m + in % gm;
+    tn = in / gm;
 }
 
 // f(std::integral_constant<int, 0>{}), ..., f(std::integral_constant<int, N - 1>{}), unrolled at compile time

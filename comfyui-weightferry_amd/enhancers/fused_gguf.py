@@ -3,7 +3,8 @@
 The reference dequantises the weight (enhancers/gguf_dequant.py:296-326, one kernel into a bf16 weight in HBM)
 and ComfyUI-GGUF then runs torch.nn.functional.linear on it. ``linear`` does both in one kernel launch for bf16
 activations and a Q4_K / Q5_K / Q6_K weight, with the same dequantised values (dequant dtype MID, then the layer
-dtype) and float32 accumulation; mode="dequant" keeps the reference's two-step flow (wf_dequant, then F.linear);
+dtype) and float32 accumulation; mode="dequant" keeps the reference's two-step flow (wf_dequant, then the bf16 GEMM:
+the library's wf_linear_bf16 where it is the faster one, ``hand_gemm``, else torch.nn.functional.linear);
 mode="auto" (the default of GGUFLinear) picks whichever measured faster on MI355X for the layer's shape
 (``prefer_fused``). Anything else -- other formats, dtypes, CPU tensors -- returns None from ``fused_linear`` and
 ``linear`` takes the two-step flow."""
@@ -115,12 +116,50 @@ def prefer_fused(rows, qtype, n_out, k):
     return rows <= limit
 
 
+# The two-step flow's GEMM: the library's wf_linear_bf16 (whole 128-byte lines through two LDS stage buffers, 256 x 320
+# tiles at these sizes) against hipBLASLt's (torch.nn.functional.linear), ms per Wan-14B shape on MI355X:
+#   4096 rows: 5120 x 5120 0.165 against 0.176, 5120 x 13824 0.432 against 0.449, 13824 x 5120 0.459 against 0.404
+#              (704 tiles: 2.75 rounds of 256 workgroups) -- the block's six linears 1.546 against 1.549;
+#   2048 rows and fewer: 0.104-0.114 against 0.095 (5120 x 5120) -- 128 or fewer 256 x 320 tiles leave CUs idle;
+#   16384 rows: 0.640 against 0.562 (5120 x 5120), 6.07 against 5.47 per block -- hipBLASLt's stream-K kernel keeps
+#              its MFMA 83 % busy against 73 % here.
+# So wf_linear_bf16 takes the products whose 256 x 320 tiling gives one to three rounds of 256 workgroups.
+HAND_GEMM_TILES = (256, 768)
+
+
+def hand_gemm(rows, n_out):
+    """True when wf_linear_bf16 is the faster GEMM for a [rows, k] x [n_out, k]^T product on MI355X."""
+    tiles = -(-rows // 256) * -(-n_out // 320)
+    return HAND_GEMM_TILES[0] <= tiles <= HAND_GEMM_TILES[1]
+
+
+def bf16_linear(x, w, bias=None):
+    """y = x @ w.T (+ bias) by wf_linear_bf16 (bf16 in and out, float32 accumulation), or None when that kernel does
+    not take the case (dtypes, devices, K % 64, alignment)."""
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or not x.is_cuda or w.device != x.device or w.dim() != 2:
+        return None
+    n_out, k = w.shape
+    if x.dim() == 0 or x.shape[-1] != k or not w.is_contiguous():
+        return None
+    if bias is not None and (bias.dtype != torch.bfloat16 or bias.device != x.device or bias.numel() != n_out):
+        return None
+    x2 = x if x.dim() == 2 and x.is_contiguous() else x.reshape(-1, k).contiguous()
+    b = bias if bias is None or bias.is_contiguous() else bias.contiguous()
+    y = torch.empty((x2.shape[0], n_out), dtype=torch.bfloat16, device=x.device)
+    with _native.on_device(x.device):
+        rc = _native.lib().wf_linear_bf16(x2.data_ptr(), w.data_ptr(), b.data_ptr() if b is not None else None,
+                                          y.data_ptr(), x2.shape[0], n_out, k, _native.stream_of(x.device))
+    if not _native.check(rc, "wf_linear_bf16"):
+        return None
+    return y if x.dim() == 2 else y.reshape(*x.shape[:-1], n_out)
+
+
 def linear(x, data, qtype, oshape, bias=None, mid_dtype=None, mode="auto"):
     """The layer's forward: the fused kernel when it takes the case (mode "fused", or "auto" where it is the faster
-    one), else the reference's flow -- the weight dequantised to x's dtype (wf_dequant), then
-    torch.nn.functional.linear."""
+    one), else the reference's flow -- the weight dequantised to x's dtype (wf_dequant), then the bf16 GEMM
+    (wf_linear_bf16 where ``hand_gemm`` says it is the faster one, else torch.nn.functional.linear)."""
+    rows = x.numel() // max(1, x.shape[-1]) if x.dim() else 0
     if mode == "auto":
-        rows = x.numel() // max(1, x.shape[-1]) if x.dim() else 0
         mode = "fused" if prefer_fused(rows, qtype, oshape[0], oshape[1]) else "dequant"
     if mode == "fused":
         y = fused_linear(x, data, qtype, oshape, bias, mid_dtype)
@@ -129,6 +168,10 @@ def linear(x, data, qtype, oshape, bias=None, mid_dtype=None, mode="auto"):
     w = gguf_dequant.dequantize(data, qtype, oshape, mid_dtype, x.dtype)
     if w is None:
         raise ValueError(f"GGML type {qtype} with shape {tuple(oshape)} is not handled on this path")
+    if hand_gemm(rows, int(oshape[0])):
+        y = bf16_linear(x, w, bias)
+        if y is not None:
+            return y
     return torch.nn.functional.linear(x, w, bias)
 
 

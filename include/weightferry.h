@@ -134,6 +134,14 @@ int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const void* wq, 
 int wf_linear_gguf_noalloc(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes, int qtype,
                            int64_t N, const void* bias_bf16, void* out_bf16, int mid_dt, void* stream);
 
+/* y[m, n] = bf16(sum_k x[m, k] * w[n, k] (+ bias[n])), float32 accumulation: the GEMM of the two-step flow, after
+ * wf_dequant -- replaces ComfyUI-GGUF's torch.nn.functional.linear on the weight that `dequantize`
+ * (enhancers/gguf_dequant.py:296-326) returns. x: bf16 [M, K], w: bf16 [N, K], both 16-byte aligned; bias: bf16 [N]
+ * or NULL; out: bf16 [M, N]. K % 64 == 0 and M * K, N * K < 2^30, else WF_EUNSUPPORTED (the caller's own GEMM runs).
+ * Tiles of 256 x 320, 256 x 256, 256 x 128 or 128 x 160 outputs, whichever fills the chip best. */
+int wf_linear_bf16(const void* x_bf16, const void* w_bf16, const void* bias_bf16, void* out_bf16, int64_t M, int64_t N,
+                   int64_t K, void* stream);
+
 /* ---------------------------------------------------------------------------------------- block streaming
  * Exact-size page-locked host memory: replaces PinnedHost's cudaHostRegister / cudaHostUnregister
  * (core/tiers/pinned.py:84-129); allocated page-locked (hipHostMalloc) instead of registered after the fact. */

@@ -70,6 +70,27 @@ def test_dequant_add_argument_checks_without_gpu():
     assert lib.wf_dequant_add(None, 0, 0, 0, 1, None, 0.5, None, 0, None) == native.OK
 
 
+def test_bf16_gemm_argument_checks_without_gpu():
+    native = sub("_native")
+    lib = native.lib()
+    buf = ctypes.create_string_buffer(4096)
+    p16 = (ctypes.addressof(buf) + 15) // 16 * 16
+    # K a whole number of 64-value stages, 16-byte aligned operands: else "not my case" (the caller's GEMM runs)
+    assert lib.wf_linear_bf16(p16, p16, None, p16, 4, 4, 96, None) == native.EUNSUPPORTED
+    assert "64" in native.last_error()
+    assert lib.wf_linear_bf16(p16 + 2, p16, None, p16, 4, 4, 64, None) == native.EUNSUPPORTED
+    assert lib.wf_linear_bf16(p16, p16 + 8, None, p16, 4, 4, 64, None) == native.EUNSUPPORTED
+    assert lib.wf_linear_bf16(p16, p16, None, p16 + 1, 4, 4, 64, None) == native.EUNSUPPORTED
+    # operands past the buffer resources' byte range
+    assert lib.wf_linear_bf16(p16, p16, None, p16, 1 << 24, 4, 64, None) == native.EUNSUPPORTED
+    assert lib.wf_linear_bf16(p16, p16, None, p16, 4, 1 << 24, 64, None) == native.EUNSUPPORTED
+    # malformed sizes, null pointers; nothing to do
+    assert lib.wf_linear_bf16(p16, p16, None, p16, -1, 4, 64, None) == native.EINVAL
+    assert lib.wf_linear_bf16(p16, p16, None, p16, 4, 4, 0, None) == native.EINVAL
+    assert lib.wf_linear_bf16(None, p16, None, p16, 4, 4, 64, None) == native.EINVAL
+    assert lib.wf_linear_bf16(p16, p16, None, p16, 0, 4, 64, None) == native.OK
+
+
 def test_check_maps_codes():
     native = sub("_native")
     assert native.check(native.OK, "x") is True

@@ -282,17 +282,21 @@ def test_pending_input_quantised_with_its_operation(native, kind, K):
     assert np.array_equal(_bits(y.reshape(-1, 640)), expect)
 
 
-@pytest.mark.parametrize("M,N,K", [(4000, 5000, 512), (4000, 4992, 512), (1024, 5000, 512), (1000, 5120, 512),
+@pytest.mark.parametrize("M,N,K", [(4000, 5000, 512), (4000, 4992, 512), (4000, 5000, 640), (4000, 4992, 128),
+                                   (4000, 5000, 576), (3000, 3000, 384), (2000, 4000, 640),
+                                   (1024, 5000, 512), (1000, 5120, 512),
                                    (1000, 5120, 576), (1024, 4992, 128), (1000, 5000, 640), (1024, 5120, 896),
                                    (4096, 8192, 80), (300, 1000, 208)])
 def test_tilings_bias_and_residual_whole_output(native, M, N, K):
-    # 4000 x N outputs take the 256 x 320 tiling (one round of 256 workgroups), 1024 x 5000 and 1000 x 5120 the
-    # 128 x 160 one (256 tiles); N = 5000 leaves a partial last tile and an odd row length (element stores), N = 4992
-    # and 5120 whole 16-byte runs, M = 1000 a partial last tile-row. The 128 x 160 tiling streams 128-byte K stages
-    # when K % 128 == 0 (K = 128: one stage; 512: whole rounds of the 4-stage ring; 640 and 896: one and three
-    # stages after them) and 64-byte stages otherwise (K = 576). K % 64 != 0 takes the register-staged kernel:
-    # 256 x 256 tiles for 4096 x 8192 (512 of them), 128 x 128 for 300 x 1000. Every element of the bias and the
-    # residual forms against the float32 epilogue in the kernel's order on an exact accumulator (|acc| <= 896 *
+    # 4000 x N outputs take the 256 x 320 tiling (one round of 256 workgroups), 3000 x 3000 the 256 x 256 one,
+    # 2000 x 4000 the 256 x 128 one, 1024 x 5000 and 1000 x 5120 the 128 x 160 one (256 tiles); N = 5000 leaves a
+    # partial last tile and an odd row length (element stores), N = 4992 and 5120 whole 16-byte runs, M = 1000 a
+    # partial last tile-row. With K % 128 == 0 the 256-row tilings stream whole 128-byte lines through two stage
+    # buffers (K = 128: one stage; 512: two whole pairs; 384 and 640: an odd last stage) and the 128 x 160 tiling
+    # 128-byte stages through its 4-stage ring (128: one stage; 512: whole rounds of the ring; 640 and 896: one and
+    # three stages after them); K = 576 takes the 64-byte ring in both. K % 64 != 0 takes the register-staged
+    # kernel: 256 x 256 tiles for 4096 x 8192 (512 of them), 128 x 128 for 300 x 1000. Every element of the bias and
+    # the residual forms against the float32 epilogue in the kernel's order on an exact accumulator (|acc| <= 896 *
     # 127^2 < 2^24).
     G = 4
     g = torch.Generator().manual_seed(N + M)
