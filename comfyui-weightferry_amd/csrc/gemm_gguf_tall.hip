@@ -22,16 +22,18 @@
 
 namespace wf {
 
-// raw bytes of an 8-value task
-struct Q6Raw8 { uint2 ql, qh; uint32_t sc, d; };
-
 typedef uint32_t u32x3t __attribute__((ext_vector_type(3)));
 
-// 8 bytes at an even offset o: one 12-byte load from the aligned-down dword, funnel-shifted (the window
-// [o & ~3, +12) ends at most 4 bytes past o + 8, inside the block for every piece loaded here)
-__device__ __forceinline__ uint2 ld8_even_rs(__amdgpu_buffer_rsrc_t r, uint32_t o) {
-    const u32x3t v = __builtin_bit_cast(u32x3t, __builtin_amdgcn_raw_buffer_load_b96(r, o & ~3u, 0, 0));
-    return funnel8(v[0], v[1], v[2], (o & 3u) * 8u);
+// raw bytes of an 8-value task: the ql and qh pieces as the 12-byte windows that hold them, and the pieces' byte
+// offset in their windows (the same for both) in bits
+struct Q6Raw8 { u32x3t ql, qh; uint32_t sh, sc, d; };
+
+// the 12-byte window of 8 bytes at an even offset o: one load from the aligned-down dword (the window [o & ~3, +12)
+// ends at most 4 bytes past o + 8, inside the block for every piece loaded here). The 8 bytes are funnel-shifted out
+// of it where they are dequantised, after the wait for the load: a shift right behind the load would make the wave
+// wait for it there.
+__device__ __forceinline__ u32x3t ld8_window(__amdgpu_buffer_rsrc_t r, uint32_t o) {
+    return __builtin_bit_cast(u32x3t, __builtin_amdgcn_raw_buffer_load_b96(r, o & ~3u, 0, 0));
 }
 
 // Raw bytes of values [8 e, 8 e + 8) of sub-block G of the Q6_K super-block at byte offset b, at phase G, v0 = 32 G +
@@ -41,8 +43,9 @@ __device__ __forceinline__ uint2 ld8_even_rs(__amdgpu_buffer_rsrc_t r, uint32_t 
 template <int G>
 __device__ __forceinline__ void q6_load8(__amdgpu_buffer_rsrc_t r, uint32_t b, int e, Q6Raw8& w) {
     constexpr uint32_t hh = G >> 2;
-    w.ql = ld8_even_rs(r, b + 64 * hh + 32 * (G & 1) + 8 * e);
-    if constexpr ((G & 3) == 0) w.qh = ld8_even_rs(r, b + 128 + 32 * hh + 8 * e);
+    w.ql = ld8_window(r, b + 64 * hh + 32 * (G & 1) + 8 * e);
+    if constexpr ((G & 3) == 0) w.qh = ld8_window(r, b + 128 + 32 * hh + 8 * e);
+    w.sh = (b & 3u) * 8u;                              // (both pieces sit a multiple of 4 bytes past b)
     w.sc = __builtin_amdgcn_raw_buffer_load_b8(r, b + 192 + 2 * G + (e >> 1), 0, 0);
     if constexpr (G == 0) w.d = __builtin_amdgcn_raw_buffer_load_b16(r, b + 208, 0, 0);
 }
@@ -51,9 +54,10 @@ __device__ __forceinline__ void q6_load8(__amdgpu_buffer_rsrc_t r, uint32_t b, i
 template <int MID, int g>
 __device__ __forceinline__ void q6_dequant8(const Q6Raw8& w, uint32_t (&o)[4]) {
     const uint32_t ns = 4u * (uint32_t)((g & 3) >> 1), hs = 2u * (uint32_t)(g & 3);
+    const uint2 ql = funnel8(w.ql[0], w.ql[1], w.ql[2], w.sh), qh = funnel8(w.qh[0], w.qh[1], w.qh[2], w.sh);
     uint32_t code[2];
-    code[0] = ((w.ql.x >> ns) & 0x0f0f0f0fu) | (((w.qh.x >> hs) & 0x03030303u) << 4);
-    code[1] = ((w.ql.y >> ns) & 0x0f0f0f0fu) | (((w.qh.y >> hs) & 0x03030303u) << 4);
+    code[0] = ((ql.x >> ns) & 0x0f0f0f0fu) | (((qh.x >> hs) & 0x03030303u) << 4);
+    code[1] = ((ql.y >> ns) & 0x0f0f0f0fu) | (((qh.y >> hs) & 0x03030303u) << 4);
     const int sc = (int8_t)(w.sc & 0xffu);
     const uint32_t dbits = w.d & 0xffffu;
     if constexpr (MID == WF_F16) {
@@ -110,12 +114,15 @@ __global__ __launch_bounds__(512) void gemm_gguf_tall(const uint16_t* __restrict
     // swizzle depends on r's bits 0-3: on l / 8, and through bit 3 on the run's parity, which flips bit 2 of the chunk
     // (bit 6 of the byte offset; the row part, a multiple of 2 K bytes, has bits 0-8 clear): xlane ^ 64 for odd runs
     const uint32_t xlane = (uint32_t)(lane >> 3) * (uint32_t)K * 2u + 16u * (uint32_t)swz8(lane >> 3, lane & 7);
+    const uint32_t xlane_odd = xlane ^ 64u;
+    // (the wave-uniform part of each offset is summed in a scalar register at each issue: kept apart from the lane
+    // part, the compiler would hold IXP lane offsets across the loop and spill them)
     auto issue_pair = [&](uint4* st, int p) {
 #pragma unroll
         for (int q = 0; q < IXP; q++) {
             const int run = wave * IXP + q;                // IXP even: run parity = q parity
-            lds_dma16(rx, st + 64 * run,
-                      (xlane ^ (q & 1 ? 64u : 0u)) + (uint32_t)(run * 8) * (uint32_t)K * 2u + (uint32_t)p * 128u);
+            const uint32_t sofs = __builtin_amdgcn_readfirstlane((uint32_t)(run * 8) * (uint32_t)K * 2u + (uint32_t)p * 128u);
+            lds_dma16(rx, st + 64 * run, (q & 1 ? xlane_odd : xlane) + sofs);
         }
     };
     // dequantisation tasks: 8 values (e = t % 4) of row t / 4; waves 0-3 also 4 values (qq = t % 8) of row
@@ -181,16 +188,19 @@ __global__ __launch_bounds__(512) void gemm_gguf_tall(const uint16_t* __restrict
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;
     using P2 = std::integral_constant<int, 2>;
-    uint4* wcur = wring;                               // stage s
-    uint4* wnxt = wring + WSLOT;                       // stage s + 1
-    uint4* wnew = wring + 2 * WSLOT;                   // stage s + 2 (stage s - 1's slot)
+    // weight ring slots as indices, the pointers formed at each use: reads through a pointer carried around the loop
+    // have no known object, and the compiler then waits for every LDS DMA in flight before each of them
+    int wcur = 0;                                      // stage s
+    int wnxt = 1;                                      // stage s + 1
+    int wnew = 2;                                      // stage s + 2 (stage s - 1's slot)
+    auto wslot = [&](int i) { return wring + i * WSLOT; };
     issue_pair(xp0, 0);
     wload(P0{}, 0);
     wait_vm<0>();
-    wstore(P0{}, wcur, 0);
+    wstore(P0{}, wslot(wcur), 0);
     wload(P1{}, 1);
     wait_vm<0>();
-    wstore(P1{}, wnxt, 1);
+    wstore(P1{}, wslot(wnxt), 1);
     wload(P2{}, 2);
     __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));   // lgkmcnt(0): this thread's LDS writes are done
     // Step s = kt + J of pair p = s / 2 (pair slot xc; the other slot xo): J even -- barrier (pair p has landed for
@@ -207,20 +217,21 @@ __global__ __launch_bounds__(512) void gemm_gguf_tall(const uint16_t* __restrict
         wave_barrier_sync();
         if constexpr (h == 0) {
             issue_pair(xo, (s >> 1) + 1);
-            fread(xc, wcur, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);         // the loads leave now, not where the scheduler would sink them
+            fread(xc, wslot(wcur), 0, 0, 0);
         }
-        fread(xc, wcur, h, 1, 1);
+        fread(xc, wslot(wcur), h, 1, 1);
         mfmas(0);
         mfmas(1);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (h == 0) wait_vm<IXP>();         // all but this step's pair loads have landed
         else wait_vm<0>();
         __builtin_amdgcn_sched_barrier(0);
-        wstore(G2{}, wnew, s + 2);
+        wstore(G2{}, wslot(wnew), s + 2);
         __builtin_amdgcn_sched_barrier(0);             // the next loads reuse the raw registers
         wload(G3{}, s + 3);
-        if constexpr (h == 0) fread(xc, wnxt, 1, 0, 0);
-        uint4* t = wcur;
+        if constexpr (h == 0) fread(xc, wslot(wnxt), 1, 0, 0);
+        const int t = wcur;
         wcur = wnxt;
         wnxt = wnew;
         wnew = t;
