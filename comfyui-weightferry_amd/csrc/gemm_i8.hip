@@ -48,6 +48,30 @@ struct Residual {
     int rows_per_group;
 };
 
+// The per-row activation scales of a wave's R = 32 WM output rows from row mw: lane l loads xs[mw + l] (and
+// xs[mw + 64 + l] for R = 128), one load each; row(ro) gives any lane the scale of row mw + ro by a lane permute
+// (ds_bpermute). A global load per output element instead left each tile's epilogue waiting on 16-32 loads in
+// turn. Rows at or past M read as zero (their outputs are not stored).
+template <int WM>
+struct RowScales {
+    static constexpr int T = (WM * 32 + 63) / 64;
+    float v[T];
+    __device__ __forceinline__ RowScales(const float* __restrict__ xs, int mw, int M, int lane) {
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            const int m = mw + 64 * t + lane;
+            v[t] = m < M ? xs[m] : 0.0f;
+        }
+    }
+    __device__ __forceinline__ float row(int ro) const {
+        float x = v[0];
+#pragma unroll
+        for (int t = 1; t < T; t++)
+            if ((ro >> 6) == t) x = v[t];
+        return __shfl(x, ro & 63);
+    }
+};
+
 template <int WM, int WN, int OUT, bool BIAS, bool RESID = false>
 __global__ __launch_bounds__(256) void gemm_i8(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
                                                const float* __restrict__ xs, const float* __restrict__ ws,
@@ -318,6 +342,7 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
         i32x4* buf = wb == 0 ? st0 : wb == 1 ? st1 : wb == 2 ? st2 : st3;
         uint16_t* ot = reinterpret_cast<uint16_t*>(buf) + (wave % PER_BUF) * TR * TC;
         const int mw = m0 + wm * TR, nw = n0 + wn * TC;
+        const RowScales<WM> rs(xs, mw, M, lane);
 #pragma unroll
         for (int j = 0; j < WN; j++) {
             const int n = nw + j * 32 + lr;
@@ -330,7 +355,7 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
                     const int r0 = i * 32 + 8 * q + 4 * lk;    // rows r0 .. r0 + 3 of this wave's tile
                     float xm[4];
 #pragma unroll
-                    for (int e = 0; e < 4; e++) xm[e] = mw + r0 + e < M ? xs[mw + r0 + e] : 0.0f;
+                    for (int e = 0; e < 4; e++) xm[e] = rs.row(r0 + e);
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
                         float t = ((float)acc[i][j][4 * q + e] * xm[e]) * wsn;
@@ -368,19 +393,23 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
         return;
     }
     // the residual form: element stores
+    // (every lane reaches each row permute: a lane that skipped it would hand a zero to the lanes reading its row)
+    const RowScales<WM> rs(xs, m0 + wm * WM * 32, M, lane);
 #pragma unroll
     for (int j = 0; j < WN; j++) {
         const int n = n0 + wn * WN * 32 + j * 32 + lr;
-        if (n >= N) continue;
-        const float wsn = ws[n];
-        const float bn = BIAS ? to_f32_out(bias, n, OUT) : 0.0f;
+        const bool in_n = n < N;
+        const float wsn = in_n ? ws[n] : 0.0f;
+        const float bn = BIAS && in_n ? to_f32_out(bias, n, OUT) : 0.0f;
 #pragma unroll
         for (int i = 0; i < WM; i++) {
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                const int m = m0 + wm * WM * 32 + i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
-                if (m >= M) continue;
-                float t = ((float)acc[i][j][e] * xs[m]) * wsn;
+                const int ro = i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
+                const int m = m0 + wm * WM * 32 + ro;
+                const float xm = rs.row(ro);
+                if (!in_n || m >= M) continue;
+                float t = ((float)acc[i][j][e] * xm) * wsn;
                 if (BIAS) t = t + bn;
                 const int64_t o = (int64_t)m * N + n;
                 if constexpr (RESID) {
@@ -439,28 +468,30 @@ __global__ __launch_bounds__(S::NT) void gemm_i8_wl(const int8_t* __restrict__ A
         wsn[j] = n < N ? ws[n] : 0.0f;
         bn[j] = BIAS && n < N ? to_f32_out(bias, n, OUT) : 0.0f;
     }
+    const RowScales<WM> rs(xs, mw, M, lane);
     if constexpr (!RESID) {
         wl_store_tile<WM, WN>(wl_out_region<S>(sb0, sb1, wave), static_cast<uint16_t*>(out), M, N, mw, nw, lane,
                               [&](int i, int j, int e) {
-                                  const int m = mw + i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
-                                  const float xm = m < M ? xs[m] : 0.0f;
+                                  const float xm = rs.row(i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3));
                                   float t = ((float)acc[i][j][e] * xm) * wsn[j];
                                   if (BIAS) t = t + bn[j];
                                   return OUT == WF_BF16 ? __builtin_bit_cast(uint16_t, (__bf16)t)
                                                         : __builtin_bit_cast(uint16_t, (_Float16)t);
                               });
     } else {
+        // (every lane reaches each row permute: a lane that skipped it would hand a zero to the lanes reading its row)
 #pragma unroll
         for (int j = 0; j < WN; j++) {
             const int n = nw + j * 32 + lr;
-            if (n >= N) continue;
 #pragma unroll
             for (int i = 0; i < WM; i++) {
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
-                    const int m = mw + i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
-                    if (m >= M) continue;
-                    const float t = ((float)acc[i][j][e] * xs[m]) * wsn[j];
+                    const int ro = i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
+                    const int m = mw + ro;
+                    const float xm = rs.row(ro);
+                    if (n >= N || m >= M) continue;
+                    const float t = ((float)acc[i][j][e] * xm) * wsn[j];
                     const int64_t o = (int64_t)m * N + n;
                     const float g = __uint_as_float((uint32_t)res.gate[(int64_t)(m / res.rows_per_group) * N + n] << 16);
                     const float r = __uint_as_float((uint32_t)res.resid[o] << 16);
