@@ -287,7 +287,7 @@ def streaming_leg(torch, native, n_blocks=40, steps=10):
                          "compute_ms": prof["streamed_compute_ms"],
                          "hidden_fraction": prof["overlap_ratio"], "dma_gbps": prof["dma_gbps"],
                          "hidden_fraction_bound": round(min(1.0, prof["streamed_compute_ms"] / prof["dma_ms"]), 4)},
-            "linears": "GGUFLinear mode auto: wf_dequant + torch bf16 GEMM at 4096 and 512 rows"}
+            "linears": "GGUFLinear mode auto: wf_dequant + wf_linear_bf16 at 4096 rows, the fused panel form at 512 rows"}
 
 
 def chunk_leg(torch, native, n_blocks=40, steps=5, chunk_mb=96, slots=4):
