@@ -75,10 +75,6 @@ static int64_t bf16_cost(int64_t M, int64_t N, int bm, int bn, int64_t eff) {
     return (tiles + 255) / 256 * bm * bn * 1000 / eff;
 }
 
-#ifndef WF_BF16_FORM
-#define WF_BF16_FORM (-1)
-#endif
-
 // 256 x 320 (8 waves of 2 x 5 MFMA tiles), 256 x 256 (8 waves of 4 x 2), 256 x 128 (4 waves of 4 x 2) or 128 x 160
 // (4 waves of 1 x 5), by modelled time
 static void run_bf16(const uint16_t* A, const uint16_t* B, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
@@ -86,8 +82,7 @@ static void run_bf16(const uint16_t* A, const uint16_t* B, const uint16_t* bias,
     const int64_t c320 = bf16_cost(M, N, 256, 320, 1000), c256 = bf16_cost(M, N, 256, 256, 900);
     const int64_t c128 = bf16_cost(M, N, 256, 128, 700), c160 = bf16_cost(M, N, 128, 160, 650);
     const int64_t best = std::min(std::min(c320, c256), std::min(c128, c160));
-    int form = best == c320 ? 0 : best == c256 ? 1 : best == c128 ? 2 : 3;
-    if (WF_BF16_FORM >= 0) form = WF_BF16_FORM;
+    const int form = best == c320 ? 0 : best == c256 ? 1 : best == c128 ? 2 : 3;
     switch (form) {
     case 0: launch_bf16<4, 2, 2, 5>(A, B, bias, Y, M, N, K, s); break;
     case 1: launch_bf16<2, 4, 4, 2>(A, B, bias, Y, M, N, K, s); break;
