@@ -52,3 +52,43 @@ def test_auto_routes_by_rows(monkeypatch):
     assert calls == ["fused", "dequant", "fused", "dequant"]
     layer = fg.GGUFLinear(256, 32, 12, bias=False)
     assert layer.mode == "auto"
+
+
+def test_hand_gemm_rule():
+    # the library's bf16 GEMM takes products whose 256 x 320 tiling gives one to three rounds of 256 workgroups
+    assert fg.hand_gemm(4096, 5120) and fg.hand_gemm(4096, 13824) and fg.hand_gemm(8192, 5120)
+    assert fg.hand_gemm(4096, 15360)                       # 768 tiles: three rounds
+    assert not fg.hand_gemm(2048, 5120)                    # 128 tiles: half the chip idle
+    assert not fg.hand_gemm(4096, 16000)                   # 800 tiles
+    assert not fg.hand_gemm(16384, 5120) and not fg.hand_gemm(8192, 13824)
+
+
+def test_bf16_linear_declines_what_its_kernel_does_not_take():
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    w = torch.zeros(8, 64, dtype=torch.bfloat16)
+    assert fg.bf16_linear(x, w) is None                    # CPU tensors
+    assert fg.bf16_linear(x.float(), w) is None
+    assert fg.bf16_linear(x, w.half()) is None
+
+
+def test_two_step_routes_its_gemm(monkeypatch):
+    calls = []
+
+    def fake_dequant(data, qtype, oshape, mid_dtype=None, out_dtype=None):
+        return torch.zeros(oshape, dtype=out_dtype)
+
+    def fake_hand(x, w, bias=None):
+        calls.append("hand")
+        return torch.zeros(*x.shape[:-1], w.shape[0], dtype=x.dtype)
+
+    def fake_torch(x, w, bias=None):
+        calls.append("torch")
+        return torch.zeros(*x.shape[:-1], w.shape[0], dtype=x.dtype)
+
+    monkeypatch.setattr(fg.gguf_dequant, "dequantize", fake_dequant)
+    monkeypatch.setattr(fg, "bf16_linear", fake_hand)
+    monkeypatch.setattr(fg.torch.nn.functional, "linear", fake_torch)
+    data = torch.zeros(16, dtype=torch.uint8)
+    fg.linear(torch.zeros(1, 4096, 256, dtype=torch.bfloat16), data, 12, (5120, 256), mode="dequant")
+    fg.linear(torch.zeros(1, 2048, 256, dtype=torch.bfloat16), data, 12, (5120, 256), mode="dequant")
+    assert calls == ["hand", "torch"]
