@@ -262,8 +262,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <int QT>
 struct SkRaw;
-template <> struct SkRaw<12> { uint4 hdr; uint2 q[4]; };
-template <> struct SkRaw<13> { uint4 hdr; uint2 q[4]; uint2 qh; };
+// (the 16-byte header as two 8-byte halves: loaded as one 16-byte tuple into the second of two register sets, it
+// landed in temporaries the compiler copied out right after the load, the wave waiting for the load there)
+template <> struct SkRaw<12> { uint2 h01, h23; uint2 q[4]; };
+template <> struct SkRaw<13> { uint2 h01, h23; uint2 q[4]; uint2 qh; };
 template <> struct SkRaw<14> { uint2 ql[4], qh[2]; uint32_t sc[4]; uint32_t d; };
 
 // bytes [o, o + 8) of the block stream at p (o even): aligned dwords funnel-shifted, inside [o - 2, o + 8)
@@ -280,7 +282,8 @@ template <int QT>
 __device__ __forceinline__ void sk_load(const uint8_t* b, int kq, SkRaw<QT>& w) {
     if constexpr (QT == 12 || QT == 13) {
         constexpr int QS = QT == 12 ? 16 : 48;
-        w.hdr = *reinterpret_cast<const uint4*>(b);
+        w.h01 = *reinterpret_cast<const uint2*>(b);
+        w.h23 = *reinterpret_cast<const uint2*>(b + 8);
 #pragma unroll
         for (int p = 0; p < 4; p++) w.q[p] = *reinterpret_cast<const uint2*>(b + QS + 32 * p + 8 * kq);
         if constexpr (QT == 13) w.qh = *reinterpret_cast<const uint2*>(b + 16 + 8 * kq);
@@ -347,10 +350,10 @@ __device__ __forceinline__ bf16x8 sk_dequant(const SkRaw<QT>& w, int kq) {
             code[1] |= ((w.qh.y >> g) & 0x01010101u) << 4;
         }
         uint32_t sc, m;
-        scale_min(w.hdr.y, w.hdr.z, w.hdr.w, g, sc, m);
+        scale_min(w.h01.y, w.h23.x, w.h23.y, g, sc, m);
         if constexpr (MID == WF_F16) {
             const h2 off = h2s(-1024.0f);
-            const h2 pr = as_h2(w.hdr.x) * (as_h2(sc | (m << 16) | 0x64006400u) + off);   // (d * sc, dmin * m)
+            const h2 pr = as_h2(w.h01.x) * (as_h2(sc | (m << 16) | 0x64006400u) + off);   // (d * sc, dmin * m)
             const h2 ds = lo2(pr), dm = hi2(pr);
 #pragma unroll
             for (int i = 0; i < 2; i++) {
@@ -359,8 +362,8 @@ __device__ __forceinline__ bf16x8 sk_dequant(const SkRaw<QT>& w, int kq) {
                 o[2 * i + 1] = pack_bf16((float)v1[0], (float)v1[1]);
             }
         } else {
-            const float d = round_to<MID>(f16_bits_to_f32(w.hdr.x & 0xffffu));
-            const float dmin = round_to<MID>(f16_bits_to_f32(w.hdr.x >> 16));
+            const float d = round_to<MID>(f16_bits_to_f32(w.h01.x & 0xffffu));
+            const float dmin = round_to<MID>(f16_bits_to_f32(w.h01.x >> 16));
             const float ds = round_to<MID>(d * (float)sc), dm = round_to<MID>(dmin * (float)m);
 #pragma unroll
             for (int i = 0; i < 2; i++) {
