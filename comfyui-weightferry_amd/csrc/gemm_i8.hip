@@ -392,8 +392,10 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
         }
         return;
     }
-    // the residual form: element stores
+    // the residual form: element stores, once the ring's last loads (stages past K among them) have landed -- no
+    // copy into this workgroup's LDS may outlive it
     // (every lane reaches each row permute: a lane that skipped it would hand a zero to the lanes reading its row)
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
     const RowScales<WM> rs(xs, m0 + wm * WM * 32, M, lane);
 #pragma unroll
     for (int j = 0; j < WN; j++) {
