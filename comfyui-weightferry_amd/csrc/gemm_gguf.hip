@@ -541,6 +541,142 @@ __global__ __launch_bounds__(64 * NW) void gemm_gguf_skinny(const uint16_t* __re
     }
 }
 
+// ------------------------------------------------------------- few activation rows, whole rows per CU (M <= 4)
+// gemm_gguf_skinny gives each workgroup 32 whole weight rows: 160 workgroups for a 5120-wide output on 256 CUs, which
+// at one or two rows are bound by the dequantisation's VALU issue (each weight value is dequantised for one or two
+// products). Here workgroup b of G takes the row quads [Qt b / G, Qt (b + 1) / G) (Qt = N / 4 quads of 4 weight
+// rows): 20 whole rows of a 5120-wide output on each of 256 CUs. The 16 columns of v_mfma_f32_16x16x32_bf16 hold 4 weight rows x 4 parts of K (column c = 4 j + h: row
+// j of the quad, part h = super-blocks [h S, h S + S), S = nsb / 4 rounded up), its 16 rows the M <= 4 activation
+// rows x the same 4 parts (row a = 4 t + h: activation row t over part h), so one step multiplies super-block
+// h S + s of every part at once and the wanted sums are the diagonal blocks D[4 t + h][4 j + h]: lane (c, kq) keeps
+// register h = c % 4 (activation row t = kq), and the 4 parts are added across lanes c ^ 1, c ^ 2. Each lane
+// dequantises its 8 values straight into its B fragment as in the few-rows kernel. Unit (quad, s) = one step over
+// super-block s of the 4 parts; a workgroup's units (quad-major) are spread evenly over its NW waves, each wave
+// streaming its range with the raw bytes two units ahead and the unit's 8 activation fragments one unit ahead. A
+// wave's sums for a quad go to LDS (red[quad][wave][4 t + j], zero where a wave has no share) and are added in wave
+// order after the barrier: no partial sums leave the workgroup. Weight and activation bytes come through buffer
+// resources; parts past K, rows past N and activation rows past M take an offset past the resource's end and read
+// as zeros.
+constexpr int kQdMaxQuads = 8;           // row quads per workgroup: N <= 8192 on 256 workgroups
+constexpr int kQdWaves = 4;              // one wave per SIMD (two measured slower: half the units per wave)
+constexpr uint32_t kQdNowhere = 0x80000000u;
+
+__device__ __forceinline__ uint2 ld64(__amdgpu_buffer_rsrc_t r, uint32_t o) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, o, 0, 0));
+}
+
+// sk_load's bytes through a buffer resource (o: the super-block's byte offset, or kQdNowhere for zeros)
+template <int QT>
+__device__ __forceinline__ void sk_load_rs(__amdgpu_buffer_rsrc_t r, uint32_t o, int kq, SkRaw<QT>& w) {
+    constexpr int QS = QT == 12 ? 16 : 48;
+    w.h01 = ld64(r, o);
+    w.h23 = ld64(r, o + 8);
+#pragma unroll
+    for (int p = 0; p < 4; p++) w.q[p] = ld64(r, o + QS + 32 * p + 8 * kq);
+    if constexpr (QT == 13) w.qh = ld64(r, o + 16 + 8 * kq);
+}
+
+template <int QT, int MID, bool BIAS>
+__global__ __launch_bounds__(64 * kQdWaves) void gemm_gguf_quad(const uint16_t* __restrict__ X,
+                                                          const uint8_t* __restrict__ W,
+                                                          const uint16_t* __restrict__ bias,
+                                                          uint16_t* __restrict__ Y, int M, int N, int K, int G) {
+    constexpr int TS = GGUFTs<QT>::TS, NW = kQdWaves;
+    __shared__ float red[kQdMaxQuads][NW][16];
+    const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, kq = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = c & 3, jt = c >> 2;                 // part; quad row (B) and activation row (A) of this lane
+    const int nsb = K / 256, S = (nsb + 3) / 4;
+    const int Qt = (N + 3) / 4;
+    const int q0 = (int)((int64_t)Qt * blockIdx.x / G), nq = (int)((int64_t)Qt * (blockIdx.x + 1) / G) - q0;
+    const int nu = nq * S;
+    const int lo = nu * wave / NW, hi = nu * (wave + 1) / NW;
+    for (int i = tid; i < kQdMaxQuads * NW * 16; i += 64 * NW) (&red[0][0][0])[i] = 0.0f;
+    const uint32_t row_bytes = (uint32_t)nsb * TS;
+    const __amdgpu_buffer_rsrc_t rw = tile_rsrc(W, (int64_t)N * row_bytes);
+    const __amdgpu_buffer_rsrc_t rx = tile_rsrc(X, (int64_t)M * K * 2);
+    // this lane's byte offsets of unit (quad lq of the workgroup's, step ls): weight row 4 (q0 + lq) + jt,
+    // super-block h S + ls; activation row jt over the same super-block
+    auto wofs = [&](int lq, int ls) {
+        const int row = 4 * (q0 + lq) + jt, sb = h * S + ls;
+        return row < N && sb < nsb ? (uint32_t)row * row_bytes + (uint32_t)sb * TS : kQdNowhere;
+    };
+    auto xofs = [&](int ls) {
+        const int sb = h * S + ls;
+        return jt < M && sb < nsb ? (uint32_t)(jt * K + sb * 256 + 8 * kq) * 2u : kQdNowhere;
+    };
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto unit = [&](const SkRaw<QT>& wr, const bf16x8 (&a)[8]) {
+        static_for<8>([&](auto Gc) {
+            const bf16x8 bw = sk_dequant<QT, MID, decltype(Gc)::value>(wr, kq);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[decltype(Gc)::value], bw, acc, 0, 0, 0);
+        });
+    };
+    // the wave's sums for quad cq: register h of lane (c, kq) is D[4 kq + h][c], parts added across lanes c ^ 1, c ^ 2
+    auto flush = [&](int cq) {
+        float v = h == 0 ? acc[0] : h == 1 ? acc[1] : h == 2 ? acc[2] : acc[3];
+        v = v + __shfl_xor(v, 1);
+        v = v + __shfl_xor(v, 2);
+        if (h == 0 && kq < M) red[cq][wave][4 * kq + jt] = v;
+        acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    };
+    __syncthreads();                                  // red is zero before any wave's sums land
+    if (lo < hi) {
+        int li = lo, lq = lo / S, ls = lo - lq * S;   // load cursor; it stops at the range's last unit
+        auto next_load = [&]() {
+            if (li + 1 < hi) {
+                li++;
+                if (++ls == S) { ls = 0; lq++; }
+            }
+        };
+        SkRaw<QT> w[2];
+        bf16x8 ax[2][8];
+        auto load_act = [&](bf16x8 (&a)[8], int s) {
+            const uint32_t o = xofs(s);
+#pragma unroll
+            for (int g = 0; g < 8; g++) a[g] = __builtin_bit_cast(bf16x8, ld128(rx, o + 64 * g));
+        };
+        int cq = lo / S, cs = lo - cq * S;            // compute cursor
+        auto finish_unit = [&](int ui) {
+            const bool quad_end = ++cs == S;
+            if (quad_end || ui + 1 == hi) flush(cq);
+            if (quad_end) { cs = 0; cq++; }
+        };
+        sk_load_rs<QT>(rw, wofs(lq, ls), kq, w[0]);
+        load_act(ax[0], ls);
+        next_load();
+        sk_load_rs<QT>(rw, wofs(lq, ls), kq, w[1]);
+        int i = lo;
+        for (; i + 2 <= hi; i += 2) {
+            next_load();                              // cursor at unit i + 2 (or the last)
+            load_act(ax[1], (i + 1) % S);
+            unit(w[0], ax[0]);
+            finish_unit(i);
+            sk_load_rs<QT>(rw, wofs(lq, ls), kq, w[0]);
+            load_act(ax[0], ls);
+            unit(w[1], ax[1]);
+            finish_unit(i + 1);
+            next_load();
+            sk_load_rs<QT>(rw, wofs(lq, ls), kq, w[1]);
+        }
+        if (i < hi) {
+            unit(w[0], ax[0]);
+            finish_unit(i);
+        }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < nq * 4 * M; idx += 64 * NW) {
+        const int qq = idx / (4 * M), e = idx - qq * 4 * M, t = e >> 2, j = e & 3;
+        const int n = 4 * (q0 + qq) + j;
+        if (n >= N) continue;
+        float y = red[qq][0][4 * t + j];
+#pragma unroll
+        for (int v = 1; v < NW; v++) y = y + red[qq][v][4 * t + j];
+        if (BIAS) y = y + __uint_as_float((uint32_t)bias[n] << 16);
+        Y[(int64_t)t * N + n] = __builtin_bit_cast(uint16_t, (__bf16)y);
+    }
+}
+
 // ------------------------------------------------------------- few activation rows, split along K (M <= 16 MT)
 // The same weight stream as gemm_gguf_skinny, cut into many more workgroups: workgroup (tn, s) takes the 128 weight
 // rows [128 tn, +128) -- 4 waves of two 16-row groups -- over super-blocks [KS s, KS s + KS) of K only (slice s of
@@ -924,6 +1060,26 @@ static void launch_splitk_mid(int mid, const uint16_t* X, const uint8_t* W, cons
     else launch_splitk<QT, WF_F32>(X, W, bias, Y, M, N, K, p, ws, st);
 }
 
+// The whole-rows form (gemm_gguf_quad): Q4_K / Q5_K at one or two rows where the few-rows kernel's 32-row
+// workgroups leave CUs idle (N < 8192: fewer than 256 of them). Measured on MI355X against the few-rows kernel, Wan
+// shapes, cold weights, per layer: Q4_K at one row 5120 x 5120 9.3 against 9.8 us, 5120 x 13824 18.6 against 24.3;
+// Q5_K 10.0 against 11.2, 20.1 against 26.4; at 13824 x 5120 (432 few-rows workgroups) 18.6 against 17.6 (Q4_K), and
+// from three rows on the few-rows kernel's shared activation loads win (Q4_K block at 3 rows 83.0 against 82.1 us).
+static constexpr int kQuadMaxRows = 2;
+
+static bool quad_takes(int64_t M, int64_t N, int64_t K, int qtype) {
+    return M >= 1 && M <= kQuadMaxRows && (qtype == 12 || qtype == 13) && (N + 31) / 32 < 256 &&
+           N * (K / 256) * (qtype == 12 ? 144 : 176) < (1LL << 31);
+}
+
+template <int QT, int MID>
+static void launch_quad(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
+                        hipStream_t st) {
+    const int G = std::min((N + 3) / 4, 256);     // quad_takes: at most 2048 quads, <= kQdMaxQuads per workgroup
+    if (bias) gemm_gguf_quad<QT, MID, true><<<dim3(G), 64 * kQdWaves, 0, st>>>(X, W, bias, Y, M, N, K, G);
+    else gemm_gguf_quad<QT, MID, false><<<dim3(G), 64 * kQdWaves, 0, st>>>(X, W, bias, Y, M, N, K, G);
+}
+
 #ifndef WF_SKINNY_NR1_MAX_N
 #define WF_SKINNY_NR1_MAX_N 8191
 #endif
@@ -983,6 +1139,12 @@ static void launch(const uint16_t* X, const uint8_t* W, const uint16_t* bias, ui
     // more CUs wait on Q6_K's slower raw loads (Wan block at one row 129 against 147 us, cold weights, MI355X). For
     // Q4_K / Q5_K the 64 CUs that then hold two workgroups set the time (88 against 82 us): their few-rows kernel is
     // bound by the dequantisation's VALU work per CU, which the split does not shrink.
+    if constexpr (QT != 14) {
+        if (quad_takes(M, N, K, QT)) {
+            launch_quad<QT, MID>(X, W, bias, Y, M, N, K, s);
+            return;
+        }
+    }
     if (M <= 8 && QT != 14) {
         launch_skinny<QT, MID, 1, 2, 8, true>(X, W, bias, Y, M, N, K, s);
         return;
