@@ -576,6 +576,12 @@ __device__ __forceinline__ void sk_load_rs(__amdgpu_buffer_rsrc_t r, uint32_t o,
     if constexpr (QT == 13) w.qh = ld64(r, o + 16 + 8 * kq);
 }
 
+template <int QT>
+__device__ __forceinline__ void quad_load(__amdgpu_buffer_rsrc_t r, uint32_t o, int kq, SkRaw<QT>& w) {
+    if constexpr (QT == 14) sk_load_q6(r, o, kq, w);
+    else sk_load_rs<QT>(r, o, kq, w);
+}
+
 template <int QT, int MID, bool BIAS>
 __global__ __launch_bounds__(64 * kQdWaves) void gemm_gguf_quad(const uint16_t* __restrict__ X,
                                                           const uint8_t* __restrict__ W,
@@ -642,22 +648,22 @@ __global__ __launch_bounds__(64 * kQdWaves) void gemm_gguf_quad(const uint16_t* 
             if (quad_end || ui + 1 == hi) flush(cq);
             if (quad_end) { cs = 0; cq++; }
         };
-        sk_load_rs<QT>(rw, wofs(lq, ls), kq, w[0]);
+        quad_load<QT>(rw, wofs(lq, ls), kq, w[0]);
         load_act(ax[0], ls);
         next_load();
-        sk_load_rs<QT>(rw, wofs(lq, ls), kq, w[1]);
+        quad_load<QT>(rw, wofs(lq, ls), kq, w[1]);
         int i = lo;
         for (; i + 2 <= hi; i += 2) {
             next_load();                              // cursor at unit i + 2 (or the last)
             load_act(ax[1], (i + 1) % S);
             unit(w[0], ax[0]);
             finish_unit(i);
-            sk_load_rs<QT>(rw, wofs(lq, ls), kq, w[0]);
+            quad_load<QT>(rw, wofs(lq, ls), kq, w[0]);
             load_act(ax[0], ls);
             unit(w[1], ax[1]);
             finish_unit(i + 1);
             next_load();
-            sk_load_rs<QT>(rw, wofs(lq, ls), kq, w[1]);
+            quad_load<QT>(rw, wofs(lq, ls), kq, w[1]);
         }
         if (i < hi) {
             unit(w[0], ax[0]);
@@ -1060,16 +1066,17 @@ static void launch_splitk_mid(int mid, const uint16_t* X, const uint8_t* W, cons
     else launch_splitk<QT, WF_F32>(X, W, bias, Y, M, N, K, p, ws, st);
 }
 
-// The whole-rows form (gemm_gguf_quad): Q4_K / Q5_K at one or two rows where the few-rows kernel's 32-row
-// workgroups leave CUs idle (N < 8192: fewer than 256 of them). Measured on MI355X against the few-rows kernel, Wan
-// shapes, cold weights, per layer: Q4_K at one row 5120 x 5120 9.3 against 9.8 us, 5120 x 13824 18.6 against 24.3;
-// Q5_K 10.0 against 11.2, 20.1 against 26.4; at 13824 x 5120 (432 few-rows workgroups) 18.6 against 17.6 (Q4_K), and
-// from three rows on the few-rows kernel's shared activation loads win (Q4_K block at 3 rows 83.0 against 82.1 us).
+// The whole-rows form (gemm_gguf_quad): one or two rows where the few-rows kernel's 32-row workgroups leave CUs idle
+// (N < 8192: fewer than 256 of them). Measured on MI355X against the few-rows kernel, Wan shapes, cold weights, per
+// layer at one row: Q4_K 5120 x 5120 9.3 against 9.8 us, 5120 x 13824 18.6 against 24.3; Q5_K 10.0 against 11.2,
+// 20.1 against 26.4; Q6_K 13.4 against 14.4, 29.2 against 37.0. At 13824 x 5120 (432 few-rows workgroups) 18.6
+// against 17.6 (Q4_K), and from three rows on the few-rows kernel's shared activation loads win (Q4_K block at 3
+// rows 83.0 against 82.1 us, Q6_K 131.2 against 131.1).
 static constexpr int kQuadMaxRows = 2;
 
 static bool quad_takes(int64_t M, int64_t N, int64_t K, int qtype) {
-    return M >= 1 && M <= kQuadMaxRows && (qtype == 12 || qtype == 13) && (N + 31) / 32 < 256 &&
-           N * (K / 256) * (qtype == 12 ? 144 : 176) < (1LL << 31);
+    return M >= 1 && M <= kQuadMaxRows && (N + 31) / 32 < 256 &&
+           N * (K / 256) * (qtype == 12 ? 144 : qtype == 13 ? 176 : 210) < (1LL << 31);
 }
 
 template <int QT, int MID>
@@ -1139,11 +1146,9 @@ static void launch(const uint16_t* X, const uint8_t* W, const uint16_t* bias, ui
     // more CUs wait on Q6_K's slower raw loads (Wan block at one row 129 against 147 us, cold weights, MI355X). For
     // Q4_K / Q5_K the 64 CUs that then hold two workgroups set the time (88 against 82 us): their few-rows kernel is
     // bound by the dequantisation's VALU work per CU, which the split does not shrink.
-    if constexpr (QT != 14) {
-        if (quad_takes(M, N, K, QT)) {
-            launch_quad<QT, MID>(X, W, bias, Y, M, N, K, s);
-            return;
-        }
+    if (quad_takes(M, N, K, QT)) {
+        launch_quad<QT, MID>(X, W, bias, Y, M, N, K, s);
+        return;
     }
     if (M <= 8 && QT != 14) {
         launch_skinny<QT, MID, 1, 2, 8, true>(X, W, bias, Y, M, N, K, s);

@@ -176,12 +176,12 @@ def test_few_rows_whole_output(native, qtype, mid, M, N, K, with_bias):
     check(y, x, weight_bf16(raw, qtype, mid, N, K), bias=bias)
 
 
-@pytest.mark.parametrize("qtype,mid", [(12, 0), (13, 0), (12, 2), (13, 1)])
+@pytest.mark.parametrize("qtype,mid", [(12, 0), (13, 0), (14, 0), (12, 2), (13, 1), (14, 2)])
 @pytest.mark.parametrize("M,N,K,with_bias", [(1, 5120, 5120, True), (2, 5120, 13824, False), (1, 8000, 5120, True),
                                              (2, 4101, 1280, True), (1, 61, 256, False), (2, 1, 768, True),
                                              (1, 1000, 2304, False)])
 def test_whole_rows_form_whole_output(native, qtype, mid, M, N, K, with_bias):
-    # Q4_K / Q5_K at one or two rows of an output narrower than 8192: each workgroup takes whole quads of 4 weight
+    # K-quants at one or two rows of an output narrower than 8192: each workgroup takes whole quads of 4 weight
     # rows, the MFMA's 16 columns holding 4 rows x 4 parts of K. The Wan shapes (5120 rows: 20 per CU; 13824: 54
     # super-blocks in parts of 14, the last part 12), 8000 rows (7-8 quads per workgroup), ragged N (4101, 61, 1:
     # quads past N), K with empty parts (1280: parts of 2, 2, 1, 0; 256, 768: one super-block per part, some parts
@@ -198,7 +198,7 @@ def test_whole_rows_form_whole_output(native, qtype, mid, M, N, K, with_bias):
     assert torch.equal(y.view(torch.int16), fused(native, xd, rd, qtype, N, bias=bd, mid=mid).view(torch.int16))
 
 
-@pytest.mark.parametrize("qtype,mid", [(12, 0), (13, 0), (13, 2)])
+@pytest.mark.parametrize("qtype,mid", [(12, 0), (13, 0), (13, 2), (14, 0), (14, 1)])
 def test_whole_rows_form_one_hot_rows_are_the_weight_bits(native, qtype, mid):
     # activation rows that are unit vectors e_k make every output the dequantised weight value w[n, k] itself (one
     # nonzero product, exact float32 sums, a bf16 value rounded to bf16 again): the whole-rows form's dequantisation
@@ -208,7 +208,8 @@ def test_whole_rows_form_one_hot_rows_are_the_weight_bits(native, qtype, mid):
     raw = encode.random_blocks(qtype, N * K // 256, seed=qtype, family="normal").reshape(N * K // 256, -1)
     rng = np.random.default_rng(qtype)
     big = rng.random(raw.shape[0]) < 0.1
-    raw[big, 0:2] = np.float16(rng.uniform(1.0, 8.0, size=int(big.sum()))).view(np.uint8).reshape(-1, 2)
+    d = 208 if qtype == 14 else 0                        # the block's float16 scale d
+    raw[big, d:d + 2] = np.float16(rng.uniform(1.0, 8.0, size=int(big.sum()))).view(np.uint8).reshape(-1, 2)
     raw = raw.ravel()
     w = weight_bf16(raw, qtype, mid, N, K)
     assert np.isfinite(w.numpy()).all()
