@@ -1075,7 +1075,8 @@ static void launch_splitk_mid(int mid, const uint16_t* X, const uint8_t* W, cons
 static constexpr int kQuadMaxRows = 2;
 
 static bool quad_takes(int64_t M, int64_t N, int64_t K, int qtype) {
-    return M >= 1 && M <= kQuadMaxRows && (N + 31) / 32 < 256 &&
+    // (weight and activation bytes both addressed by 32-bit buffer offsets)
+    return M >= 1 && M <= kQuadMaxRows && (N + 31) / 32 < 256 && M * K * 2 < (1LL << 31) &&
            N * (K / 256) * (qtype == 12 ? 144 : qtype == 13 ? 176 : 210) < (1LL << 31);
 }
 
