@@ -299,6 +299,16 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
     // The ring always issues: stages at or past K read past the row's end -- inside the buffer range (other rows'
     // bytes) or past it (zeros) -- into a buffer no later stage reads. Branch-free issue keeps the compiler's
     // per-buffer tracking of the outstanding loads exact, so it adds no waits of its own before LDS reads.
+    // the epilogue's scales (and bias) load first: their latency passes under the main loop instead of after it
+    const int mw = m0 + wm * WM * 32, nw = n0 + wn * WN * 32;
+    const RowScales<WM> rs(xs, mw, M, lane);
+    float wsn[WN], bn[WN];
+#pragma unroll
+    for (int j = 0; j < WN; j++) {
+        const int n = nw + j * 32 + lr;
+        wsn[j] = n < N ? ws[n] : 0.0f;
+        bn[j] = BIAS && n < N ? to_f32_out(bias, n, OUT) : 0.0f;
+    }
     issue(st0, 0);
     issue(st1, 1);
     issue(st2, 2);
@@ -341,13 +351,8 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
         const int wb = wave / PER_BUF;
         i32x4* buf = wb == 0 ? st0 : wb == 1 ? st1 : wb == 2 ? st2 : st3;
         uint16_t* ot = reinterpret_cast<uint16_t*>(buf) + (wave % PER_BUF) * TR * TC;
-        const int mw = m0 + wm * TR, nw = n0 + wn * TC;
-        const RowScales<WM> rs(xs, mw, M, lane);
 #pragma unroll
         for (int j = 0; j < WN; j++) {
-            const int n = nw + j * 32 + lr;
-            const float wsn = n < N ? ws[n] : 0.0f;
-            const float bn = BIAS && n < N ? to_f32_out(bias, n, OUT) : 0.0f;
 #pragma unroll
             for (int i = 0; i < WM; i++) {
 #pragma unroll
@@ -358,8 +363,8 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
                     for (int e = 0; e < 4; e++) xm[e] = rs.row(r0 + e);
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        float t = ((float)acc[i][j][4 * q + e] * xm[e]) * wsn;
-                        if (BIAS) t = t + bn;
+                        float t = ((float)acc[i][j][4 * q + e] * xm[e]) * wsn[j];
+                        if (BIAS) t = t + bn[j];
                         ot[(r0 + e) * TC + j * 32 + lr] = OUT == WF_BF16 ? __builtin_bit_cast(uint16_t, (__bf16)t)
                                                                          : __builtin_bit_cast(uint16_t, (_Float16)t);
                     }
@@ -396,23 +401,20 @@ __global__ __launch_bounds__(64 * VM * VN) void gemm_i8_dl(const int8_t* __restr
     // copy into this workgroup's LDS may outlive it
     // (every lane reaches each row permute: a lane that skipped it would hand a zero to the lanes reading its row)
     __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
-    const RowScales<WM> rs(xs, m0 + wm * WM * 32, M, lane);
 #pragma unroll
     for (int j = 0; j < WN; j++) {
-        const int n = n0 + wn * WN * 32 + j * 32 + lr;
+        const int n = nw + j * 32 + lr;
         const bool in_n = n < N;
-        const float wsn = in_n ? ws[n] : 0.0f;
-        const float bn = BIAS && in_n ? to_f32_out(bias, n, OUT) : 0.0f;
 #pragma unroll
         for (int i = 0; i < WM; i++) {
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const int ro = i * 32 + 8 * (e >> 2) + 4 * lk + (e & 3);
-                const int m = m0 + wm * WM * 32 + ro;
+                const int m = mw + ro;
                 const float xm = rs.row(ro);
                 if (!in_n || m >= M) continue;
-                float t = ((float)acc[i][j][e] * xm) * wsn;
-                if (BIAS) t = t + bn;
+                float t = ((float)acc[i][j][e] * xm) * wsn[j];
+                if (BIAS) t = t + bn[j];
                 const int64_t o = (int64_t)m * N + n;
                 if constexpr (RESID) {
                     const float g = __uint_as_float((uint32_t)res.gate[(int64_t)(m / res.rows_per_group) * N + n] << 16);
@@ -460,6 +462,7 @@ __global__ __launch_bounds__(S::NT) void gemm_i8_wl(const int8_t* __restrict__ A
                    [](const i32x16& c, const wl_frag& a, const wl_frag& b) {
                        return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
                    });
+    // (the scales load after the main loop here: held through it, the 256-row tilings' accumulators spill)
     const int wm = wave / S::VN, wn = wave % S::VN;
     const int mw = m0 + wm * WM * 32, nw = n0 + wn * WN * 32;
     const int lr = lane & 31, lk = lane >> 5;
