@@ -544,19 +544,19 @@ __global__ __launch_bounds__(64 * NW) void gemm_gguf_skinny(const uint16_t* __re
 // ------------------------------------------------------------- few activation rows, whole rows per CU (M <= 4)
 // gemm_gguf_skinny gives each workgroup 32 whole weight rows: 160 workgroups for a 5120-wide output on 256 CUs, which
 // at one or two rows are bound by the dequantisation's VALU issue (each weight value is dequantised for one or two
-// products). Here workgroup b of G takes the row quads [Qt b / G, Qt (b + 1) / G) (Qt = N / 4 quads of 4 weight
-// rows): 20 whole rows of a 5120-wide output on each of 256 CUs. The 16 columns of v_mfma_f32_16x16x32_bf16 hold 4 weight rows x 4 parts of K (column c = 4 j + h: row
-// j of the quad, part h = super-blocks [h S, h S + S), S = nsb / 4 rounded up), its 16 rows the M <= 4 activation
-// rows x the same 4 parts (row a = 4 t + h: activation row t over part h), so one step multiplies super-block
-// h S + s of every part at once and the wanted sums are the diagonal blocks D[4 t + h][4 j + h]: lane (c, kq) keeps
-// register h = c % 4 (activation row t = kq), and the 4 parts are added across lanes c ^ 1, c ^ 2. Each lane
-// dequantises its 8 values straight into its B fragment as in the few-rows kernel. Unit (quad, s) = one step over
-// super-block s of the 4 parts; a workgroup's units (quad-major) are spread evenly over its NW waves, each wave
-// streaming its range with the raw bytes two units ahead and the unit's 8 activation fragments one unit ahead. A
-// wave's sums for a quad go to LDS (red[quad][wave][4 t + j], zero where a wave has no share) and are added in wave
-// order after the barrier: no partial sums leave the workgroup. Weight and activation bytes come through buffer
-// resources; parts past K, rows past N and activation rows past M take an offset past the resource's end and read
-// as zeros.
+// products). Here workgroup b of G takes the row quads [Qt b / G, Qt (b + 1) / G) (Qt = N / 4 quads of 4 weight rows):
+// 20 whole rows of a 5120-wide output on each of 256 CUs. The 16 columns of v_mfma_f32_16x16x32_bf16 hold 4 weight
+// rows x 4 parts of K (column c = 4 j + h: row j of the quad, part h = super-blocks [h S, h S + S), S = nsb / 4
+// rounded up), its 16 rows the M <= 4 activation rows x the same 4 parts (row a = 4 t + h: activation row t over
+// part h), so one step multiplies super-block h S + s of every part at once, and the wanted sums are the diagonal
+// blocks D[4 t + h][4 j + h]: lane (c, kq) keeps register h = c % 4 (activation row t = kq), and the 4 parts are
+// added across lanes c ^ 1 and c ^ 2. Each lane dequantises its 8 values straight into its B fragment as in the
+// few-rows kernel. Unit (quad, s) = one step over super-block s of the 4 parts; a workgroup's units (quad-major) are
+// spread evenly over its NW waves, each wave streaming its range with the raw bytes two units ahead and the unit's 8
+// activation fragments one unit ahead. A wave's sums for a quad go to LDS (red[quad][wave][4 t + j], zero where a
+// wave has no share) and are added in wave order after the barrier: no partial sums leave the workgroup. Weight and
+// activation bytes come through buffer resources; parts past K, rows past N and activation rows past M take an
+// offset past the resource's end and read as zeros.
 constexpr int kQdMaxQuads = 8;           // row quads per workgroup: N <= 8192 on 256 workgroups
 constexpr int kQdWaves = 4;              // one wave per SIMD (two measured slower: half the units per wave)
 constexpr uint32_t kQdNowhere = 0x80000000u;
