@@ -557,7 +557,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_gguf_skinny(const uint16_t* __re
 // wave has no share) and are added in wave order after the barrier: no partial sums leave the workgroup. Weight and
 // activation bytes come through buffer resources; parts past K, rows past N and activation rows past M take an
 // offset past the resource's end and read as zeros.
-constexpr int kQdMaxQuads = 8;           // row quads per workgroup: N <= 8192 on 256 workgroups
+constexpr int kQdMaxQuads = 8;           // row quads per workgroup: N < 8192 on 256 workgroups, < 16384 on 512
 constexpr int kQdWaves = 4;              // one wave per SIMD (two measured slower: half the units per wave)
 constexpr uint32_t kQdNowhere = 0x80000000u;
 
@@ -1067,23 +1067,26 @@ static void launch_splitk_mid(int mid, const uint16_t* X, const uint8_t* W, cons
 }
 
 // The whole-rows form (gemm_gguf_quad): one or two rows where the few-rows kernel's 32-row workgroups leave CUs idle
-// (N < 8192: fewer than 256 of them). Measured on MI355X against the few-rows kernel, Wan shapes, cold weights, per
-// layer at one row: Q4_K 5120 x 5120 9.3 against 9.8 us, 5120 x 13824 18.6 against 24.3; Q5_K 10.0 against 11.2,
-// 20.1 against 26.4; Q6_K 13.4 against 14.4, 29.2 against 37.0. At 13824 x 5120 (432 few-rows workgroups) 18.6
-// against 17.6 (Q4_K), and from three rows on the few-rows kernel's shared activation loads win (Q4_K block at 3
-// rows 83.0 against 82.1 us, Q6_K 131.2 against 131.1).
+// (N < 8192: fewer than 256 of them), and for Q6_K, whose few-rows kernel waits on its raw loads, up to N < 16384 on
+// 512 workgroups. Measured on MI355X against the few-rows kernel, Wan shapes, cold weights, per layer at one row:
+// Q4_K 5120 x 5120 9.3 against 9.8 us, 5120 x 13824 18.6 against 24.3; Q5_K 10.0 against 11.2, 20.1 against 26.4;
+// Q6_K 13.4 against 14.4, 29.2 against 37.0, 13824 x 5120 24.3 against 35.2 (512 workgroups). At 13824 x 5120 the
+// Q4_K / Q5_K few-rows kernel (432 workgroups) stays as fast or faster (Q4_K 17.5 against 18.2 on 512 workgroups,
+// 18.6 on 256), and from three rows on its shared activation loads win (Q4_K block at 3 rows 83.0 against 82.1 us,
+// Q6_K 131.2 against 131.1).
 static constexpr int kQuadMaxRows = 2;
 
 static bool quad_takes(int64_t M, int64_t N, int64_t K, int qtype) {
     // (weight and activation bytes both addressed by 32-bit buffer offsets)
-    return M >= 1 && M <= kQuadMaxRows && (N + 31) / 32 < 256 && M * K * 2 < (1LL << 31) &&
+    return M >= 1 && M <= kQuadMaxRows && (N + 31) / 32 < (qtype == 14 ? 512 : 256) && M * K * 2 < (1LL << 31) &&
            N * (K / 256) * (qtype == 12 ? 144 : qtype == 13 ? 176 : 210) < (1LL << 31);
 }
 
 template <int QT, int MID>
 static void launch_quad(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
                         hipStream_t st) {
-    const int G = std::min((N + 3) / 4, 256);     // quad_takes: at most 2048 quads, <= kQdMaxQuads per workgroup
+    // 256 workgroups (one per CU) below 8192 rows, 512 (two per CU) up to 16384: at most kQdMaxQuads quads each
+    const int G = std::min((N + 3) / 4, N >= 8192 ? 512 : 256);
     if (bias) gemm_gguf_quad<QT, MID, true><<<dim3(G), 64 * kQdWaves, 0, st>>>(X, W, bias, Y, M, N, K, G);
     else gemm_gguf_quad<QT, MID, false><<<dim3(G), 64 * kQdWaves, 0, st>>>(X, W, bias, Y, M, N, K, G);
 }
