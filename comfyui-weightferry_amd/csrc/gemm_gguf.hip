@@ -1072,13 +1072,15 @@ static void launch_splitk_mid(int mid, const uint16_t* X, const uint8_t* W, cons
 // Q4_K 5120 x 5120 9.3 against 9.8 us, 5120 x 13824 18.6 against 24.3; Q5_K 10.0 against 11.2, 20.1 against 26.4;
 // Q6_K 13.4 against 14.4, 29.2 against 37.0, 13824 x 5120 24.3 against 35.2 (512 workgroups). At 13824 x 5120 the
 // Q4_K / Q5_K few-rows kernel (432 workgroups) stays as fast or faster (Q4_K 17.5 against 18.2 on 512 workgroups,
-// 18.6 on 256), and from three rows on its shared activation loads win (Q4_K block at 3 rows 83.0 against 82.1 us,
-// Q6_K 131.2 against 131.1).
-static constexpr int kQuadMaxRows = 2;
+// 18.6 on 256), and from three rows on its shared activation loads win (Q4_K block at 3 rows 83.0 against 82.1 us);
+// Q6_K keeps the whole-rows form up to four rows (block at 3 rows 118.3 against 131.5 us, at 4 rows 125.6 against
+// 132.7).
+static constexpr int kQuadMaxRows = 2, kQuadMaxRowsQ6 = 4;
 
 static bool quad_takes(int64_t M, int64_t N, int64_t K, int qtype) {
     // (weight and activation bytes both addressed by 32-bit buffer offsets)
-    return M >= 1 && M <= kQuadMaxRows && (N + 31) / 32 < (qtype == 14 ? 512 : 256) && M * K * 2 < (1LL << 31) &&
+    return M >= 1 && M <= (qtype == 14 ? kQuadMaxRowsQ6 : kQuadMaxRows) && (N + 31) / 32 < (qtype == 14 ? 512 : 256) &&
+           M * K * 2 < (1LL << 31) &&
            N * (K / 256) * (qtype == 12 ? 144 : qtype == 13 ? 176 : 210) < (1LL << 31);
 }
 

@@ -99,7 +99,7 @@ int wf_linear_i8_residual(const int8_t* xq, const int8_t* wq, const float* xs, c
  * reference function does this in one step: it replaces `dequantize` (enhancers/gguf_dequant.py:296-326) followed
  * by ComfyUI-GGUF's torch.nn.functional.linear on the bf16 weight. x: bf16 [M, K], 16-byte aligned; bias: bf16 [N]
  * or NULL; out: bf16 [M, N]. K % 256 == 0. M <= 64 runs the few-rows forms (the weight streamed once; at 1-2 rows
- * of N < 8192, Q6_K N < 16384, workgroups of whole 4-row quads), 65-512 rows the panel form (128 x 128 panels),
+ * of N < 8192, Q6_K 1-4 rows of N < 16384: workgroups of whole 4-row quads), 65-512 rows the panel form,
  * larger M the tiled form (256 x 320 tiles; Q6_K from 1024 rows 512 x 160). */
 int wf_linear_gguf(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes, int qtype, int64_t N,
                    const void* bias_bf16, void* out_bf16, int mid_dt, void* stream);

@@ -179,9 +179,11 @@ def test_few_rows_whole_output(native, qtype, mid, M, N, K, with_bias):
 @pytest.mark.parametrize("qtype,mid", [(12, 0), (13, 0), (14, 0), (12, 2), (13, 1), (14, 2)])
 @pytest.mark.parametrize("M,N,K,with_bias", [(1, 5120, 5120, True), (2, 5120, 13824, False), (1, 8000, 5120, True),
                                              (2, 4101, 1280, True), (1, 61, 256, False), (2, 1, 768, True),
-                                             (1, 1000, 2304, False), (1, 13824, 5120, True), (2, 9001, 512, False)])
+                                             (1, 1000, 2304, False), (1, 13824, 5120, True), (2, 9001, 512, False),
+                                             (3, 5120, 1280, True), (4, 13000, 768, False)])
 def test_whole_rows_form_whole_output(native, qtype, mid, M, N, K, with_bias):
-    # K-quants at one or two rows of an output narrower than 8192 (Q6_K: 16384, on 512 workgroups from 8192): each
+    # K-quants at one or two rows of an output narrower than 8192 (Q6_K: up to four rows and 16384 wide, on 512
+    # workgroups from 8192; Q4_K / Q5_K take the few-rows kernel at the Q6_K-only shapes): each
     # workgroup takes whole quads of 4 weight rows, the MFMA's 16 columns holding 4 rows x 4 parts of K. The Wan
     # shapes (5120 rows: 20 per CU; 13824: 54 super-blocks in parts of 14, the last part 12; 13824 rows: Q6_K's
     # 512-workgroup grid, Q4_K / Q5_K's few-rows kernel), 8000 rows (7-8 quads per workgroup), ragged N (4101, 61, 1,
