@@ -267,6 +267,8 @@ struct SkRaw;
 template <> struct SkRaw<12> { uint2 h01, h23; uint2 q[4]; };
 template <> struct SkRaw<13> { uint2 h01, h23; uint2 q[4]; uint2 qh; };
 template <> struct SkRaw<14> { uint2 ql[4], qh[2]; uint32_t sc[4]; uint32_t d; };
+// Q8_0 (the whole-rows form only): the 8 blocks of 32 values that make 256, each lane's 8 quants and each block's d
+template <> struct SkRaw<8> { uint2 q[8]; uint32_t d[8]; };
 
 // bytes [o, o + 8) of the block stream at p (o even): aligned dwords funnel-shifted, inside [o - 2, o + 8)
 __device__ __forceinline__ uint2 ld8_even(const uint8_t* p, uint32_t o) {
@@ -341,7 +343,31 @@ template <int QT, int MID, int g>
 __device__ __forceinline__ bf16x8 sk_dequant(const SkRaw<QT>& w, int kq) {
     uint32_t code[2];
     uint32_t o[4];
-    if constexpr (QT == 12 || QT == 13) {
+    if constexpr (QT == 8) {
+        // block g's 8 values of this lane: MID(d * q), q the signed byte (the reference's chain for Q8_0)
+        const uint2 qq = w.q[g];
+        if constexpr (MID == WF_F16) {
+            const h2 d2 = as_h2(w.d[g] | (w.d[g] << 16));
+            const h2 bias = h2s(-1152.0f);                    // 1024 + 128: the signed byte as unsigned ^ 0x80
+            const uint32_t u0 = qq.x ^ 0x80808080u, u1 = qq.y ^ 0x80808080u;
+            const h2 v0 = d2 * (biased_lo(u0) + bias), v1 = d2 * (biased_hi(u0) + bias);
+            const h2 v2 = d2 * (biased_lo(u1) + bias), v3 = d2 * (biased_hi(u1) + bias);
+            o[0] = pack_bf16((float)v0[0], (float)v0[1]);
+            o[1] = pack_bf16((float)v1[0], (float)v1[1]);
+            o[2] = pack_bf16((float)v2[0], (float)v2[1]);
+            o[3] = pack_bf16((float)v3[0], (float)v3[1]);
+        } else {
+            const float d = round_to<MID>(f16_bits_to_f32(w.d[g] & 0xffffu));
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                v[e] = round_to<MID>(d * (float)(int8_t)byte_of(qq.x, e));
+                v[4 + e] = round_to<MID>(d * (float)(int8_t)byte_of(qq.y, e));
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = pack_bf16(v[2 * e], v[2 * e + 1]);
+        }
+    } else if constexpr (QT == 12 || QT == 13) {
         const uint2 qq = w.q[g >> 1];
         code[0] = (qq.x >> (4 * (g & 1))) & 0x0f0f0f0fu;
         code[1] = (qq.y >> (4 * (g & 1))) & 0x0f0f0f0fu;
@@ -576,18 +602,33 @@ __device__ __forceinline__ void sk_load_rs(__amdgpu_buffer_rsrc_t r, uint32_t o,
     if constexpr (QT == 13) w.qh = ld64(r, o + 16 + 8 * kq);
 }
 
+// Q8_0 through a buffer resource: 8 blocks of 34 bytes from byte offset o (2-byte aligned), each block's d one
+// 2-byte load, this lane's 8 quants (bytes 2 + 8 kq of the block) one 12-byte load from the dword below, shifted
+__device__ __forceinline__ void sk_load_q8(__amdgpu_buffer_rsrc_t r, uint32_t o, int kq, SkRaw<8>& w) {
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+        w.d[g] = __builtin_amdgcn_raw_buffer_load_b16(r, o + 34 * g, 0, 0);
+        w.q[g] = ld8_rs(r, o + 34 * g + 2 + 8 * kq);
+    }
+}
+
 template <int QT>
 __device__ __forceinline__ void quad_load(__amdgpu_buffer_rsrc_t r, uint32_t o, int kq, SkRaw<QT>& w) {
     if constexpr (QT == 14) sk_load_q6(r, o, kq, w);
+    else if constexpr (QT == 8) sk_load_q8(r, o, kq, w);
     else sk_load_rs<QT>(r, o, kq, w);
 }
+
+// bytes per 256 values: a K-quant super-block, or 8 Q8_0 blocks
+template <int QT>
+struct QdTs { static constexpr int TS = QT == 8 ? 272 : GGUFTs<QT>::TS; };
 
 template <int QT, int MID, bool BIAS>
 __global__ __launch_bounds__(64 * kQdWaves) void gemm_gguf_quad(const uint16_t* __restrict__ X,
                                                           const uint8_t* __restrict__ W,
                                                           const uint16_t* __restrict__ bias,
                                                           uint16_t* __restrict__ Y, int M, int N, int K, int G) {
-    constexpr int TS = GGUFTs<QT>::TS, NW = kQdWaves;
+    constexpr int TS = QdTs<QT>::TS, NW = kQdWaves;
     __shared__ float red[kQdMaxQuads][NW][16];
     const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, kq = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1075,13 +1116,16 @@ static void launch_splitk_mid(int mid, const uint16_t* X, const uint8_t* W, cons
 // 18.6 on 256), and from three rows on its shared activation loads win (Q4_K block at 3 rows 83.0 against 82.1 us);
 // Q6_K keeps the whole-rows form up to four rows (block at 3 rows 118.3 against 131.5 us, at 4 rows 125.6 against
 // 132.7).
+// Q8_0 has no other fused form: the whole-rows form takes it where Q6_K's rule does, and every other Q8_0 shape is
+// left to the caller's two-step flow (the entry points answer WF_EUNSUPPORTED).
 static constexpr int kQuadMaxRows = 2, kQuadMaxRowsQ6 = 4;
 
 static bool quad_takes(int64_t M, int64_t N, int64_t K, int qtype) {
+    const bool wide = qtype == 14 || qtype == 8;
+    const int64_t ts = qtype == 12 ? 144 : qtype == 13 ? 176 : qtype == 14 ? 210 : 272;
     // (weight and activation bytes both addressed by 32-bit buffer offsets)
-    return M >= 1 && M <= (qtype == 14 ? kQuadMaxRowsQ6 : kQuadMaxRows) && (N + 31) / 32 < (qtype == 14 ? 512 : 256) &&
-           M * K * 2 < (1LL << 31) &&
-           N * (K / 256) * (qtype == 12 ? 144 : qtype == 13 ? 176 : 210) < (1LL << 31);
+    return M >= 1 && M <= (wide ? kQuadMaxRowsQ6 : kQuadMaxRows) && (N + 31) / 32 < (wide ? 512 : 256) &&
+           M * K * 2 < (1LL << 31) && N * (K / 256) * ts < (1LL << 31);
 }
 
 template <int QT, int MID>
@@ -1091,6 +1135,17 @@ static void launch_quad(const uint16_t* X, const uint8_t* W, const uint16_t* bia
     const int G = std::min((N + 3) / 4, N >= 8192 ? 512 : 256);
     if (bias) gemm_gguf_quad<QT, MID, true><<<dim3(G), 64 * kQdWaves, 0, st>>>(X, W, bias, Y, M, N, K, G);
     else gemm_gguf_quad<QT, MID, false><<<dim3(G), 64 * kQdWaves, 0, st>>>(X, W, bias, Y, M, N, K, G);
+}
+
+static void run_gguf_q8(int mid, const void* x_bf16, const void* wq, const void* bias_bf16, void* out_bf16, int M,
+                        int N, int K, hipStream_t s) {
+    const uint16_t* X = static_cast<const uint16_t*>(x_bf16);
+    const uint8_t* W = static_cast<const uint8_t*>(wq);
+    const uint16_t* B = static_cast<const uint16_t*>(bias_bf16);
+    uint16_t* Y = static_cast<uint16_t*>(out_bf16);
+    if (mid == WF_F16) launch_quad<8, WF_F16>(X, W, B, Y, M, N, K, s);
+    else if (mid == WF_BF16) launch_quad<8, WF_BF16>(X, W, B, Y, M, N, K, s);
+    else launch_quad<8, WF_F32>(X, W, B, Y, M, N, K, s);
 }
 
 #ifndef WF_SKINNY_NR1_MAX_N
@@ -1189,8 +1244,8 @@ namespace wf {
 // argument checks shared by the entry points; WF_OK with M == 0 or N == 0 means nothing to do
 static int check_gguf(const char* who, const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes,
                       int qtype, int64_t N, const void* bias_bf16, const void* out_bf16, int mid_dt) {
-    if (qtype != 12 && qtype != 13 && qtype != 14) {
-        set_error("%s: GGML type %d is not handled (Q4_K, Q5_K, Q6_K)", who, qtype);
+    if (qtype != 12 && qtype != 13 && qtype != 14 && qtype != 8) {
+        set_error("%s: GGML type %d is not handled (Q4_K, Q5_K, Q6_K; Q8_0 at 1-4 rows)", who, qtype);
         return WF_EUNSUPPORTED;
     }
     if (mid_dt < 0 || mid_dt > 2) { set_error("%s: dequant dtype %d", who, mid_dt); return WF_EUNSUPPORTED; }
@@ -1199,7 +1254,7 @@ static int check_gguf(const char* who, const void* x_bf16, int64_t M, int64_t K,
         return WF_EINVAL;
     }
     if (K % 256) { set_error("%s: K = %lld is not a multiple of 256", who, (long long)K); return WF_EUNSUPPORTED; }
-    const int ts = qtype == 12 ? 144 : qtype == 13 ? 176 : 210;
+    const int ts = qtype == 12 ? 144 : qtype == 13 ? 176 : qtype == 14 ? 210 : 272;   // bytes per 256 values
     if (wq_bytes != N * (K / 256) * ts) {
         set_error("%s: %lld weight bytes for [%lld, %lld]", who, (long long)wq_bytes, (long long)N, (long long)K);
         return WF_EUNSUPPORTED;
@@ -1212,6 +1267,11 @@ static int check_gguf(const char* who, const void* x_bf16, int64_t M, int64_t K,
     }
     if (M >= (1LL << 31) || N >= (1LL << 31) || K >= (1LL << 31)) {
         set_error("%s: sizes too large", who);
+        return WF_EUNSUPPORTED;
+    }
+    if (qtype == 8 && !quad_takes(M, N, K, 8)) {
+        set_error("%s: Q8_0 is fused at 1-4 rows of outputs at most 16352 wide only (%lld x %lld here)", who,
+                  (long long)M, (long long)N);
         return WF_EUNSUPPORTED;
     }
     return WF_OK;
@@ -1353,7 +1413,9 @@ extern "C" int wf_linear_gguf(const void* x_bf16, int64_t M, int64_t K, const vo
     using namespace wf;
     const int rc = check_gguf("wf_linear_gguf", x_bf16, M, K, wq, wq_bytes, qtype, N, bias_bf16, out_bf16, mid_dt);
     if (rc != WF_OK || M == 0 || N == 0) return rc;
-    run_gguf(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, static_cast<hipStream_t>(stream));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (qtype == 8) run_gguf_q8(mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, s);
+    else run_gguf(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, s);
     WF_LAUNCH_CHECK("wf_linear_gguf launch");
     return WF_OK;
 }
@@ -1381,6 +1443,11 @@ extern "C" int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const
     const int rc = check_gguf("wf_linear_gguf_ws", x_bf16, M, K, wq, wq_bytes, qtype, N, bias_bf16, out_bf16, mid_dt);
     if (rc != WF_OK || M == 0 || N == 0) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (qtype == 8) {                                 // the whole-rows form: no workspace
+        run_gguf_q8(mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, s);
+        WF_LAUNCH_CHECK("wf_linear_gguf_ws launch");
+        return WF_OK;
+    }
     // up to 64 rows the panel form runs only in more than one slice (in one, the few-rows kernel is faster)
     const bool panel = !split_takes(M, N, K) && panel_takes_ws(M, N, K, qtype) &&
                        (panel_takes(M) || panel_plan(M, N, K, INT64_MAX, qtype).s > 1);
@@ -1463,6 +1530,11 @@ extern "C" int wf_linear_gguf_noalloc(const void* x_bf16, int64_t M, int64_t K, 
                               mid_dt);
     if (rc != WF_OK || M == 0 || N == 0) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (qtype == 8) {                                 // the whole-rows form: no scratch
+        run_gguf_q8(mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, s);
+        WF_LAUNCH_CHECK("wf_linear_gguf_noalloc launch");
+        return WF_OK;
+    }
     // (up to 64 rows only when the scratch holds more than one slice: in one slice the few-rows kernel is faster)
     if (!split_takes(M, N, K) && panel_takes_ws(M, N, K, qtype) &&
         (panel_takes(M) || panel_plan(M, N, K, kScratchBytes - kSplitCounterBytes, qtype).s > 1)) {

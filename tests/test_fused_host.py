@@ -7,6 +7,15 @@ from conftest import sub
 fg = sub("enhancers.fused_gguf")
 
 
+def test_prefer_fused_rule_q8_0():
+    # Q8_0 is fused only in the library's whole-rows form: 1-4 rows of outputs up to 16352 wide
+    for rows in (1, 2, 4):
+        assert fg.prefer_fused(rows, 8, 5120, 5120) and fg.prefer_fused(rows, 8, 13824, 5120)
+        assert fg.prefer_fused(rows, 8, 16352, 5120) and not fg.prefer_fused(rows, 8, 16353, 5120)
+    for rows in (5, 32, 128, 4096):
+        assert not fg.prefer_fused(rows, 8, 5120, 5120)
+
+
 def test_prefer_fused_rule():
     # few activation rows: the fused kernel streams the weight once
     for rows in (1, 16, 32, 64):

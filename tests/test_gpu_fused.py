@@ -176,20 +176,25 @@ def test_few_rows_whole_output(native, qtype, mid, M, N, K, with_bias):
     check(y, x, weight_bf16(raw, qtype, mid, N, K), bias=bias)
 
 
-@pytest.mark.parametrize("qtype,mid", [(12, 0), (13, 0), (14, 0), (12, 2), (13, 1), (14, 2)])
+def nblocks(qtype, N, K):
+    return N * K // (32 if qtype == 8 else 256)
+
+
+@pytest.mark.parametrize("qtype,mid", [(12, 0), (13, 0), (14, 0), (8, 0), (12, 2), (13, 1), (14, 2), (8, 1)])
 @pytest.mark.parametrize("M,N,K,with_bias", [(1, 5120, 5120, True), (2, 5120, 13824, False), (1, 8000, 5120, True),
                                              (2, 4101, 1280, True), (1, 61, 256, False), (2, 1, 768, True),
                                              (1, 1000, 2304, False), (1, 13824, 5120, True), (2, 9001, 512, False),
                                              (3, 5120, 1280, True), (4, 13000, 768, False)])
 def test_whole_rows_form_whole_output(native, qtype, mid, M, N, K, with_bias):
     # K-quants at one or two rows of an output narrower than 8192 (Q6_K: up to four rows and 16384 wide, on 512
-    # workgroups from 8192; Q4_K / Q5_K take the few-rows kernel at the Q6_K-only shapes): each
+    # workgroups from 8192, and Q8_0 likewise, which has no other fused form; Q4_K / Q5_K take the few-rows kernel at
+    # the Q6_K-only shapes): each
     # workgroup takes whole quads of 4 weight rows, the MFMA's 16 columns holding 4 rows x 4 parts of K. The Wan
     # shapes (5120 rows: 20 per CU; 13824: 54 super-blocks in parts of 14, the last part 12; 13824 rows: Q6_K's
     # 512-workgroup grid, Q4_K / Q5_K's few-rows kernel), 8000 rows (7-8 quads per workgroup), ragged N (4101, 61, 1,
     # 9001: quads past N), K with empty parts (1280: parts of 2, 2, 1, 0; 256, 512, 768: one super-block per part,
     # some parts empty); every output element checked, and a second call gives the same bits
-    raw = encode.random_blocks(qtype, N * K // 256, seed=qtype * 3 + M + N, family="normal")
+    raw = encode.random_blocks(qtype, nblocks(qtype, N, K), seed=qtype * 3 + M + N, family="normal")
     g = torch.Generator().manual_seed(M * 13 + N + K)
     x = torch.randn((M, K), generator=g).to(torch.bfloat16)
     bias = torch.randn(N, generator=g).to(torch.bfloat16) if with_bias else None
@@ -201,17 +206,17 @@ def test_whole_rows_form_whole_output(native, qtype, mid, M, N, K, with_bias):
     assert torch.equal(y.view(torch.int16), fused(native, xd, rd, qtype, N, bias=bd, mid=mid).view(torch.int16))
 
 
-@pytest.mark.parametrize("qtype,mid", [(12, 0), (13, 0), (13, 2), (14, 0), (14, 1)])
+@pytest.mark.parametrize("qtype,mid", [(12, 0), (13, 0), (13, 2), (14, 0), (14, 1), (8, 0), (8, 2)])
 def test_whole_rows_form_one_hot_rows_are_the_weight_bits(native, qtype, mid):
     # activation rows that are unit vectors e_k make every output the dequantised weight value w[n, k] itself (one
     # nonzero product, exact float32 sums, a bf16 value rounded to bf16 again): the whole-rows form's dequantisation
     # equals the oracle's bit for bit, columns at part and super-block edges and random ones, scales of realistic
     # size and blocks with d in [1, 8)
     N, K = 1000, 5120
-    raw = encode.random_blocks(qtype, N * K // 256, seed=qtype, family="normal").reshape(N * K // 256, -1)
+    raw = encode.random_blocks(qtype, nblocks(qtype, N, K), seed=qtype, family="normal").reshape(N * K // 256, -1)
     rng = np.random.default_rng(qtype)
     big = rng.random(raw.shape[0]) < 0.1
-    d = 208 if qtype == 14 else 0                        # the block's float16 scale d
+    d = 208 if qtype == 14 else 0                        # a block's float16 scale d (Q8_0: the first of 8 blocks)
     raw[big, d:d + 2] = np.float16(rng.uniform(1.0, 8.0, size=int(big.sum()))).view(np.uint8).reshape(-1, 2)
     raw = raw.ravel()
     w = weight_bf16(raw, qtype, mid, N, K)
@@ -224,6 +229,23 @@ def test_whole_rows_form_one_hot_rows_are_the_weight_bits(native, qtype, mid):
         x[torch.arange(len(sel)), torch.from_numpy(sel)] = 1.0
         y = fused(native, x.cuda(), rd, qtype, N, mid=mid).cpu().float()
         assert torch.equal(y, w[:, torch.from_numpy(sel)].T), sel
+
+
+def test_q8_0_drop_in_fuses_few_rows_and_falls_back_elsewhere(native):
+    # the GGUF linear with a Q8_0 weight: at 1-4 rows the library's whole-rows form, at 5 rows and more the two-step
+    # flow (wf_dequant, then the bf16 GEMM); both against the float32 product of the oracle's bf16 weight
+    fg = sub("enhancers.fused_gguf")
+    N, K = 5120, 2048
+    raw = encode.random_blocks(8, nblocks(8, N, K), seed=8, family="normal")
+    rd = torch.from_numpy(raw).cuda()
+    w = weight_bf16(raw, 8, 0, N, K)
+    for rows, fused in ((1, True), (4, True), (5, False), (64, False)):
+        x = torch.randn((rows, K), generator=torch.Generator().manual_seed(rows)).to(torch.bfloat16)
+        assert fg.prefer_fused(rows, 8, N, K) is fused
+        assert (fg.fused_linear(x.cuda(), rd, 8, (N, K)) is not None) is fused
+        y = fg.linear(x.cuda(), rd, 8, (N, K))
+        torch.cuda.synchronize()
+        check(y, x, w)
 
 
 def test_rejects_what_it_does_not_handle(native):
