@@ -188,8 +188,8 @@ class GGUFLinear(torch.nn.Module):
     def __init__(self, in_features, out_features, qtype=12, bias=True, mode="auto", mid_dtype=None):
         super().__init__()
         q = int(qtype)
-        ts = _FUSED_TYPES.get(q) or gguf_dequant._FORMATS.get(q, (None, None))[1]
-        per = 256 if q in gguf_dequant._KFORMATS else 32
+        per = 256 if q in gguf_dequant._KFORMATS else 32                 # values per block
+        ts = (gguf_dequant._KFORMATS if q in gguf_dequant._KFORMATS else gguf_dequant._FORMATS).get(q, (None, None))[1]
         if ts is None or in_features % per:
             raise ValueError(f"GGML type {qtype} with {in_features} inputs")
         self.in_features, self.out_features, self.qtype = in_features, out_features, q

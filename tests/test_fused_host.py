@@ -7,6 +7,14 @@ from conftest import sub
 fg = sub("enhancers.fused_gguf")
 
 
+def test_gguf_linear_holds_the_blocks_of_its_format():
+    # the raw weight holds whole GGUF blocks: 34 bytes per 32 values for Q8_0, 144 / 176 / 210 per 256 for the
+    # K-quants, 18 per 32 for Q4_0, 84 per 256 for Q2_K
+    for q, block_bytes, per in ((8, 34, 32), (12, 144, 256), (13, 176, 256), (14, 210, 256), (2, 18, 32), (10, 84, 256)):
+        layer = fg.GGUFLinear(5120, 64, q, bias=False)
+        assert layer.weight.numel() == 64 * 5120 // per * block_bytes, q
+
+
 def test_prefer_fused_rule_q8_0():
     # Q8_0 is fused only in the library's whole-rows form: 1-4 rows of outputs up to 16352 wide
     for rows in (1, 2, 4):
