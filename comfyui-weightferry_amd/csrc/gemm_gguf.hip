@@ -267,8 +267,10 @@ struct SkRaw;
 template <> struct SkRaw<12> { uint2 h01, h23; uint2 q[4]; };
 template <> struct SkRaw<13> { uint2 h01, h23; uint2 q[4]; uint2 qh; };
 template <> struct SkRaw<14> { uint2 ql[4], qh[2]; uint32_t sc[4]; uint32_t d; };
-// Q8_0 (the whole-rows form only): the 8 blocks of 32 values that make 256, each lane's 8 quants and each block's d
-template <> struct SkRaw<8> { uint2 q[8]; uint32_t d[8]; };
+// Q8_0 (the whole-rows form only): for each of the 8 blocks of 32 values that make 256, the 12 bytes (from a dword
+// boundary) that hold this lane's 8 quants -- and, for the lanes with kq = 0, the block's d as well
+typedef uint32_t u32x3q __attribute__((ext_vector_type(3)));
+template <> struct SkRaw<8> { u32x3q raw[8]; };
 
 // bytes [o, o + 8) of the block stream at p (o even): aligned dwords funnel-shifted, inside [o - 2, o + 8)
 __device__ __forceinline__ uint2 ld8_even(const uint8_t* p, uint32_t o) {
@@ -344,10 +346,24 @@ __device__ __forceinline__ bf16x8 sk_dequant(const SkRaw<QT>& w, int kq) {
     uint32_t code[2];
     uint32_t o[4];
     if constexpr (QT == 8) {
-        // block g's 8 values of this lane: MID(d * q), q the signed byte (the reference's chain for Q8_0)
-        const uint2 qq = w.q[g];
+        // block g's 8 values of this lane: MID(d * q), q the signed byte (the reference's chain for Q8_0). Block g
+        // starts at byte 34 g of the unit (a multiple of 4 for even g, 2 past one for odd g); lane kq's quants at
+        // 34 g + 2 + 8 kq. The lanes with kq = 0 hold the 12 bytes from the dword at or below 34 g (d, then their
+        // quants 2 or 4 bytes in), the others those from the dword at or below their quants (0 or 2 bytes in); d
+        // comes from lane (c, 0) through a lane permute
+        const u32x3q v = w.raw[g];
+        uint2 qq;
+        uint32_t dl;
+        if constexpr ((g & 1) == 0) {
+            qq = funnel8(v[0], v[1], v[2], 16u);
+            dl = v[0] & 0xffffu;
+        } else {
+            qq = kq == 0 ? make_uint2(v[1], v[2]) : make_uint2(v[0], v[1]);
+            dl = v[0] >> 16;
+        }
+        const uint32_t dg = (uint32_t)__shfl((int)dl, (int)(__lane_id() & 15u));
         if constexpr (MID == WF_F16) {
-            const h2 d2 = as_h2(w.d[g] | (w.d[g] << 16));
+            const h2 d2 = as_h2(dg | (dg << 16));
             const h2 bias = h2s(-1152.0f);                    // 1024 + 128: the signed byte as unsigned ^ 0x80
             const uint32_t u0 = qq.x ^ 0x80808080u, u1 = qq.y ^ 0x80808080u;
             const h2 v0 = d2 * (biased_lo(u0) + bias), v1 = d2 * (biased_hi(u0) + bias);
@@ -357,15 +373,15 @@ __device__ __forceinline__ bf16x8 sk_dequant(const SkRaw<QT>& w, int kq) {
             o[2] = pack_bf16((float)v2[0], (float)v2[1]);
             o[3] = pack_bf16((float)v3[0], (float)v3[1]);
         } else {
-            const float d = round_to<MID>(f16_bits_to_f32(w.d[g] & 0xffffu));
-            float v[8];
+            const float d = round_to<MID>(f16_bits_to_f32(dg));
+            float t[8];
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                v[e] = round_to<MID>(d * (float)(int8_t)byte_of(qq.x, e));
-                v[4 + e] = round_to<MID>(d * (float)(int8_t)byte_of(qq.y, e));
+                t[e] = round_to<MID>(d * (float)(int8_t)byte_of(qq.x, e));
+                t[4 + e] = round_to<MID>(d * (float)(int8_t)byte_of(qq.y, e));
             }
 #pragma unroll
-            for (int e = 0; e < 4; e++) o[e] = pack_bf16(v[2 * e], v[2 * e + 1]);
+            for (int e = 0; e < 4; e++) o[e] = pack_bf16(t[2 * e], t[2 * e + 1]);
         }
     } else if constexpr (QT == 12 || QT == 13) {
         const uint2 qq = w.q[g >> 1];
@@ -602,13 +618,14 @@ __device__ __forceinline__ void sk_load_rs(__amdgpu_buffer_rsrc_t r, uint32_t o,
     if constexpr (QT == 13) w.qh = ld64(r, o + 16 + 8 * kq);
 }
 
-// Q8_0 through a buffer resource: 8 blocks of 34 bytes from byte offset o (2-byte aligned), each block's d one
-// 2-byte load, this lane's 8 quants (bytes 2 + 8 kq of the block) one 12-byte load from the dword below, shifted
+// Q8_0 through a buffer resource: 8 blocks of 34 bytes from byte offset o (a multiple of 4: the units are 272 bytes
+// in rows of whole units), one 12-byte load per block from the dword at or below 34 g (lanes kq = 0: the block's d
+// and their quants) or below 34 g + 2 + 8 kq (the others' quants); sk_dequant<8> takes them apart
 __device__ __forceinline__ void sk_load_q8(__amdgpu_buffer_rsrc_t r, uint32_t o, int kq, SkRaw<8>& w) {
 #pragma unroll
     for (int g = 0; g < 8; g++) {
-        w.d[g] = __builtin_amdgcn_raw_buffer_load_b16(r, o + 34 * g, 0, 0);
-        w.q[g] = ld8_rs(r, o + 34 * g + 2 + 8 * kq);
+        const uint32_t b = (kq == 0 ? o + 34 * g : o + 34 * g + 2 + 8 * kq) & ~3u;
+        w.raw[g] = __builtin_bit_cast(u32x3q, __builtin_amdgcn_raw_buffer_load_b96(r, b, 0, 0));
     }
 }
 
