@@ -629,9 +629,52 @@ __device__ __forceinline__ void sk_load_q8(__amdgpu_buffer_rsrc_t r, uint32_t o,
     }
 }
 
+// Q6_K for the whole-rows form: the raw words of sk_load_q6's pieces, shifted only where they are dequantised (a
+// shift right behind its load would make the wave wait for a prefetch there). Every piece starts (b & 3) bytes
+// into its dword, b the block's offset. d keeps its own 2-byte load: the dword holding it runs 2 bytes past a
+// dword-aligned block, which the per-dword range check reads as zeros at the weight's end.
+struct Q6Win { u32x3q ql[4], qh[2]; uint4 sc; uint32_t t, d, sh; };
+
+__device__ __forceinline__ void sk_load_q6w(__amdgpu_buffer_rsrc_t r, uint32_t b, int kq, Q6Win& w) {
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int gp = 0; gp < 2; gp++)
+            w.ql[2 * h + gp] = __builtin_bit_cast(
+                u32x3q, __builtin_amdgcn_raw_buffer_load_b96(r, (b + 64 * h + 32 * gp + 8 * kq) & ~3u, 0, 0));
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+        w.qh[h] = __builtin_bit_cast(u32x3q, __builtin_amdgcn_raw_buffer_load_b96(r, (b + 128 + 32 * h + 8 * kq) & ~3u,
+                                                                                   0, 0));
+    const uint32_t a = (b + 192) & ~3u;
+    w.sc = ld128(r, a);
+    w.t = ld32(r, a + 16);
+    w.d = __builtin_amdgcn_raw_buffer_load_b16(r, b + 208, 0, 0);
+    w.sh = (b & 3u) * 8u;
+}
+
+__device__ __forceinline__ SkRaw<14> q6_unwin(const Q6Win& w) {
+    SkRaw<14> s;
+#pragma unroll
+    for (int i = 0; i < 4; i++) s.ql[i] = funnel8(w.ql[i][0], w.ql[i][1], w.ql[i][2], w.sh);
+#pragma unroll
+    for (int h = 0; h < 2; h++) s.qh[h] = funnel8(w.qh[h][0], w.qh[h][1], w.qh[h][2], w.sh);
+    s.sc[0] = __builtin_amdgcn_alignbit(w.sc.y, w.sc.x, w.sh);
+    s.sc[1] = __builtin_amdgcn_alignbit(w.sc.z, w.sc.y, w.sh);
+    s.sc[2] = __builtin_amdgcn_alignbit(w.sc.w, w.sc.z, w.sh);
+    s.sc[3] = __builtin_amdgcn_alignbit(w.t, w.sc.w, w.sh);
+    s.d = w.d;
+    return s;
+}
+
 template <int QT>
-__device__ __forceinline__ void quad_load(__amdgpu_buffer_rsrc_t r, uint32_t o, int kq, SkRaw<QT>& w) {
-    if constexpr (QT == 14) sk_load_q6(r, o, kq, w);
+struct QdRaw { typedef SkRaw<QT> type; };
+template <>
+struct QdRaw<14> { typedef Q6Win type; };
+
+template <int QT>
+__device__ __forceinline__ void quad_load(__amdgpu_buffer_rsrc_t r, uint32_t o, int kq, typename QdRaw<QT>::type& w) {
+    if constexpr (QT == 14) sk_load_q6w(r, o, kq, w);
     else if constexpr (QT == 8) sk_load_q8(r, o, kq, w);
     else sk_load_rs<QT>(r, o, kq, w);
 }
@@ -670,7 +713,11 @@ __global__ __launch_bounds__(64 * kQdWaves) void gemm_gguf_quad(const uint16_t* 
         return jt < M && sb < nsb ? (uint32_t)(jt * K + sb * 256 + 8 * kq) * 2u : kQdNowhere;
     };
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto unit = [&](const SkRaw<QT>& wr, const bf16x8 (&a)[8]) {
+    typedef typename QdRaw<QT>::type Raw;
+    auto unit = [&](const Raw& raw, const bf16x8 (&a)[8]) {
+        SkRaw<QT> wr;
+        if constexpr (QT == 14) wr = q6_unwin(raw);
+        else wr = raw;
         static_for<8>([&](auto Gc) {
             const bf16x8 bw = sk_dequant<QT, MID, decltype(Gc)::value>(wr, kq);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[decltype(Gc)::value], bw, acc, 0, 0, 0);
@@ -693,7 +740,7 @@ __global__ __launch_bounds__(64 * kQdWaves) void gemm_gguf_quad(const uint16_t* 
                 if (++ls == S) { ls = 0; lq++; }
             }
         };
-        SkRaw<QT> w[2];
+        Raw w[2];
         bf16x8 ax[2][8];
         auto load_act = [&](bf16x8 (&a)[8], int s) {
             const uint32_t o = xofs(s);
