@@ -1175,11 +1175,10 @@ static void launch_splitk_mid(int mid, const uint16_t* X, const uint8_t* W, cons
 // (N < 8192: fewer than 256 of them), and for Q6_K, whose few-rows kernel waits on its raw loads, up to N < 16384 on
 // 512 workgroups. Measured on MI355X against the few-rows kernel, Wan shapes, cold weights, per layer at one row:
 // Q4_K 5120 x 5120 9.3 against 9.8 us, 5120 x 13824 18.6 against 24.3; Q5_K 10.0 against 11.2, 20.1 against 26.4;
-// Q6_K 13.4 against 14.4, 29.2 against 37.0, 13824 x 5120 24.3 against 35.2 (512 workgroups). At 13824 x 5120 the
+// Q6_K 10.2 against 14.4, 23.8 against 37.0, 13824 x 5120 22.3 against 35.2 (512 workgroups). At 13824 x 5120 the
 // Q4_K / Q5_K few-rows kernel (432 workgroups) stays as fast or faster (Q4_K 17.5 against 18.2 on 512 workgroups,
 // 18.6 on 256), and from three rows on its shared activation loads win (Q4_K block at 3 rows 83.0 against 82.1 us);
-// Q6_K keeps the whole-rows form up to four rows (block at 3 rows 118.3 against 131.5 us, at 4 rows 125.6 against
-// 132.7).
+// Q6_K keeps the whole-rows form up to four rows (block at 4 rows 114.6 against 132.7 us).
 // Q8_0 has no other fused form: the whole-rows form takes it where Q6_K's rule does, and every other Q8_0 shape is
 // left to the caller's two-step flow (the entry points answer WF_EUNSUPPORTED).
 static constexpr int kQuadMaxRows = 2, kQuadMaxRowsQ6 = 4;
