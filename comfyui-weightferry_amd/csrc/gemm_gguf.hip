@@ -308,37 +308,53 @@ __device__ __forceinline__ void sk_load(const uint8_t* b, int kq, SkRaw<QT>& w) 
     }
 }
 
-typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-
 // Q6_K's raw bytes of K-quarter kq through a buffer resource over the workgroup's weight rows, b = the super-block's
-// byte offset in it (2-byte aligned: 210-byte blocks). Each 8-byte piece is one 12-byte load from its aligned-down
-// dword, the 16 scale bytes one 16- and one 4-byte load (the 4 bytes are used only when the block starts 2 bytes
-// past a dword, and then end with it), d one 2-byte load at its place: the buffer's range check works per dword,
-// so a wider load of the last block's last bytes would read as zeros. Fewer load instructions than sk_load<14>,
-// whose many narrow loads (each touching 16 rows) kept the few-rows kernel's Q6_K waves waiting on the address unit.
-// Rows past N (past the resource's end) read as zeros.
-__device__ __forceinline__ uint2 ld8_rs(__amdgpu_buffer_rsrc_t r, uint32_t o) {
-    const uint32_t a = o & ~3u;
-    const u32x3 v = __builtin_bit_cast(u32x3, __builtin_amdgcn_raw_buffer_load_b96(r, a, 0, 0));
-    return funnel8(v[0], v[1], v[2], (o & 3u) * 8u);
-}
+// byte offset in it (2-byte aligned: 210-byte blocks), for the few-rows and whole-rows forms. Each 8-byte piece is
+// one 12-byte load from its aligned-down dword, the 16 scale bytes one 16- and one 4-byte load (the 4 bytes are used
+// only when the block starts 2 bytes past a dword, and then end with it), d one 2-byte load at its place: the
+// buffer's range check works per dword, so the dword holding d, which runs 2 bytes past a dword-aligned block, would
+// read as zeros at the weight's last block. Fewer load instructions than sk_load<14>, whose many narrow loads (each
+// touching 16 rows) kept the few-rows kernel's Q6_K waves waiting on the address unit. The words are kept as loaded
+// and shifted by q6_unwin where they are dequantised: a shift right behind its load makes the wave wait for that
+// prefetch there. Rows past N (past the resource's end) read as zeros.
+struct Q6Win { u32x3q ql[4], qh[2]; uint4 sc; uint32_t t, d, sh; };
 
-__device__ __forceinline__ void sk_load_q6(__amdgpu_buffer_rsrc_t r, uint32_t b, int kq, SkRaw<14>& w) {
+__device__ __forceinline__ void sk_load_q6w(__amdgpu_buffer_rsrc_t r, uint32_t b, int kq, Q6Win& w) {
 #pragma unroll
     for (int h = 0; h < 2; h++)
 #pragma unroll
-        for (int gp = 0; gp < 2; gp++) w.ql[2 * h + gp] = ld8_rs(r, b + 64 * h + 32 * gp + 8 * kq);
+        for (int gp = 0; gp < 2; gp++)
+            w.ql[2 * h + gp] = __builtin_bit_cast(
+                u32x3q, __builtin_amdgcn_raw_buffer_load_b96(r, (b + 64 * h + 32 * gp + 8 * kq) & ~3u, 0, 0));
 #pragma unroll
-    for (int h = 0; h < 2; h++) w.qh[h] = ld8_rs(r, b + 128 + 32 * h + 8 * kq);
-    const uint32_t a = (b + 192) & ~3u, sh = ((b + 192) & 3u) * 8u;
-    const uint4 v = ld128(r, a);
-    const uint32_t t = ld32(r, a + 16);
-    w.sc[0] = __builtin_amdgcn_alignbit(v.y, v.x, sh);
-    w.sc[1] = __builtin_amdgcn_alignbit(v.z, v.y, sh);
-    w.sc[2] = __builtin_amdgcn_alignbit(v.w, v.z, sh);
-    w.sc[3] = __builtin_amdgcn_alignbit(t, v.w, sh);
+    for (int h = 0; h < 2; h++)
+        w.qh[h] = __builtin_bit_cast(u32x3q, __builtin_amdgcn_raw_buffer_load_b96(r, (b + 128 + 32 * h + 8 * kq) & ~3u,
+                                                                                   0, 0));
+    const uint32_t a = (b + 192) & ~3u;
+    w.sc = ld128(r, a);
+    w.t = ld32(r, a + 16);
     w.d = __builtin_amdgcn_raw_buffer_load_b16(r, b + 208, 0, 0);
+    w.sh = (b & 3u) * 8u;
 }
+
+__device__ __forceinline__ SkRaw<14> q6_unwin(const Q6Win& w) {
+    SkRaw<14> s;
+#pragma unroll
+    for (int i = 0; i < 4; i++) s.ql[i] = funnel8(w.ql[i][0], w.ql[i][1], w.ql[i][2], w.sh);
+#pragma unroll
+    for (int h = 0; h < 2; h++) s.qh[h] = funnel8(w.qh[h][0], w.qh[h][1], w.qh[h][2], w.sh);
+    s.sc[0] = __builtin_amdgcn_alignbit(w.sc.y, w.sc.x, w.sh);
+    s.sc[1] = __builtin_amdgcn_alignbit(w.sc.z, w.sc.y, w.sh);
+    s.sc[2] = __builtin_amdgcn_alignbit(w.sc.w, w.sc.z, w.sh);
+    s.sc[3] = __builtin_amdgcn_alignbit(w.t, w.sc.w, w.sh);
+    s.d = w.d;
+    return s;
+}
+
+template <int QT>
+struct QdRaw { typedef SkRaw<QT> type; };
+template <>
+struct QdRaw<14> { typedef Q6Win type; };
 
 // the 8 values of stage g as a bf16x8 B fragment, the reference's rounding chain in MID
 template <int QT, int MID, int g>
@@ -480,11 +496,19 @@ __global__ __launch_bounds__(64 * NW) void gemm_gguf_skinny(const uint16_t* __re
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[nr][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const int nsb = K / 256;
-    auto load = [&](SkRaw<QT> (&w)[NR], int sb) {
+    typedef typename QdRaw<QT>::type Raw;
+    auto load = [&](Raw (&w)[NR], int sb) {
 #pragma unroll
         for (int nr = 0; nr < NR; nr++) {
-            if constexpr (QT == 14) sk_load_q6(rw, rofs[nr] + (uint32_t)sb * TS, kq, w[nr]);
+            if constexpr (QT == 14) sk_load_q6w(rw, rofs[nr] + (uint32_t)sb * TS, kq, w[nr]);
             else sk_load<QT>(wrow[nr] + (int64_t)sb * TS, kq, w[nr]);
+        }
+    };
+    auto unwin = [&](const Raw (&w)[NR], SkRaw<QT> (&u)[NR]) {
+#pragma unroll
+        for (int nr = 0; nr < NR; nr++) {
+            if constexpr (QT == 14) u[nr] = q6_unwin(w[nr]);
+            else u[nr] = w[nr];
         }
     };
     // NR groups of 16 weight rows share each activation fragment (NR MFMAs per activation load)
@@ -500,7 +524,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_gguf_skinny(const uint16_t* __re
     auto act = [&](int mt, int sb, int g) {
         return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(xrow[mt] + sb * 256 + 32 * g));
     };
-    SkRaw<QT> w[2][NR];
+    Raw w[2][NR];
     if constexpr (AHEAD) {
         static_assert(MT == 1, "activations one super-block ahead: one row group");
         // one activation row group: its 8 fragments of a super-block fit in registers, so they are loaded one
@@ -513,7 +537,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_gguf_skinny(const uint16_t* __re
 #pragma unroll
             for (int g = 0; g < 8; g++) a[g] = act(0, sb, g);
         };
-        auto superblock = [&](const SkRaw<QT> (&wr)[NR], const bf16x8 (&a)[8]) {
+        auto superblock = [&](const Raw (&wraw)[NR], const bf16x8 (&a)[8]) {
+            SkRaw<QT> wr[NR];
+            unwin(wraw, wr);
             static_for<8>([&](auto G) {
                 bf16x8 bw[NR];
                 dequant(G, wr, bw);
@@ -540,7 +566,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_gguf_skinny(const uint16_t* __re
     } else {
         // activation fragments read at each stage; the raw bytes of the next two super-blocks stay in flight (two
         // register sets, each refilled two super-blocks ahead)
-        auto superblock = [&](const SkRaw<QT> (&wr)[NR], int sb) {
+        auto superblock = [&](const Raw (&wraw)[NR], int sb) {
+            SkRaw<QT> wr[NR];
+            unwin(wraw, wr);
             static_for<8>([&](auto G) {
                 bf16x8 bw[NR];
                 dequant(G, wr, bw);
@@ -628,49 +656,6 @@ __device__ __forceinline__ void sk_load_q8(__amdgpu_buffer_rsrc_t r, uint32_t o,
         w.raw[g] = __builtin_bit_cast(u32x3q, __builtin_amdgcn_raw_buffer_load_b96(r, b, 0, 0));
     }
 }
-
-// Q6_K for the whole-rows form: the raw words of sk_load_q6's pieces, shifted only where they are dequantised (a
-// shift right behind its load would make the wave wait for a prefetch there). Every piece starts (b & 3) bytes
-// into its dword, b the block's offset. d keeps its own 2-byte load: the dword holding it runs 2 bytes past a
-// dword-aligned block, which the per-dword range check reads as zeros at the weight's end.
-struct Q6Win { u32x3q ql[4], qh[2]; uint4 sc; uint32_t t, d, sh; };
-
-__device__ __forceinline__ void sk_load_q6w(__amdgpu_buffer_rsrc_t r, uint32_t b, int kq, Q6Win& w) {
-#pragma unroll
-    for (int h = 0; h < 2; h++)
-#pragma unroll
-        for (int gp = 0; gp < 2; gp++)
-            w.ql[2 * h + gp] = __builtin_bit_cast(
-                u32x3q, __builtin_amdgcn_raw_buffer_load_b96(r, (b + 64 * h + 32 * gp + 8 * kq) & ~3u, 0, 0));
-#pragma unroll
-    for (int h = 0; h < 2; h++)
-        w.qh[h] = __builtin_bit_cast(u32x3q, __builtin_amdgcn_raw_buffer_load_b96(r, (b + 128 + 32 * h + 8 * kq) & ~3u,
-                                                                                   0, 0));
-    const uint32_t a = (b + 192) & ~3u;
-    w.sc = ld128(r, a);
-    w.t = ld32(r, a + 16);
-    w.d = __builtin_amdgcn_raw_buffer_load_b16(r, b + 208, 0, 0);
-    w.sh = (b & 3u) * 8u;
-}
-
-__device__ __forceinline__ SkRaw<14> q6_unwin(const Q6Win& w) {
-    SkRaw<14> s;
-#pragma unroll
-    for (int i = 0; i < 4; i++) s.ql[i] = funnel8(w.ql[i][0], w.ql[i][1], w.ql[i][2], w.sh);
-#pragma unroll
-    for (int h = 0; h < 2; h++) s.qh[h] = funnel8(w.qh[h][0], w.qh[h][1], w.qh[h][2], w.sh);
-    s.sc[0] = __builtin_amdgcn_alignbit(w.sc.y, w.sc.x, w.sh);
-    s.sc[1] = __builtin_amdgcn_alignbit(w.sc.z, w.sc.y, w.sh);
-    s.sc[2] = __builtin_amdgcn_alignbit(w.sc.w, w.sc.z, w.sh);
-    s.sc[3] = __builtin_amdgcn_alignbit(w.t, w.sc.w, w.sh);
-    s.d = w.d;
-    return s;
-}
-
-template <int QT>
-struct QdRaw { typedef SkRaw<QT> type; };
-template <>
-struct QdRaw<14> { typedef Q6Win type; };
 
 template <int QT>
 __device__ __forceinline__ void quad_load(__amdgpu_buffer_rsrc_t r, uint32_t o, int kq, typename QdRaw<QT>::type& w) {
@@ -1263,7 +1248,7 @@ static void launch(const uint16_t* X, const uint8_t* W, const uint16_t* bias, ui
     // few rows: 32 weight rows per workgroup (two 16-row groups sharing each activation fragment)
     // Up to 8 rows the activations go one super-block ahead: 10-22 % faster than the per-stage reads (Wan shapes,
     // cold weights); from 9 rows on, their 16 distinct rows per fragment make it slower. Q6_K keeps the per-stage
-    // reads at every row count: with its raw bytes through sk_load_q6 the 32-row, 8-wave form is the fastest one
+    // reads at every row count: with its raw bytes through sk_load_q6w the 32-row, 8-wave form is the fastest one
     // (Wan shapes at 1-8 rows, per layer: 18.4 / 34.8 / 39.1 us against 20.3 / 37.2 / 47.4 for the 16-row, 4-wave
     // workgroups with activations ahead and the narrow loads).
     // Up to 16 rows of a Q6_K product narrower than 256 workgroups of 32 rows, 16 weight rows per workgroup (NR = 1):
