@@ -1336,14 +1336,17 @@ static constexpr int64_t kPanelMinRowsWs = 17;       // fewest rows the panel fo
 // Without a workspace (one slice) the panel form takes 65-512 rows.
 static bool panel_takes(int64_t M) { return M > 64 && M <= kPanelMaxRows; }
 
-// With a workspace (K in slices) it also takes 33-64 rows, and 17-32 rows of Q6_K or of a deep product (K >= 2 N),
-// where the few-rows kernel's one workgroup per 32 weight rows leaves CUs idle or runs long (measured on MI355X, Wan
-// shapes, warmed, with the workspace, per layer: Q4_K 5120 x 13824 at 32 rows 34.8 against 38.0 us, at 64 rows 45.1
-// against 70.0; Q6_K 5120 x 5120 at 17 rows 22.8 against 28.0; Q4_K 5120 x 5120 at 32 rows 17.0 against 16.5, so
-// shallow Q4_K / Q5_K products keep the few-rows kernel up to 32 rows).
-static bool panel_takes_ws(int64_t M, int64_t N, int64_t K, int qtype) {
+// With a workspace (K in slices) it also takes 33-64 rows, and 17-32 rows of a deep product (K >= 2 N), where the
+// few-rows kernel's one workgroup per 32 weight rows leaves CUs idle or runs long (measured on MI355X, Wan shapes,
+// warmed, with the workspace, per layer: Q4_K 5120 x 13824 at 32 rows 34.8 against 38.0 us, at 64 rows 45.1 against
+// 70.0; Q6_K 43.9 against 46.5 at 32 rows, 47.1 against 62.5 at 40). Shallow products keep the few-rows kernel up
+// to 32 rows (Q4_K 5120 x 5120 at 32 rows 16.5 against 17.0; Q6_K, its raw words shifted where dequantised, 18.8
+// against 24.0, 13824 x 5120 36.3 against 47.4, and 16.4 against 22.9 at 17 rows). From 33 rows the panel form
+// takes them too: Q6_K's few-rows kernel is still 3-11 % faster on them at 40-48 rows but not at 64, and the deep
+// product's panel gain (25-30 %) is larger.
+static bool panel_takes_ws(int64_t M, int64_t N, int64_t K) {
     if (M > 32) return M <= kPanelMaxRows;
-    return M >= kPanelMinRowsWs && (qtype == 14 || K >= 2 * N);
+    return M >= kPanelMinRowsWs && K >= 2 * N;
 }
 
 struct PanelPlan {
@@ -1473,10 +1476,9 @@ extern "C" int wf_linear_gguf_workspace(int64_t M, int64_t N, int64_t K, int64_t
     if (!bytes) { set_error("wf_linear_gguf_workspace: null out-pointer"); return WF_EINVAL; }
     *bytes = 0;
     if (M < 0 || N < 0 || K <= 0 || K % 256) { set_error("wf_linear_gguf_workspace: M, N, K"); return WF_EINVAL; }
-    // the format is not known here: the largest need over them (Q6_K takes the panel form from 17 rows, and more
-    // slices up to 128 rows)
+    // the format is not known here: the largest need over them (Q6_K's panels take more slices up to 128 rows)
     if (split_takes(M, N, K)) *bytes = split_plan(M, N, K).bytes();
-    else if (panel_takes_ws(M, N, K, 14)) {
+    else if (panel_takes_ws(M, N, K)) {
         const int64_t part = std::max(panel_plan(M, N, K, INT64_MAX, 12).part_bytes,
                                       panel_plan(M, N, K, INT64_MAX, 14).part_bytes);
         if (part > 0) *bytes = kSplitCounterBytes + part;   // the split form's counters stay untouched
@@ -1497,7 +1499,7 @@ extern "C" int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const
         return WF_OK;
     }
     // up to 64 rows the panel form runs only in more than one slice (in one, the few-rows kernel is faster)
-    const bool panel = !split_takes(M, N, K) && panel_takes_ws(M, N, K, qtype) &&
+    const bool panel = !split_takes(M, N, K) && panel_takes_ws(M, N, K) &&
                        (panel_takes(M) || panel_plan(M, N, K, INT64_MAX, qtype).s > 1);
     if (panel) {
         // the panel form's partial sums go past the split form's counters, which must stay zero between calls (one
@@ -1584,7 +1586,7 @@ extern "C" int wf_linear_gguf_noalloc(const void* x_bf16, int64_t M, int64_t K, 
         return WF_OK;
     }
     // (up to 64 rows only when the scratch holds more than one slice: in one slice the few-rows kernel is faster)
-    if (!split_takes(M, N, K) && panel_takes_ws(M, N, K, qtype) &&
+    if (!split_takes(M, N, K) && panel_takes_ws(M, N, K) &&
         (panel_takes(M) || panel_plan(M, N, K, kScratchBytes - kSplitCounterBytes, qtype).s > 1)) {
         // the panel form's partial sums in the scratch array, as many slices as fit there
         const PanelPlan p = panel_plan(M, N, K, kScratchBytes - kSplitCounterBytes, qtype);

@@ -95,7 +95,7 @@ def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
 # Wan-14B shapes (5120 x 5120, 13824 x 5120, 5120 x 13824), µs per block of six layers:
 #   * up to 64 rows, its few-rows form (the weight streamed through the chip once): 32 rows 124-134 µs against
 #     269-334 two-step (Q4_K); with the workspace the library runs the panel form in K slices from 33 rows, and from
-#     17 rows for Q6_K and deep products (K >= 2 N) (Wan shapes at 64 rows: 5120 x 13824 Q4_K 45 against 70 µs);
+#     17 rows for deep products (K >= 2 N) (Wan shapes at 64 rows: 5120 x 13824 Q4_K 45 against 70 µs);
 #   * 65-256 rows, its panel form (128 x 128 panels, K in slices): Q4_K 183 against 367 µs at 128 rows, 290 against
 #     496 at 256; Q5_K 198 / 306 against 363 / 500; Q6_K 269 / 451 against 364 / 502; and up to 384 rows for Q4_K /
 #     Q5_K (three 128-row panels): Q4_K 375 / 380 against 411 / 417 at 320 / 384 rows, Q5_K 408 / 412 against

@@ -112,12 +112,12 @@ int wf_linear_gguf(const void* x_bf16, int64_t M, int64_t K, const void* wq, int
  * 256-byte aligned, at least the bytes wf_linear_gguf_workspace gives; its first 16 KiB are counters that must be
  * zero on entry and are zero again when the call has run, whatever its shape (a workspace cleared once can be reused
  * by later calls of any shape on the same stream; calls that overlap on one workspace race). With 33-512 rows,
- * and with 17-32 rows of Q6_K or of a deep product (K >= 2 N), the panel form splits K into slices (at least two
+ * and with 17-32 rows of a deep product (K >= 2 N), the panel form splits K into slices (at least two
  * super-blocks each), enough to give the chip 256 workgroups: each slice writes float32 partial sums into the
  * workspace past the split form's 16 KiB of counters, which it leaves untouched (16 KiB + S * M * N * 4 bytes), and a
  * second kernel adds them in slice order; up to 64 rows only when
  * K gives more than one slice. wf_linear_gguf_workspace does not know the format and gives the largest need over
- * them (the panel form's bytes from 17 rows). Any other shape does not use the workspace (workspace may be NULL) and
+ * them. Any other shape does not use the workspace (workspace may be NULL) and
  * is wf_linear_gguf. */
 int wf_linear_gguf_workspace(int64_t M, int64_t N, int64_t K, int64_t* bytes);
 int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes, int qtype, int64_t N,

@@ -150,11 +150,15 @@ def test_fused_gemm_workspace_sizes_without_gpu():
         assert need(M, 5120, 5120) == 0 and need(M, 13824, 5120) == 0
     # up to 8 rows of a narrow deep product: the split form (16 KiB of counters, then the partial sums)
     assert need(1, 2048, 8192) > 16384 and need(8, 2048, 8192) > need(1, 2048, 8192)
-    # 17-512 rows: the panel form's slices, S * M * N * 4 bytes with S >= 2 (the largest need over the formats), past
-    # the split form's 16 KiB of counters (one workspace serves both forms)
-    for M, N, K in ((17, 5120, 5120), (32, 13824, 5120), (64, 5120, 13824), (128, 5120, 5120), (512, 13824, 5120)):
+    # 17-32 rows of a deep product (K >= 2 N) and 33-512 rows of any: the panel form's slices, S * M * N * 4 bytes with
+    # S >= 2 (the largest need over the formats), past the split form's 16 KiB of counters (one workspace serves both)
+    for M, N, K in ((17, 5120, 13824), (32, 5120, 13824), (33, 5120, 5120), (64, 5120, 13824), (128, 5120, 5120),
+                    (512, 13824, 5120)):
         n = need(M, N, K) - 16384
         assert n > 0 and n % (M * N * 4) == 0 and n // (M * N * 4) >= 2, (M, N, K, n)
+    # 17-32 rows of a shallow product: the few-rows kernel, no workspace
+    for M, N, K in ((17, 5120, 5120), (32, 13824, 5120), (32, 5120, 5120)):
+        assert need(M, N, K) == 0, (M, N, K)
     # too shallow for two slices of two super-blocks, or past the panel form: nothing
     assert need(128, 5120, 768) == 0 and need(513, 5120, 5120) == 0 and need(4096, 5120, 5120) == 0
     # bad shapes are refused
