@@ -197,7 +197,7 @@ def fused_leg(torch, native):
     # Q5_K for the 5120-wide outputs, Q6_K and Q8_0 for all six); the few-rows form otherwise.
     fg = importlib.import_module(PKG + ".enhancers.fused_gguf")
     for rows in (128, 32, 1):
-        # (Q8_0 has one fused form, at 1-4 rows: measured at one token)
+        # (Q8_0 has one fused form, at 1-8 rows: measured at one token)
         for qt, name in ((12, "q4_k"), (13, "q5_k"), (14, "q6_k")) + (((8, "q8_0"),) if rows == 1 else ()):
             tf = tc = tu = 0.0
             wbytes = 0

@@ -611,7 +611,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_gguf_skinny(const uint16_t* __re
     }
 }
 
-// ------------------------------------------------------------- few activation rows, whole rows per CU (M <= 4)
+// ------------------------------------------------------------- few activation rows, whole rows per CU (M <= 8)
 // gemm_gguf_skinny gives each workgroup 32 whole weight rows: 160 workgroups for a 5120-wide output on 256 CUs, which
 // at one or two rows are bound by the dequantisation's VALU issue (each weight value is dequantised for one or two
 // products). Here workgroup b of G takes the row quads [Qt b / G, Qt (b + 1) / G) (Qt = N / 4 quads of 4 weight rows):
@@ -621,7 +621,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_gguf_skinny(const uint16_t* __re
 // part h), so one step multiplies super-block h S + s of every part at once, and the wanted sums are the diagonal
 // blocks D[4 t + h][4 j + h]: lane (c, kq) keeps register h = c % 4 (activation row t = kq), and the 4 parts are
 // added across lanes c ^ 1 and c ^ 2. Each lane dequantises its 8 values straight into its B fragment as in the
-// few-rows kernel. Unit (quad, s) = one step over super-block s of the 4 parts; a workgroup's units (quad-major) are
+// few-rows kernel. With MT = 2 groups of activation rows (5-8 rows) each B fragment feeds a second MFMA whose A rows
+// are activation rows 4-7 over the same parts. Unit (quad, s) = one step over super-block s of the 4 parts; a workgroup's units (quad-major) are
 // spread evenly over its NW waves, each wave streaming its range with the raw bytes two units ahead and the unit's 8
 // activation fragments one unit ahead. A wave's sums for a quad go to LDS (red[quad][wave][4 t + j], zero where a
 // wave has no share) and are added in wave order after the barrier: no partial sums leave the workgroup. Weight and
@@ -668,13 +669,13 @@ __device__ __forceinline__ void quad_load(__amdgpu_buffer_rsrc_t r, uint32_t o, 
 template <int QT>
 struct QdTs { static constexpr int TS = QT == 8 ? 272 : GGUFTs<QT>::TS; };
 
-template <int QT, int MID, bool BIAS>
+template <int QT, int MID, bool BIAS, int MT>
 __global__ __launch_bounds__(64 * kQdWaves) void gemm_gguf_quad(const uint16_t* __restrict__ X,
                                                           const uint8_t* __restrict__ W,
                                                           const uint16_t* __restrict__ bias,
                                                           uint16_t* __restrict__ Y, int M, int N, int K, int G) {
     constexpr int TS = QdTs<QT>::TS, NW = kQdWaves;
-    __shared__ float red[kQdMaxQuads][NW][16];
+    __shared__ float red[kQdMaxQuads][NW][16 * MT];
     const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, kq = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = c & 3, jt = c >> 2;                 // part; quad row (B) and activation row (A) of this lane
@@ -683,7 +684,7 @@ __global__ __launch_bounds__(64 * kQdWaves) void gemm_gguf_quad(const uint16_t* 
     const int q0 = (int)((int64_t)Qt * blockIdx.x / G), nq = (int)((int64_t)Qt * (blockIdx.x + 1) / G) - q0;
     const int nu = nq * S;
     const int lo = nu * wave / NW, hi = nu * (wave + 1) / NW;
-    for (int i = tid; i < kQdMaxQuads * NW * 16; i += 64 * NW) (&red[0][0][0])[i] = 0.0f;
+    for (int i = tid; i < kQdMaxQuads * NW * 16 * MT; i += 64 * NW) (&red[0][0][0])[i] = 0.0f;
     const uint32_t row_bytes = (uint32_t)nsb * TS;
     const __amdgpu_buffer_rsrc_t rw = tile_rsrc(W, (int64_t)N * row_bytes);
     const __amdgpu_buffer_rsrc_t rx = tile_rsrc(X, (int64_t)M * K * 2);
@@ -693,28 +694,38 @@ __global__ __launch_bounds__(64 * kQdWaves) void gemm_gguf_quad(const uint16_t* 
         const int row = 4 * (q0 + lq) + jt, sb = h * S + ls;
         return row < N && sb < nsb ? (uint32_t)row * row_bytes + (uint32_t)sb * TS : kQdNowhere;
     };
-    auto xofs = [&](int ls) {
-        const int sb = h * S + ls;
-        return jt < M && sb < nsb ? (uint32_t)(jt * K + sb * 256 + 8 * kq) * 2u : kQdNowhere;
+    // activation row jt + 4 mt (row group mt of MT)
+    auto xofs = [&](int ls, int mt) {
+        const int sb = h * S + ls, t = jt + 4 * mt;
+        return t < M && sb < nsb ? (uint32_t)(t * K + sb * 256 + 8 * kq) * 2u : kQdNowhere;
     };
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     typedef typename QdRaw<QT>::type Raw;
-    auto unit = [&](const Raw& raw, const bf16x8 (&a)[8]) {
+    // each B fragment is dequantised once for the MT row groups' MFMAs
+    auto unit = [&](const Raw& raw, const bf16x8 (&a)[MT][8]) {
         SkRaw<QT> wr;
         if constexpr (QT == 14) wr = q6_unwin(raw);
         else wr = raw;
         static_for<8>([&](auto Gc) {
             const bf16x8 bw = sk_dequant<QT, MID, decltype(Gc)::value>(wr, kq);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[decltype(Gc)::value], bw, acc, 0, 0, 0);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mt][decltype(Gc)::value], bw, acc[mt], 0, 0, 0);
         });
     };
-    // the wave's sums for quad cq: register h of lane (c, kq) is D[4 kq + h][c], parts added across lanes c ^ 1, c ^ 2
+    // the wave's sums for quad cq: register h of lane (c, kq) in group mt is D[4 kq + h][c] of activation rows
+    // 4 mt .. 4 mt + 3, parts added across lanes c ^ 1, c ^ 2; row t = kq + 4 mt lands at red[cq][wave][4 t + jt]
     auto flush = [&](int cq) {
-        float v = h == 0 ? acc[0] : h == 1 ? acc[1] : h == 2 ? acc[2] : acc[3];
-        v = v + __shfl_xor(v, 1);
-        v = v + __shfl_xor(v, 2);
-        if (h == 0 && kq < M) red[cq][wave][4 * kq + jt] = v;
-        acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            float v = h == 0 ? acc[mt][0] : h == 1 ? acc[mt][1] : h == 2 ? acc[mt][2] : acc[mt][3];
+            v = v + __shfl_xor(v, 1);
+            v = v + __shfl_xor(v, 2);
+            if (h == 0 && kq + 4 * mt < M) red[cq][wave][16 * mt + 4 * kq + jt] = v;
+            acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
     };
     __syncthreads();                                  // red is zero before any wave's sums land
     if (lo < hi) {
@@ -726,11 +737,14 @@ __global__ __launch_bounds__(64 * kQdWaves) void gemm_gguf_quad(const uint16_t* 
             }
         };
         Raw w[2];
-        bf16x8 ax[2][8];
-        auto load_act = [&](bf16x8 (&a)[8], int s) {
-            const uint32_t o = xofs(s);
+        bf16x8 ax[2][MT][8];
+        auto load_act = [&](bf16x8 (&a)[MT][8], int s) {
 #pragma unroll
-            for (int g = 0; g < 8; g++) a[g] = __builtin_bit_cast(bf16x8, ld128(rx, o + 64 * g));
+            for (int mt = 0; mt < MT; mt++) {
+                const uint32_t o = xofs(s, mt);
+#pragma unroll
+                for (int g = 0; g < 8; g++) a[mt][g] = __builtin_bit_cast(bf16x8, ld128(rx, o + 64 * g));
+            }
         };
         int cq = lo / S, cs = lo - cq * S;            // compute cursor
         auto finish_unit = [&](int ui) {
@@ -1156,24 +1170,29 @@ static void launch_splitk_mid(int mid, const uint16_t* X, const uint8_t* W, cons
     else launch_splitk<QT, WF_F32>(X, W, bias, Y, M, N, K, p, ws, st);
 }
 
-// The whole-rows form (gemm_gguf_quad): one or two rows where the few-rows kernel's 32-row workgroups leave CUs idle
-// (N < 8192: fewer than 256 of them), and for Q6_K, whose few-rows kernel waits on its raw loads, up to N < 16384 on
-// 512 workgroups. Measured on MI355X against the few-rows kernel, Wan shapes, cold weights, per layer at one row:
-// Q4_K 5120 x 5120 9.3 against 9.8 us, 5120 x 13824 18.6 against 24.3; Q5_K 10.0 against 11.2, 20.1 against 26.4;
-// Q6_K 10.2 against 14.4, 23.8 against 37.0, 13824 x 5120 22.3 against 35.2 (512 workgroups). At 13824 x 5120 the
-// Q4_K / Q5_K few-rows kernel (432 workgroups) stays as fast or faster (Q4_K 17.5 against 18.2 on 512 workgroups,
-// 18.6 on 256), and from three rows on its shared activation loads win (Q4_K block at 3 rows 83.0 against 82.1 us);
-// Q6_K keeps the whole-rows form up to four rows (block at 4 rows 114.6 against 132.7 us).
-// Q8_0 has no other fused form: the whole-rows form takes it where Q6_K's rule does, and every other Q8_0 shape is
-// left to the caller's two-step flow (the entry points answer WF_EUNSUPPORTED).
-static constexpr int kQuadMaxRows = 2, kQuadMaxRowsQ6 = 4;
+// The whole-rows form (gemm_gguf_quad): one to three rows where the few-rows kernel's 32-row workgroups leave CUs
+// idle (N < 8192: fewer than 256 of them), and for Q6_K, whose few-rows kernel waits on its raw loads, up to
+// N < 16384 on 512 workgroups. Measured on MI355X against the few-rows kernel, Wan shapes, cold weights, per layer at
+// one row: Q4_K 5120 x 5120 9.3 against 9.8 us, 5120 x 13824 18.6 against 24.3; Q5_K 10.0 against 11.2, 20.1 against
+// 26.4; Q6_K 10.2 against 14.4, 23.8 against 37.0, 13824 x 5120 22.3 against 35.2 (512 workgroups). At 13824 x 5120
+// the Q4_K / Q5_K few-rows kernel (432 workgroups) stays as fast or faster (Q4_K 17.5 against 18.2 on 512
+// workgroups, 18.6 on 256). Q4_K / Q5_K blocks at 3 rows 79.0 / 85.5 against 82.5 / 92.9 us; at 4 rows the few-rows
+// kernel's shared activation loads win (Q4_K 83.5 against 87.1). Q6_K keeps the whole-rows form up to four rows
+// (block at 4 rows 114.6 against 132.7 us); at 5-8 rows (two groups of four activation rows) it loses (123.3
+// against 168.9 at 8 rows), as do Q4_K / Q5_K.
+// Q8_0 has no other fused form: the whole-rows form takes it at 1-8 rows of outputs narrower than 16384 (Wan block
+// at 5 / 8 rows 135.3 / 166.8 us, at 4 rows 115.1; the two-step flow about 257), and every other Q8_0 shape is left
+// to the caller's two-step flow (the entry points answer WF_EUNSUPPORTED).
+static constexpr int kQuadMaxRows = 3, kQuadMaxRowsQ6 = 4, kQuadMaxRowsQ8 = 8;
+static_assert(kQuadMaxRowsQ8 <= 8, "the whole-rows kernel takes two groups of 4 activation rows at most");
 
 static bool quad_takes(int64_t M, int64_t N, int64_t K, int qtype) {
     const bool wide = qtype == 14 || qtype == 8;
     const int64_t ts = qtype == 12 ? 144 : qtype == 13 ? 176 : qtype == 14 ? 210 : 272;
+    const int rows = qtype == 8 ? kQuadMaxRowsQ8 : qtype == 14 ? kQuadMaxRowsQ6 : kQuadMaxRows;
     // (weight and activation bytes both addressed by 32-bit buffer offsets)
-    return M >= 1 && M <= (wide ? kQuadMaxRowsQ6 : kQuadMaxRows) && (N + 31) / 32 < (wide ? 512 : 256) &&
-           M * K * 2 < (1LL << 31) && N * (K / 256) * ts < (1LL << 31);
+    return M >= 1 && M <= rows && (N + 31) / 32 < (wide ? 512 : 256) && M * K * 2 < (1LL << 31) &&
+           N * (K / 256) * ts < (1LL << 31);
 }
 
 template <int QT, int MID>
@@ -1181,8 +1200,14 @@ static void launch_quad(const uint16_t* X, const uint8_t* W, const uint16_t* bia
                         hipStream_t st) {
     // 256 workgroups (one per CU) below 8192 rows, 512 (two per CU) up to 16384: at most kQdMaxQuads quads each
     const int G = std::min((N + 3) / 4, N >= 8192 ? 512 : 256);
-    if (bias) gemm_gguf_quad<QT, MID, true><<<dim3(G), 64 * kQdWaves, 0, st>>>(X, W, bias, Y, M, N, K, G);
-    else gemm_gguf_quad<QT, MID, false><<<dim3(G), 64 * kQdWaves, 0, st>>>(X, W, bias, Y, M, N, K, G);
+    if (M > 4) {                                      // two groups of 4 activation rows (Q8_0)
+        if (bias) gemm_gguf_quad<QT, MID, true, 2><<<dim3(G), 64 * kQdWaves, 0, st>>>(X, W, bias, Y, M, N, K, G);
+        else gemm_gguf_quad<QT, MID, false, 2><<<dim3(G), 64 * kQdWaves, 0, st>>>(X, W, bias, Y, M, N, K, G);
+    } else if (bias) {
+        gemm_gguf_quad<QT, MID, true, 1><<<dim3(G), 64 * kQdWaves, 0, st>>>(X, W, bias, Y, M, N, K, G);
+    } else {
+        gemm_gguf_quad<QT, MID, false, 1><<<dim3(G), 64 * kQdWaves, 0, st>>>(X, W, bias, Y, M, N, K, G);
+    }
 }
 
 static void run_gguf_q8(int mid, const void* x_bf16, const void* wq, const void* bias_bf16, void* out_bf16, int M,
@@ -1293,7 +1318,7 @@ namespace wf {
 static int check_gguf(const char* who, const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes,
                       int qtype, int64_t N, const void* bias_bf16, const void* out_bf16, int mid_dt) {
     if (qtype != 12 && qtype != 13 && qtype != 14 && qtype != 8) {
-        set_error("%s: GGML type %d is not handled (Q4_K, Q5_K, Q6_K; Q8_0 at 1-4 rows)", who, qtype);
+        set_error("%s: GGML type %d is not handled (Q4_K, Q5_K, Q6_K; Q8_0 at 1-8 rows)", who, qtype);
         return WF_EUNSUPPORTED;
     }
     if (mid_dt < 0 || mid_dt > 2) { set_error("%s: dequant dtype %d", who, mid_dt); return WF_EUNSUPPORTED; }
@@ -1318,7 +1343,7 @@ static int check_gguf(const char* who, const void* x_bf16, int64_t M, int64_t K,
         return WF_EUNSUPPORTED;
     }
     if (qtype == 8 && !quad_takes(M, N, K, 8)) {
-        set_error("%s: Q8_0 is fused at 1-4 rows of outputs at most 16352 wide only (%lld x %lld here)", who,
+        set_error("%s: Q8_0 is fused at 1-8 rows of outputs at most 16352 wide only (%lld x %lld here)", who,
                   (long long)M, (long long)N);
         return WF_EUNSUPPORTED;
     }

@@ -16,7 +16,7 @@ from .. import _native
 from . import gguf_dequant
 
 _FUSED_TYPES = {12: 144, 13: 176, 14: 210, 8: 272}   # weight bytes per 256 values (Q8_0: 8 blocks of 34)
-Q8_0_ROWS = 4                # Q8_0 is fused at 1-4 rows of outputs up to 16352 wide (the library's whole-rows form)
+Q8_0_ROWS = 8                # Q8_0 is fused at 1-8 rows of outputs up to 16352 wide (the library's whole-rows form)
 Q8_0_MAX_N = 16352
 _MID = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 _workspaces = {}             # (device index, stream) -> uint8 workspace whose counter words are zero between calls

@@ -95,30 +95,30 @@ int wf_linear_i8_residual(const int8_t* xq, const int8_t* wq, const float* xs, c
 /* ------------------------------------------------------------------------------- fused dequant + bf16 GEMM
  * y[m, n] = bf16(sum_k x[m, k] * W[n, k] (+ bias[n])) with W given as GGUF K-quant blocks (qtype 12 Q4_K, 13 Q5_K,
  * 14 Q6_K; [N, K] row-major in 256-value super-blocks, wq_bytes = N * K / 256 * block bytes; also qtype 8 Q8_0, 34
- * bytes per 32 values, at 1-4 rows of N <= 16352 only, WF_EUNSUPPORTED elsewhere) and dequantised inside
+ * bytes per 32 values, at 1-8 rows of N <= 16352 only, WF_EUNSUPPORTED elsewhere) and dequantised inside
  * the kernel exactly as wf_dequant does with dequant dtype mid_dt and output bf16; float32 accumulation. No
  * reference function does this in one step: it replaces `dequantize` (enhancers/gguf_dequant.py:296-326) followed
  * by ComfyUI-GGUF's torch.nn.functional.linear on the bf16 weight. x: bf16 [M, K], 16-byte aligned; bias: bf16 [N]
- * or NULL; out: bf16 [M, N]. K % 256 == 0. M <= 64 runs the few-rows forms (the weight streamed once; at 1-2 rows
- * of N < 8192, Q6_K 1-4 rows of N < 16384: workgroups of whole 4-row quads), 65-512 rows the panel form,
+ * or NULL; out: bf16 [M, N]. K % 256 == 0. M <= 64 runs the few-rows forms (the weight streamed once; at 1-3 rows
+ * of N < 8192, Q6_K 1-4 rows and Q8_0 1-8 rows of N < 16384: workgroups of whole 4-row quads), 65-512 rows the panel
+ * form,
  * larger M the tiled form (256 x 320 tiles; Q6_K from 1024 rows 512 x 160). */
 int wf_linear_gguf(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes, int qtype, int64_t N,
                    const void* bias_bf16, void* out_bf16, int mid_dt, void* stream);
 
 /* wf_linear_gguf with a caller-provided workspace, for the same reference call site (enhancers/gguf_dequant.py:
- * 296-326 followed by ComfyUI-GGUF's F.linear). A narrow, deep product (N <= 2048, K >= 8192, K >= 2 N) with
- * 1 <= M <= 8 rows is split along K over many more workgroups than weight rows allow: each writes float32 partial sums into the workspace, and the
- * last workgroup of each column tile adds them in a fixed order (the result is the same on every run). Workspace:
- * 256-byte aligned, at least the bytes wf_linear_gguf_workspace gives; its first 16 KiB are counters that must be
- * zero on entry and are zero again when the call has run, whatever its shape (a workspace cleared once can be reused
- * by later calls of any shape on the same stream; calls that overlap on one workspace race). With 33-512 rows,
- * and with 17-32 rows of a deep product (K >= 2 N), the panel form splits K into slices (at least two
+ * 296-326 followed by ComfyUI-GGUF's F.linear). A narrow, deep product (N <= 2048, K >= 8192, K >= 2 N) with 1 <= M <=
+ * 8 rows is split along K over many more workgroups than weight rows allow: each writes float32 partial sums into the
+ * workspace, and the last workgroup of each column tile adds them in a fixed order (the result is the same on every
+ * run). Workspace: 256-byte aligned, at least the bytes wf_linear_gguf_workspace gives; its first 16 KiB are counters
+ * that must be zero on entry and are zero again when the call has run, whatever its shape (a workspace cleared once
+ * can be reused by later calls of any shape on the same stream; calls that overlap on one workspace race). With 33-512
+ * rows, and with 17-32 rows of a deep product (K >= 2 N), the panel form splits K into slices (at least two
  * super-blocks each), enough to give the chip 256 workgroups: each slice writes float32 partial sums into the
  * workspace past the split form's 16 KiB of counters, which it leaves untouched (16 KiB + S * M * N * 4 bytes), and a
- * second kernel adds them in slice order; up to 64 rows only when
- * K gives more than one slice. wf_linear_gguf_workspace does not know the format and gives the largest need over
- * them. Any other shape does not use the workspace (workspace may be NULL) and
- * is wf_linear_gguf. */
+ * second kernel adds them in slice order; up to 64 rows only when K gives more than one slice.
+ * wf_linear_gguf_workspace does not know the format and gives the largest need over them. Any other shape does not use
+ * the workspace (workspace may be NULL) and is wf_linear_gguf. */
 int wf_linear_gguf_workspace(int64_t M, int64_t N, int64_t K, int64_t* bytes);
 int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes, int qtype, int64_t N,
                       const void* bias_bf16, void* out_bf16, int mid_dt, void* workspace, int64_t workspace_bytes,
