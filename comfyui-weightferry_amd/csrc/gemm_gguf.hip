@@ -351,6 +351,21 @@ __device__ __forceinline__ SkRaw<14> q6_unwin(const Q6Win& w) {
     return s;
 }
 
+// Q8_0 through a buffer resource: 8 blocks of 34 bytes from byte offset o (a multiple of 4: the units are 272 bytes
+// in rows of whole units), one 12-byte load per block from the dword at or below 34 g (lanes kq = 0: the block's d
+// and their quants) or below 34 g + 2 + 8 kq (the others' quants); sk_dequant<8> takes them apart
+__device__ __forceinline__ void sk_load_q8(__amdgpu_buffer_rsrc_t r, uint32_t o, int kq, SkRaw<8>& w) {
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+        const uint32_t b = (kq == 0 ? o + 34 * g : o + 34 * g + 2 + 8 * kq) & ~3u;
+        w.raw[g] = __builtin_bit_cast(u32x3q, __builtin_amdgcn_raw_buffer_load_b96(r, b, 0, 0));
+    }
+}
+
+// bytes per 256 values: a K-quant super-block, or 8 Q8_0 blocks
+template <int QT>
+struct QdTs { static constexpr int TS = QT == 8 ? 272 : GGUFTs<QT>::TS; };
+
 template <int QT>
 struct QdRaw { typedef SkRaw<QT> type; };
 template <>
@@ -472,7 +487,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_gguf_skinny(const uint16_t* __re
                                                             const uint8_t* __restrict__ W,
                                                             const uint16_t* __restrict__ bias,
                                                             uint16_t* __restrict__ Y, int M, int N, int K) {
-    constexpr int TS = GGUFTs<QT>::TS;
+    constexpr int TS = QdTs<QT>::TS;
     __shared__ f32x4 red[NW][NR * MT][64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -482,7 +497,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_gguf_skinny(const uint16_t* __re
     const uint8_t* wrow[NR];
 #pragma unroll
     for (int nr = 0; nr < NR; nr++) wrow[nr] = W + (int64_t)min(n0 + 16 * nr + r, N - 1) * row_bytes;
-    // Q6_K: the workgroup's rows through a buffer resource (rows past N read as zeros; their sums are not stored)
+    // Q6_K, Q8_0: the workgroup's rows through a buffer resource (rows past N read as zeros; their sums are not
+    // stored)
     const __amdgpu_buffer_rsrc_t rw = tile_rsrc(W + (int64_t)n0 * row_bytes, (int64_t)min(16 * NR, N - n0) * row_bytes);
     uint32_t rofs[NR];
 #pragma unroll
@@ -501,6 +517,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_gguf_skinny(const uint16_t* __re
 #pragma unroll
         for (int nr = 0; nr < NR; nr++) {
             if constexpr (QT == 14) sk_load_q6w(rw, rofs[nr] + (uint32_t)sb * TS, kq, w[nr]);
+            else if constexpr (QT == 8) sk_load_q8(rw, rofs[nr] + (uint32_t)sb * TS, kq, w[nr]);
             else sk_load<QT>(wrow[nr] + (int64_t)sb * TS, kq, w[nr]);
         }
     };
@@ -611,7 +628,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_gguf_skinny(const uint16_t* __re
     }
 }
 
-// ------------------------------------------------------------- few activation rows, whole rows per CU (M <= 8)
+// ------------------------------------------------------------- few activation rows, whole rows per CU (M <= 4)
 // gemm_gguf_skinny gives each workgroup 32 whole weight rows: 160 workgroups for a 5120-wide output on 256 CUs, which
 // at one or two rows are bound by the dequantisation's VALU issue (each weight value is dequantised for one or two
 // products). Here workgroup b of G takes the row quads [Qt b / G, Qt (b + 1) / G) (Qt = N / 4 quads of 4 weight rows):
@@ -621,8 +638,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_gguf_skinny(const uint16_t* __re
 // part h), so one step multiplies super-block h S + s of every part at once, and the wanted sums are the diagonal
 // blocks D[4 t + h][4 j + h]: lane (c, kq) keeps register h = c % 4 (activation row t = kq), and the 4 parts are
 // added across lanes c ^ 1 and c ^ 2. Each lane dequantises its 8 values straight into its B fragment as in the
-// few-rows kernel. With MT = 2 groups of activation rows (5-8 rows) each B fragment feeds a second MFMA whose A rows
-// are activation rows 4-7 over the same parts. Unit (quad, s) = one step over super-block s of the 4 parts; a workgroup's units (quad-major) are
+// few-rows kernel. Unit (quad, s) = one step over super-block s of the 4 parts; a workgroup's units (quad-major) are
 // spread evenly over its NW waves, each wave streaming its range with the raw bytes two units ahead and the unit's 8
 // activation fragments one unit ahead. A wave's sums for a quad go to LDS (red[quad][wave][4 t + j], zero where a
 // wave has no share) and are added in wave order after the barrier: no partial sums leave the workgroup. Weight and
@@ -647,17 +663,6 @@ __device__ __forceinline__ void sk_load_rs(__amdgpu_buffer_rsrc_t r, uint32_t o,
     if constexpr (QT == 13) w.qh = ld64(r, o + 16 + 8 * kq);
 }
 
-// Q8_0 through a buffer resource: 8 blocks of 34 bytes from byte offset o (a multiple of 4: the units are 272 bytes
-// in rows of whole units), one 12-byte load per block from the dword at or below 34 g (lanes kq = 0: the block's d
-// and their quants) or below 34 g + 2 + 8 kq (the others' quants); sk_dequant<8> takes them apart
-__device__ __forceinline__ void sk_load_q8(__amdgpu_buffer_rsrc_t r, uint32_t o, int kq, SkRaw<8>& w) {
-#pragma unroll
-    for (int g = 0; g < 8; g++) {
-        const uint32_t b = (kq == 0 ? o + 34 * g : o + 34 * g + 2 + 8 * kq) & ~3u;
-        w.raw[g] = __builtin_bit_cast(u32x3q, __builtin_amdgcn_raw_buffer_load_b96(r, b, 0, 0));
-    }
-}
-
 template <int QT>
 __device__ __forceinline__ void quad_load(__amdgpu_buffer_rsrc_t r, uint32_t o, int kq, typename QdRaw<QT>::type& w) {
     if constexpr (QT == 14) sk_load_q6w(r, o, kq, w);
@@ -665,17 +670,14 @@ __device__ __forceinline__ void quad_load(__amdgpu_buffer_rsrc_t r, uint32_t o, 
     else sk_load_rs<QT>(r, o, kq, w);
 }
 
-// bytes per 256 values: a K-quant super-block, or 8 Q8_0 blocks
-template <int QT>
-struct QdTs { static constexpr int TS = QT == 8 ? 272 : GGUFTs<QT>::TS; };
 
-template <int QT, int MID, bool BIAS, int MT>
+template <int QT, int MID, bool BIAS>
 __global__ __launch_bounds__(64 * kQdWaves) void gemm_gguf_quad(const uint16_t* __restrict__ X,
                                                           const uint8_t* __restrict__ W,
                                                           const uint16_t* __restrict__ bias,
                                                           uint16_t* __restrict__ Y, int M, int N, int K, int G) {
     constexpr int TS = QdTs<QT>::TS, NW = kQdWaves;
-    __shared__ float red[kQdMaxQuads][NW][16 * MT];
+    __shared__ float red[kQdMaxQuads][NW][16];
     const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, kq = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = c & 3, jt = c >> 2;                 // part; quad row (B) and activation row (A) of this lane
@@ -684,7 +686,7 @@ __global__ __launch_bounds__(64 * kQdWaves) void gemm_gguf_quad(const uint16_t* 
     const int q0 = (int)((int64_t)Qt * blockIdx.x / G), nq = (int)((int64_t)Qt * (blockIdx.x + 1) / G) - q0;
     const int nu = nq * S;
     const int lo = nu * wave / NW, hi = nu * (wave + 1) / NW;
-    for (int i = tid; i < kQdMaxQuads * NW * 16 * MT; i += 64 * NW) (&red[0][0][0])[i] = 0.0f;
+    for (int i = tid; i < kQdMaxQuads * NW * 16; i += 64 * NW) (&red[0][0][0])[i] = 0.0f;
     const uint32_t row_bytes = (uint32_t)nsb * TS;
     const __amdgpu_buffer_rsrc_t rw = tile_rsrc(W, (int64_t)N * row_bytes);
     const __amdgpu_buffer_rsrc_t rx = tile_rsrc(X, (int64_t)M * K * 2);
@@ -694,38 +696,28 @@ __global__ __launch_bounds__(64 * kQdWaves) void gemm_gguf_quad(const uint16_t* 
         const int row = 4 * (q0 + lq) + jt, sb = h * S + ls;
         return row < N && sb < nsb ? (uint32_t)row * row_bytes + (uint32_t)sb * TS : kQdNowhere;
     };
-    // activation row jt + 4 mt (row group mt of MT)
-    auto xofs = [&](int ls, int mt) {
-        const int sb = h * S + ls, t = jt + 4 * mt;
-        return t < M && sb < nsb ? (uint32_t)(t * K + sb * 256 + 8 * kq) * 2u : kQdNowhere;
+    auto xofs = [&](int ls) {
+        const int sb = h * S + ls;
+        return jt < M && sb < nsb ? (uint32_t)(jt * K + sb * 256 + 8 * kq) * 2u : kQdNowhere;
     };
-    f32x4 acc[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     typedef typename QdRaw<QT>::type Raw;
-    // each B fragment is dequantised once for the MT row groups' MFMAs
-    auto unit = [&](const Raw& raw, const bf16x8 (&a)[MT][8]) {
+    auto unit = [&](const Raw& raw, const bf16x8 (&a)[8]) {
         SkRaw<QT> wr;
         if constexpr (QT == 14) wr = q6_unwin(raw);
         else wr = raw;
         static_for<8>([&](auto Gc) {
             const bf16x8 bw = sk_dequant<QT, MID, decltype(Gc)::value>(wr, kq);
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mt][decltype(Gc)::value], bw, acc[mt], 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[decltype(Gc)::value], bw, acc, 0, 0, 0);
         });
     };
-    // the wave's sums for quad cq: register h of lane (c, kq) in group mt is D[4 kq + h][c] of activation rows
-    // 4 mt .. 4 mt + 3, parts added across lanes c ^ 1, c ^ 2; row t = kq + 4 mt lands at red[cq][wave][4 t + jt]
+    // the wave's sums for quad cq: register h of lane (c, kq) is D[4 kq + h][c], parts added across lanes c ^ 1, c ^ 2
     auto flush = [&](int cq) {
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            float v = h == 0 ? acc[mt][0] : h == 1 ? acc[mt][1] : h == 2 ? acc[mt][2] : acc[mt][3];
-            v = v + __shfl_xor(v, 1);
-            v = v + __shfl_xor(v, 2);
-            if (h == 0 && kq + 4 * mt < M) red[cq][wave][16 * mt + 4 * kq + jt] = v;
-            acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
+        float v = h == 0 ? acc[0] : h == 1 ? acc[1] : h == 2 ? acc[2] : acc[3];
+        v = v + __shfl_xor(v, 1);
+        v = v + __shfl_xor(v, 2);
+        if (h == 0 && kq < M) red[cq][wave][4 * kq + jt] = v;
+        acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     };
     __syncthreads();                                  // red is zero before any wave's sums land
     if (lo < hi) {
@@ -737,14 +729,11 @@ __global__ __launch_bounds__(64 * kQdWaves) void gemm_gguf_quad(const uint16_t* 
             }
         };
         Raw w[2];
-        bf16x8 ax[2][MT][8];
-        auto load_act = [&](bf16x8 (&a)[MT][8], int s) {
+        bf16x8 ax[2][8];
+        auto load_act = [&](bf16x8 (&a)[8], int s) {
+            const uint32_t o = xofs(s);
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++) {
-                const uint32_t o = xofs(s, mt);
-#pragma unroll
-                for (int g = 0; g < 8; g++) a[mt][g] = __builtin_bit_cast(bf16x8, ld128(rx, o + 64 * g));
-            }
+            for (int g = 0; g < 8; g++) a[g] = __builtin_bit_cast(bf16x8, ld128(rx, o + 64 * g));
         };
         int cq = lo / S, cs = lo - cq * S;            // compute cursor
         auto finish_unit = [&](int ui) {
@@ -1178,13 +1167,12 @@ static void launch_splitk_mid(int mid, const uint16_t* X, const uint8_t* W, cons
 // the Q4_K / Q5_K few-rows kernel (432 workgroups) stays as fast or faster (Q4_K 17.5 against 18.2 on 512
 // workgroups, 18.6 on 256). Q4_K / Q5_K blocks at 3 rows 79.0 / 85.5 against 82.5 / 92.9 us; at 4 rows the few-rows
 // kernel's shared activation loads win (Q4_K 83.5 against 87.1). Q6_K keeps the whole-rows form up to four rows
-// (block at 4 rows 114.6 against 132.7 us); at 5-8 rows (two groups of four activation rows) it loses (123.3
-// against 168.9 at 8 rows), as do Q4_K / Q5_K.
-// Q8_0 has no other fused form: the whole-rows form takes it at 1-8 rows of outputs narrower than 16384 (Wan block
-// at 5 / 8 rows 135.3 / 166.8 us, at 4 rows 115.1; the two-step flow about 257), and every other Q8_0 shape is left
-// to the caller's two-step flow (the entry points answer WF_EUNSUPPORTED).
-static constexpr int kQuadMaxRows = 3, kQuadMaxRowsQ6 = 4, kQuadMaxRowsQ8 = 8;
-static_assert(kQuadMaxRowsQ8 <= 8, "the whole-rows kernel takes two groups of 4 activation rows at most");
+// (block at 4 rows 114.6 against 132.7 us), as does Q8_0 (105 / 115 us at 3 / 4 rows against 143 with the
+// few-rows kernel). A second group of four activation rows (two MFMAs per dequantised fragment) lost to the few-rows
+// kernel at 5-8 rows for every format (Q8_0 block at 8 rows 168.9 against 124.0 us, Q6_K 168.9 against 123.3).
+static constexpr int kQuadMaxRows = 3, kQuadMaxRowsQ6 = 4, kQuadMaxRowsQ8 = 4;
+static_assert(kQuadMaxRows <= 4 && kQuadMaxRowsQ6 <= 4 && kQuadMaxRowsQ8 <= 4,
+              "the whole-rows kernel takes 4 activation rows at most");
 
 static bool quad_takes(int64_t M, int64_t N, int64_t K, int qtype) {
     const bool wide = qtype == 14 || qtype == 8;
@@ -1200,26 +1188,10 @@ static void launch_quad(const uint16_t* X, const uint8_t* W, const uint16_t* bia
                         hipStream_t st) {
     // 256 workgroups (one per CU) below 8192 rows, 512 (two per CU) up to 16384: at most kQdMaxQuads quads each
     const int G = std::min((N + 3) / 4, N >= 8192 ? 512 : 256);
-    if (M > 4) {                                      // two groups of 4 activation rows (Q8_0)
-        if (bias) gemm_gguf_quad<QT, MID, true, 2><<<dim3(G), 64 * kQdWaves, 0, st>>>(X, W, bias, Y, M, N, K, G);
-        else gemm_gguf_quad<QT, MID, false, 2><<<dim3(G), 64 * kQdWaves, 0, st>>>(X, W, bias, Y, M, N, K, G);
-    } else if (bias) {
-        gemm_gguf_quad<QT, MID, true, 1><<<dim3(G), 64 * kQdWaves, 0, st>>>(X, W, bias, Y, M, N, K, G);
-    } else {
-        gemm_gguf_quad<QT, MID, false, 1><<<dim3(G), 64 * kQdWaves, 0, st>>>(X, W, bias, Y, M, N, K, G);
-    }
+    if (bias) gemm_gguf_quad<QT, MID, true><<<dim3(G), 64 * kQdWaves, 0, st>>>(X, W, bias, Y, M, N, K, G);
+    else gemm_gguf_quad<QT, MID, false><<<dim3(G), 64 * kQdWaves, 0, st>>>(X, W, bias, Y, M, N, K, G);
 }
 
-static void run_gguf_q8(int mid, const void* x_bf16, const void* wq, const void* bias_bf16, void* out_bf16, int M,
-                        int N, int K, hipStream_t s) {
-    const uint16_t* X = static_cast<const uint16_t*>(x_bf16);
-    const uint8_t* W = static_cast<const uint8_t*>(wq);
-    const uint16_t* B = static_cast<const uint16_t*>(bias_bf16);
-    uint16_t* Y = static_cast<uint16_t*>(out_bf16);
-    if (mid == WF_F16) launch_quad<8, WF_F16>(X, W, B, Y, M, N, K, s);
-    else if (mid == WF_BF16) launch_quad<8, WF_BF16>(X, W, B, Y, M, N, K, s);
-    else launch_quad<8, WF_F32>(X, W, B, Y, M, N, K, s);
-}
 
 #ifndef WF_SKINNY_NR1_MAX_N
 #define WF_SKINNY_NR1_MAX_N 8191
@@ -1232,6 +1204,38 @@ static void launch_skinny(const uint16_t* X, const uint8_t* W, const uint16_t* b
     const dim3 grid((unsigned)((N + 16 * NR - 1) / (16 * NR)));
     if (bias) gemm_gguf_skinny<QT, MID, true, MT, NR, NW, AHEAD><<<grid, 64 * NW, 0, s>>>(X, W, bias, Y, M, N, K);
     else gemm_gguf_skinny<QT, MID, false, MT, NR, NW, AHEAD><<<grid, 64 * NW, 0, s>>>(X, W, bias, Y, M, N, K);
+}
+
+// Q8_0's fused forms: the whole-rows form where it takes the shape, else the few-rows kernel up to 64 rows (its
+// 12-byte block loads and d shared by a lane permute as in the whole-rows form; activations read per stage, which
+// measured faster than one super-block ahead: 124.0 against 148.0 us at 8 rows). Wan block against the two-step flow
+// (wf_dequant, then torch's GEMM), cold weights: 122 / 125 / 130 / 169 / 273 us at 5 / 9 / 16 / 32 / 64 rows against
+// 304-337. Every other Q8_0 shape is left to the caller's two-step flow (the entry points answer WF_EUNSUPPORTED).
+static bool q8_skinny_takes(int64_t M, int64_t N, int64_t K) {
+    // (a workgroup's 32 weight rows addressed by 32-bit buffer offsets)
+    return M >= 1 && M <= 64 && N >= 1 && 32 * (K / 256) * 272 < (1LL << 31);
+}
+
+static bool q8_takes(int64_t M, int64_t N, int64_t K) { return quad_takes(M, N, K, 8) || q8_skinny_takes(M, N, K); }
+
+template <int MID>
+static void launch_q8(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
+                      hipStream_t s) {
+    if (quad_takes(M, N, K, 8)) launch_quad<8, MID>(X, W, bias, Y, M, N, K, s);
+    else if (M <= 16) launch_skinny<8, MID, 1, 2, 8>(X, W, bias, Y, M, N, K, s);
+    else if (M <= 32) launch_skinny<8, MID, 2, 2, 8>(X, W, bias, Y, M, N, K, s);
+    else launch_skinny<8, MID, 4, 2, 8>(X, W, bias, Y, M, N, K, s);
+}
+
+static void run_gguf_q8(int mid, const void* x_bf16, const void* wq, const void* bias_bf16, void* out_bf16, int M,
+                        int N, int K, hipStream_t s) {
+    const uint16_t* X = static_cast<const uint16_t*>(x_bf16);
+    const uint8_t* W = static_cast<const uint8_t*>(wq);
+    const uint16_t* B = static_cast<const uint16_t*>(bias_bf16);
+    uint16_t* Y = static_cast<uint16_t*>(out_bf16);
+    if (mid == WF_F16) launch_q8<WF_F16>(X, W, B, Y, M, N, K, s);
+    else if (mid == WF_BF16) launch_q8<WF_BF16>(X, W, B, Y, M, N, K, s);
+    else launch_q8<WF_F32>(X, W, B, Y, M, N, K, s);
 }
 
 template <int QT, int MID, int VM, int VN, int WM, int WN>
@@ -1318,7 +1322,7 @@ namespace wf {
 static int check_gguf(const char* who, const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes,
                       int qtype, int64_t N, const void* bias_bf16, const void* out_bf16, int mid_dt) {
     if (qtype != 12 && qtype != 13 && qtype != 14 && qtype != 8) {
-        set_error("%s: GGML type %d is not handled (Q4_K, Q5_K, Q6_K; Q8_0 at 1-8 rows)", who, qtype);
+        set_error("%s: GGML type %d is not handled (Q4_K, Q5_K, Q6_K; Q8_0 at 1-64 rows)", who, qtype);
         return WF_EUNSUPPORTED;
     }
     if (mid_dt < 0 || mid_dt > 2) { set_error("%s: dequant dtype %d", who, mid_dt); return WF_EUNSUPPORTED; }
@@ -1342,9 +1346,8 @@ static int check_gguf(const char* who, const void* x_bf16, int64_t M, int64_t K,
         set_error("%s: sizes too large", who);
         return WF_EUNSUPPORTED;
     }
-    if (qtype == 8 && !quad_takes(M, N, K, 8)) {
-        set_error("%s: Q8_0 is fused at 1-8 rows of outputs at most 16352 wide only (%lld x %lld here)", who,
-                  (long long)M, (long long)N);
+    if (qtype == 8 && !q8_takes(M, N, K)) {
+        set_error("%s: Q8_0 is fused at 1-64 rows only (%lld x %lld here)", who, (long long)M, (long long)N);
         return WF_EUNSUPPORTED;
     }
     return WF_OK;

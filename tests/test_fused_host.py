@@ -16,11 +16,11 @@ def test_gguf_linear_holds_the_blocks_of_its_format():
 
 
 def test_prefer_fused_rule_q8_0():
-    # Q8_0 is fused only in the library's whole-rows form: 1-8 rows of outputs up to 16352 wide
-    for rows in (1, 2, 4, 5, 8):
+    # Q8_0 is fused in the library's whole-rows and few-rows forms: 1-64 rows of any width
+    for rows in (1, 2, 4, 5, 8, 9, 32, 64):
         assert fg.prefer_fused(rows, 8, 5120, 5120) and fg.prefer_fused(rows, 8, 13824, 5120)
-        assert fg.prefer_fused(rows, 8, 16352, 5120) and not fg.prefer_fused(rows, 8, 16353, 5120)
-    for rows in (9, 32, 128, 4096):
+        assert fg.prefer_fused(rows, 8, 16353, 5120)
+    for rows in (65, 128, 4096):
         assert not fg.prefer_fused(rows, 8, 5120, 5120)
 
 

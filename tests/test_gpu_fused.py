@@ -156,7 +156,7 @@ def test_q6k_tall_form_whole_output(native, M, N, K, with_bias, mid, offset):
     check_gpu(y, x, weight_bf16(raw, qtype, mid, N, K), bias=bias)
 
 
-@pytest.mark.parametrize("qtype", [12, 13, 14])
+@pytest.mark.parametrize("qtype", [12, 13, 14, 8])
 @pytest.mark.parametrize("mid", [0, 2])
 @pytest.mark.parametrize("M,N,K,with_bias", [(1, 300, 256, True), (5, 5120, 5120, False), (16, 61, 512, True),
                                              (17, 1000, 1024, False), (33, 300, 2048, True), (64, 5120, 512, False),
@@ -166,8 +166,11 @@ def test_few_rows_whole_output(native, qtype, mid, M, N, K, with_bias):
     # up to 64 activation rows take the few-rows kernel (32 weight rows per workgroup, K split over its 8 waves,
     # 1 to 4 row tiles of 16; K = 256 and 512 leave waves with no super-block); 65 rows the panel kernel: ragged M
     # and N, every output element checked. 777 x 1280: the last workgroup's last weight row ends with a Q6_K block
-    # that starts on a dword (the buffer range check ends at that row)
-    raw = encode.random_blocks(qtype, N * K // 256, seed=qtype * 7 + M, family="normal")
+    # that starts on a dword (the buffer range check ends at that row). Q8_0 takes the few-rows kernel from 5 rows (1-4
+    # rows of outputs narrower than 16384: the whole-rows form) and is not the library's case at 65
+    if qtype == 8 and M > 64:
+        pytest.skip("Q8_0 is not the library's case beyond 64 rows")
+    raw = encode.random_blocks(qtype, nblocks(qtype, N, K), seed=qtype * 7 + M, family="normal")
     g = torch.Generator().manual_seed(M * 31 + N)
     x = torch.randn((M, K), generator=g).to(torch.bfloat16)
     bias = torch.randn(N, generator=g).to(torch.bfloat16) if with_bias else None
@@ -184,12 +187,10 @@ def nblocks(qtype, N, K):
 @pytest.mark.parametrize("M,N,K,with_bias", [(1, 5120, 5120, True), (2, 5120, 13824, False), (1, 8000, 5120, True),
                                              (2, 4101, 1280, True), (1, 61, 256, False), (2, 1, 768, True),
                                              (1, 1000, 2304, False), (1, 13824, 5120, True), (2, 9001, 512, False),
-                                             (3, 5120, 1280, True), (4, 13000, 768, False), (5, 5120, 1280, True),
-                                             (8, 4101, 768, False), (7, 13000, 512, True), (6, 61, 256, False)])
+                                             (3, 5120, 1280, True), (4, 13000, 768, False), (1, 16400, 512, True)])
 def test_whole_rows_form_whole_output(native, qtype, mid, M, N, K, with_bias):
-    # K-quants at one to three rows of an output narrower than 8192 (Q6_K: up to four rows and 16384 wide, on 512
-    # workgroups from 8192; Q8_0, which has no other fused form, up to eight rows in two groups of four activation
-    # rows; the other shapes take the few-rows kernel): each
+    # K-quants at one to three rows of an output narrower than 8192 (Q6_K and Q8_0: up to four rows and 16384 wide,
+    # on 512 workgroups from 8192; the other shapes, and 16400 rows, take the few-rows kernel): each
     # workgroup takes whole quads of 4 weight rows, the MFMA's 16 columns holding 4 rows x 4 parts of K. The Wan
     # shapes (5120 rows: 20 per CU; 13824: 54 super-blocks in parts of 14, the last part 12; 13824 rows: Q6_K's
     # 512-workgroup grid, Q4_K / Q5_K's few-rows kernel), 8000 rows (7-8 quads per workgroup), ragged N (4101, 61, 1,
@@ -224,9 +225,11 @@ def test_whole_rows_form_one_hot_rows_are_the_weight_bits(native, qtype, mid):
     assert np.isfinite(w.numpy()).all()
     rd = torch.from_numpy(raw).cuda()
     ks = np.concatenate([[0, 31, 32, 255, 256, 1279, 1280, 2559, 2560, 3839, 3840, K - 1], rng.integers(0, K, 20)])
-    per = {12: 3, 13: 3, 14: 4, 8: 8}[qtype]             # the most rows the whole-rows form takes (ragged last call)
-    for i in range(0, len(ks), per):
-        sel = ks[i:i + per]
+    per = {12: 3, 13: 3, 14: 4, 8: 4}[qtype]             # the most rows the whole-rows form takes (ragged last call)
+    calls = [ks[i:i + per] for i in range(0, len(ks), per)]
+    if qtype == 8:
+        calls += [ks[:16], ks[16:]]                      # and Q8_0 through the few-rows kernel
+    for sel in calls:
         x = torch.zeros((len(sel), K), dtype=torch.bfloat16)
         x[torch.arange(len(sel)), torch.from_numpy(sel)] = 1.0
         y = fused(native, x.cuda(), rd, qtype, N, mid=mid).cpu().float()
@@ -234,14 +237,15 @@ def test_whole_rows_form_one_hot_rows_are_the_weight_bits(native, qtype, mid):
 
 
 def test_q8_0_drop_in_fuses_few_rows_and_falls_back_elsewhere(native):
-    # the GGUF linear with a Q8_0 weight: at 1-8 rows the library's whole-rows form, at 9 rows and more the two-step
-    # flow (wf_dequant, then the bf16 GEMM); both against the float32 product of the oracle's bf16 weight
+    # the GGUF linear with a Q8_0 weight: at 1-4 rows the library's whole-rows form, at 5-64 its few-rows kernel,
+    # beyond the two-step flow (wf_dequant, then the bf16 GEMM); all against the float32 product of the oracle's bf16
+    # weight
     fg = sub("enhancers.fused_gguf")
     N, K = 5120, 2048
     raw = encode.random_blocks(8, nblocks(8, N, K), seed=8, family="normal")
     rd = torch.from_numpy(raw).cuda()
     w = weight_bf16(raw, 8, 0, N, K)
-    for rows, fused in ((1, True), (4, True), (5, True), (8, True), (9, False), (64, False)):
+    for rows, fused in ((1, True), (4, True), (5, True), (64, True), (65, False), (128, False)):
         x = torch.randn((rows, K), generator=torch.Generator().manual_seed(rows)).to(torch.bfloat16)
         assert fg.prefer_fused(rows, 8, N, K) is fused
         assert (fg.fused_linear(x.cuda(), rd, 8, (N, K)) is not None) is fused
