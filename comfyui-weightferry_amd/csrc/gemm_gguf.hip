@@ -937,7 +937,7 @@ __global__ __launch_bounds__(64 * kPnWaves) __attribute__((amdgpu_waves_per_eu(2
                                                                  const uint16_t* __restrict__ bias,
                                                                  uint16_t* __restrict__ Y, float* __restrict__ part,
                                                                  int M, int N, int K, int NT, int MTI, int KS) {
-    constexpr int TS = GGUFTs<QT>::TS, NR = 2, BM = 16 * MT;
+    constexpr int TS = QdTs<QT>::TS, NR = 2, BM = 16 * MT;
     constexpr int RPW = BM / 4 / kPnWaves;             // 1 KiB DMA runs per wave per half super-block
     __shared__ __align__(1024) uint8_t xs0[BM * 256], xs1[BM * 256];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -953,6 +953,9 @@ __global__ __launch_bounds__(64 * kPnWaves) __attribute__((amdgpu_waves_per_eu(2
     const uint8_t* wrow[NR];
 #pragma unroll
     for (int nr = 0; nr < NR; nr++) wrow[nr] = W + (int64_t)min(n0 + 16 * nr + r, N - 1) * row_bytes;
+    // Q8_0: the wave's 32 weight rows through a buffer resource (rows past N read as zeros; their sums are not stored)
+    const __amdgpu_buffer_rsrc_t rw = tile_rsrc(W + (int64_t)min(n0, N) * row_bytes,
+                                                (int64_t)max(0, min(32, N - n0)) * row_bytes);
     // rows past M read as zeros (the buffer's range ends at row M); their sums are never stored
     const __amdgpu_buffer_rsrc_t rx = tile_rsrc(X + (int64_t)m0 * K, (int64_t)(M - m0) * K * 2);
     uint32_t aoff[RPW];
@@ -971,7 +974,10 @@ __global__ __launch_bounds__(64 * kPnWaves) __attribute__((amdgpu_waves_per_eu(2
     SkRaw<QT> w0[NR], w1[NR];
     auto load_raw = [&](SkRaw<QT> (&wr)[NR], int sb) {
 #pragma unroll
-        for (int nr = 0; nr < NR; nr++) sk_load<QT>(wrow[nr] + (int64_t)sb * TS, kq, wr[nr]);
+        for (int nr = 0; nr < NR; nr++) {
+            if constexpr (QT == 8) sk_load_q8(rw, (uint32_t)((16 * nr + r) * row_bytes + sb * TS), kq, wr[nr]);
+            else sk_load<QT>(wrow[nr] + (int64_t)sb * TS, kq, wr[nr]);
+        }
     };
     f32x4 acc[NR][MT];
 #pragma unroll
@@ -1216,7 +1222,11 @@ static bool q8_skinny_takes(int64_t M, int64_t N, int64_t K) {
     return M >= 1 && M <= 64 && N >= 1 && 32 * (K / 256) * 272 < (1LL << 31);
 }
 
-static bool q8_takes(int64_t M, int64_t N, int64_t K) { return quad_takes(M, N, K, 8) || q8_skinny_takes(M, N, K); }
+// (the panel form takes Q8_0 at 65-512 rows, a wave's 32 weight rows in 32-bit buffer offsets as in the few-rows
+// kernel; kPanelMaxRows)
+static bool q8_takes(int64_t M, int64_t N, int64_t K) {
+    return quad_takes(M, N, K, 8) || q8_skinny_takes(M, N, K) || (M > 64 && M <= 512 && q8_skinny_takes(1, N, K));
+}
 
 template <int MID>
 static void launch_q8(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
@@ -1322,7 +1332,7 @@ namespace wf {
 static int check_gguf(const char* who, const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes,
                       int qtype, int64_t N, const void* bias_bf16, const void* out_bf16, int mid_dt) {
     if (qtype != 12 && qtype != 13 && qtype != 14 && qtype != 8) {
-        set_error("%s: GGML type %d is not handled (Q4_K, Q5_K, Q6_K; Q8_0 at 1-64 rows)", who, qtype);
+        set_error("%s: GGML type %d is not handled (Q4_K, Q5_K, Q6_K; Q8_0 at 1-512 rows)", who, qtype);
         return WF_EUNSUPPORTED;
     }
     if (mid_dt < 0 || mid_dt > 2) { set_error("%s: dequant dtype %d", who, mid_dt); return WF_EUNSUPPORTED; }
@@ -1347,7 +1357,7 @@ static int check_gguf(const char* who, const void* x_bf16, int64_t M, int64_t K,
         return WF_EUNSUPPORTED;
     }
     if (qtype == 8 && !q8_takes(M, N, K)) {
-        set_error("%s: Q8_0 is fused at 1-64 rows only (%lld x %lld here)", who, (long long)M, (long long)N);
+        set_error("%s: Q8_0 is fused at 1-512 rows only (%lld x %lld here)", who, (long long)M, (long long)N);
         return WF_EUNSUPPORTED;
     }
     return WF_OK;
@@ -1359,6 +1369,7 @@ static int check_gguf(const char* who, const void* x_bf16, int64_t M, int64_t K,
 // slice: 563 against 856 us at 128 rows, 684 against 887 at 512); from 1024 rows the tiled kernel's 256 x 320 tiles,
 // which dequantise each weight value once per 256 rows instead of once per 128, are faster (909 against 1334 us).
 static constexpr int64_t kPanelMaxRows = 512;
+static_assert(kPanelMaxRows == 512, "q8_takes states the panel form's rows");
 static constexpr int64_t kPanelMinRowsWs = 17;       // fewest rows the panel form takes with a workspace
 
 // Without a workspace (one slice) the panel form takes 65-512 rows.
@@ -1390,7 +1401,9 @@ static int panel_target(int64_t M, int qtype) { return M > 384 || (qtype == 14 &
 
 static PanelPlan panel_plan(int64_t M, int64_t N, int64_t K, int64_t max_part, int qtype) {
     PanelPlan p{};
-    p.mt = M <= 32 ? 2 : M <= 64 ? 4 : 8;
+    // (Q8_0's raw bytes, 24 registers per row group and set against the K-quants' 12, leave 128-row panels short of
+    // registers at two waves per SIMD: they spilled 60; its panels take 64 rows)
+    p.mt = M <= 32 ? 2 : M <= 64 || qtype == 8 ? 4 : 8;
     p.mti = (int)((M + 16 * p.mt - 1) / (16 * p.mt));
     p.nt = (int)((N + kPnRows - 1) / kPnRows);
     const int nsb = (int)(K / 256);
@@ -1432,11 +1445,11 @@ static void launch_panel(int mid, const uint16_t* X, const uint8_t* W, const uin
         if (mid == WF_F16) launch_panel_mt<QT, WF_F16, 2>(X, W, bias, Y, M, N, K, p, ws, st);
         else if (mid == WF_BF16) launch_panel_mt<QT, WF_BF16, 2>(X, W, bias, Y, M, N, K, p, ws, st);
         else launch_panel_mt<QT, WF_F32, 2>(X, W, bias, Y, M, N, K, p, ws, st);
-    } else if (p.mt == 4) {
+    } else if (p.mt == 4 || QT == 8) {                // (Q8_0: 64-row panels at most, panel_plan)
         if (mid == WF_F16) launch_panel_mt<QT, WF_F16, 4>(X, W, bias, Y, M, N, K, p, ws, st);
         else if (mid == WF_BF16) launch_panel_mt<QT, WF_BF16, 4>(X, W, bias, Y, M, N, K, p, ws, st);
         else launch_panel_mt<QT, WF_F32, 4>(X, W, bias, Y, M, N, K, p, ws, st);
-    } else {
+    } else if constexpr (QT != 8) {
         if (mid == WF_F16) launch_panel_mt<QT, WF_F16, 8>(X, W, bias, Y, M, N, K, p, ws, st);
         else if (mid == WF_BF16) launch_panel_mt<QT, WF_BF16, 8>(X, W, bias, Y, M, N, K, p, ws, st);
         else launch_panel_mt<QT, WF_F32, 8>(X, W, bias, Y, M, N, K, p, ws, st);
@@ -1451,6 +1464,7 @@ static void run_gguf_panel(int qtype, int mid_dt, const void* x_bf16, const void
     uint16_t* Y = static_cast<uint16_t*>(out_bf16);
     if (qtype == 12) launch_panel<12>(mid_dt, X, W, B, Y, M, N, K, p, ws, s);
     else if (qtype == 13) launch_panel<13>(mid_dt, X, W, B, Y, M, N, K, p, ws, s);
+    else if (qtype == 8) launch_panel<8>(mid_dt, X, W, B, Y, M, N, K, p, ws, s);
     else launch_panel<14>(mid_dt, X, W, B, Y, M, N, K, p, ws, s);
 }
 
@@ -1493,7 +1507,7 @@ extern "C" int wf_linear_gguf(const void* x_bf16, int64_t M, int64_t K, const vo
     const int rc = check_gguf("wf_linear_gguf", x_bf16, M, K, wq, wq_bytes, qtype, N, bias_bf16, out_bf16, mid_dt);
     if (rc != WF_OK || M == 0 || N == 0) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (qtype == 8) run_gguf_q8(mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, s);
+    if (qtype == 8 && M <= 64) run_gguf_q8(mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, s);
     else run_gguf(qtype, mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, s);
     WF_LAUNCH_CHECK("wf_linear_gguf launch");
     return WF_OK;
@@ -1507,8 +1521,9 @@ extern "C" int wf_linear_gguf_workspace(int64_t M, int64_t N, int64_t K, int64_t
     // the format is not known here: the largest need over them (Q6_K's panels take more slices up to 128 rows)
     if (split_takes(M, N, K)) *bytes = split_plan(M, N, K).bytes();
     else if (panel_takes_ws(M, N, K)) {
-        const int64_t part = std::max(panel_plan(M, N, K, INT64_MAX, 12).part_bytes,
-                                      panel_plan(M, N, K, INT64_MAX, 14).part_bytes);
+        const int64_t part = std::max({panel_plan(M, N, K, INT64_MAX, 12).part_bytes,
+                                       panel_plan(M, N, K, INT64_MAX, 14).part_bytes,
+                                       panel_plan(M, N, K, INT64_MAX, 8).part_bytes});
         if (part > 0) *bytes = kSplitCounterBytes + part;   // the split form's counters stay untouched
     }
     return WF_OK;
@@ -1521,7 +1536,7 @@ extern "C" int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const
     const int rc = check_gguf("wf_linear_gguf_ws", x_bf16, M, K, wq, wq_bytes, qtype, N, bias_bf16, out_bf16, mid_dt);
     if (rc != WF_OK || M == 0 || N == 0) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (qtype == 8) {                                 // the whole-rows form: no workspace
+    if (qtype == 8 && M <= 64) {                      // the whole-rows or few-rows form: no workspace
         run_gguf_q8(mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, s);
         WF_LAUNCH_CHECK("wf_linear_gguf_ws launch");
         return WF_OK;
@@ -1608,7 +1623,7 @@ extern "C" int wf_linear_gguf_noalloc(const void* x_bf16, int64_t M, int64_t K, 
                               mid_dt);
     if (rc != WF_OK || M == 0 || N == 0) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (qtype == 8) {                                 // the whole-rows form: no scratch
+    if (qtype == 8 && M <= 64) {                      // the whole-rows or few-rows form: no scratch
         run_gguf_q8(mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, s);
         WF_LAUNCH_CHECK("wf_linear_gguf_noalloc launch");
         return WF_OK;

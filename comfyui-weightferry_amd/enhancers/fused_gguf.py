@@ -16,7 +16,7 @@ from .. import _native
 from . import gguf_dequant
 
 _FUSED_TYPES = {12: 144, 13: 176, 14: 210, 8: 272}   # weight bytes per 256 values (Q8_0: 8 blocks of 34)
-Q8_0_ROWS = 64               # Q8_0 is fused at 1-64 rows (the library's whole-rows and few-rows forms)
+Q8_0_ROWS = 512              # Q8_0 is fused at 1-512 rows (the library's whole-rows, few-rows and panel forms)
 _MID = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 _workspaces = {}             # (device index, stream) -> uint8 workspace whose counter words are zero between calls
 _needs = {}                  # (rows, n_out, k) -> the workspace bytes wf_linear_gguf_workspace gives
@@ -106,14 +106,14 @@ def fused_linear(x, data, qtype, oshape, bias=None, mid_dtype=None):
 #     5 % (Q4_K).
 # mode "fused" still takes the tiled form at any row count.
 FEW_ROWS = 64
-PANEL_ROWS = {12: 512, 13: 384, 14: 256}
+# Q8_0 (64-row panels): 243 / 252 / 437 µs against 339 / 424 / 553 at 65 / 128 / 256 rows; at 384 rows its ffn_up
+# 150 against 114 µs, the other layers 56 / 131 against 59 / 136; at 512 rows 721 against 540 per block. At 1-64 rows
+# (whole-rows and few-rows forms) 87-273 µs against 257-337.
+PANEL_ROWS = {12: 512, 13: 384, 14: 256, 8: 384}
 
 
 def prefer_fused(rows, qtype, n_out, k):
     """mode "auto": True when the fused kernel is the faster way to compute this layer on MI355X."""
-    if int(qtype) == 8:
-        # Wan block, cold weights: 87-273 µs at 1-64 rows against 257-337 two-step
-        return rows <= Q8_0_ROWS
     if rows <= FEW_ROWS:
         return True
     limit = PANEL_ROWS.get(int(qtype), 0)

@@ -118,14 +118,14 @@ def test_probe_is_a_separate_library_with_its_own_checks():
 
 
 def test_fused_gemm_q8_0_checks_without_gpu():
-    # Q8_0 (8 blocks of 34 bytes per 256 values) is the library's case only at 1-64 rows;
+    # Q8_0 (8 blocks of 34 bytes per 256 values) is the library's case only at 1-512 rows;
     # elsewhere it answers "not my case" before any launch, so the caller's two-step flow runs
     native = sub("_native")
     lib = native.lib()
     buf = ctypes.create_string_buffer(64)
     p16 = (ctypes.addressof(buf) + 15) // 16 * 16
     N, K = 4, 256
-    for M, n in ((65, N), (128, N), (4096, 16353)):
+    for M, n in ((513, N), (1024, N), (4096, 16353)):
         rc = lib.wf_linear_gguf(p16, M, K, p16, n * (K // 256) * 272, 8, n, None, p16, 0, None)
         assert rc == native.EUNSUPPORTED and "Q8_0" in native.last_error(), (M, n)
     # a block count that is not 34 bytes per 32 values

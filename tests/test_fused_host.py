@@ -16,11 +16,14 @@ def test_gguf_linear_holds_the_blocks_of_its_format():
 
 
 def test_prefer_fused_rule_q8_0():
-    # Q8_0 is fused in the library's whole-rows and few-rows forms: 1-64 rows of any width
-    for rows in (1, 2, 4, 5, 8, 9, 32, 64):
+    # Q8_0 is fused in the library's whole-rows and few-rows forms at 1-64 rows of any width, and in its panel form
+    # up to 384 rows (256 for outputs wider than K); beyond the two-step flow is faster
+    for rows in (1, 2, 4, 5, 8, 9, 32, 64, 65, 128, 256):
         assert fg.prefer_fused(rows, 8, 5120, 5120) and fg.prefer_fused(rows, 8, 13824, 5120)
         assert fg.prefer_fused(rows, 8, 16353, 5120)
-    for rows in (65, 128, 4096):
+    assert fg.prefer_fused(384, 8, 5120, 5120) and fg.prefer_fused(384, 8, 5120, 13824)
+    assert not fg.prefer_fused(384, 8, 13824, 5120)
+    for rows in (385, 512, 4096):
         assert not fg.prefer_fused(rows, 8, 5120, 5120)
 
 

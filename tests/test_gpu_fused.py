@@ -167,9 +167,7 @@ def test_few_rows_whole_output(native, qtype, mid, M, N, K, with_bias):
     # 1 to 4 row tiles of 16; K = 256 and 512 leave waves with no super-block); 65 rows the panel kernel: ragged M
     # and N, every output element checked. 777 x 1280: the last workgroup's last weight row ends with a Q6_K block
     # that starts on a dword (the buffer range check ends at that row). Q8_0 takes the few-rows kernel from 5 rows (1-4
-    # rows of outputs narrower than 16384: the whole-rows form) and is not the library's case at 65
-    if qtype == 8 and M > 64:
-        pytest.skip("Q8_0 is not the library's case beyond 64 rows")
+    # rows of outputs narrower than 16384: the whole-rows form), the panel form at 65
     raw = encode.random_blocks(qtype, nblocks(qtype, N, K), seed=qtype * 7 + M, family="normal")
     g = torch.Generator().manual_seed(M * 31 + N)
     x = torch.randn((M, K), generator=g).to(torch.bfloat16)
@@ -237,18 +235,20 @@ def test_whole_rows_form_one_hot_rows_are_the_weight_bits(native, qtype, mid):
 
 
 def test_q8_0_drop_in_fuses_few_rows_and_falls_back_elsewhere(native):
-    # the GGUF linear with a Q8_0 weight: at 1-4 rows the library's whole-rows form, at 5-64 its few-rows kernel,
-    # beyond the two-step flow (wf_dequant, then the bf16 GEMM); all against the float32 product of the oracle's bf16
-    # weight
+    # the GGUF linear with a Q8_0 weight: at 1-4 rows the library's whole-rows form, at 5-64 its few-rows kernel, then
+    # its panel form (up to 256 rows for this output, wider than K), beyond the two-step flow (wf_dequant, then the
+    # bf16 GEMM) -- the fused kernel itself takes up to 512 rows and declines more; all against the float32 product of
+    # the oracle's bf16 weight
     fg = sub("enhancers.fused_gguf")
     N, K = 5120, 2048
     raw = encode.random_blocks(8, nblocks(8, N, K), seed=8, family="normal")
     rd = torch.from_numpy(raw).cuda()
     w = weight_bf16(raw, 8, 0, N, K)
-    for rows, fused in ((1, True), (4, True), (5, True), (64, True), (65, False), (128, False)):
+    for rows, fused in ((1, True), (4, True), (5, True), (64, True), (65, True), (256, True), (257, False),
+                        (513, False)):
         x = torch.randn((rows, K), generator=torch.Generator().manual_seed(rows)).to(torch.bfloat16)
         assert fg.prefer_fused(rows, 8, N, K) is fused
-        assert (fg.fused_linear(x.cuda(), rd, 8, (N, K)) is not None) is fused
+        assert (fg.fused_linear(x.cuda(), rd, 8, (N, K)) is not None) is (rows <= 512)
         y = fg.linear(x.cuda(), rd, 8, (N, K))
         torch.cuda.synchronize()
         check(y, x, w)
@@ -345,7 +345,7 @@ def noalloc(native, x, raw_dev, qtype, N, bias=None, mid=0):
     return y
 
 
-@pytest.mark.parametrize("qtype", [12, 13, 14])
+@pytest.mark.parametrize("qtype", [12, 13, 14, 8])
 @pytest.mark.parametrize("M,N,K,with_bias,mid", [(65, 300, 512, True, 0), (128, 256, 2048, False, 2),
                                                  (129, 1002, 1024, True, 0), (300, 520, 5120, False, 0),
                                                  (512, 130, 768, True, 2), (257, 384, 1024, False, 1),
@@ -358,9 +358,10 @@ def test_panel_whole_output(native, qtype, M, N, K, with_bias, mid):
     # super-blocks at least), their float32 partial sums added in slice order by a second kernel; allocation-free
     # with the slices its scratch holds. With the workspace it also takes 33-64 rows (MT = 4) and 17-32 rows (MT = 2)
     # of a deep product (K >= 2 N), when K gives more than one slice (else the few-rows kernel: 40 x 512, and the
-    # shallow 24 x 640 x 1024); wf_linear_gguf keeps the few-rows kernel up to 64 rows. Ragged M and N (N % 4 != 0 takes the reduction's
-    # element path), every output element checked; the three agree bit for bit where they run the same slices
-    raw = encode.random_blocks(qtype, N * K // 256, seed=qtype * 3 + M, family="normal")
+    # shallow 24 x 640 x 1024); wf_linear_gguf keeps the few-rows kernel up to 64 rows. Ragged M and N (N % 4 != 0
+    # takes the reduction's element path), every output element checked; the three agree bit for bit where they run
+    # the same slices. Q8_0 takes the panel form from 65 rows only (64-row panels), its few-rows forms below
+    raw = encode.random_blocks(qtype, nblocks(qtype, N, K), seed=qtype * 3 + M, family="normal")
     g = torch.Generator().manual_seed(M * 7 + N)
     x = torch.randn((M, K), generator=g).to(torch.bfloat16)
     bias = torch.randn(N, generator=g).to(torch.bfloat16) if with_bias else None
