@@ -193,12 +193,11 @@ def fused_leg(torch, native):
     # layer spanning > 600 MB, so MI355X's 256 MB last-level cache cannot serve a call from the one before (a weight
     # in a real forward was last read a step earlier); "warm": the same weight every call. Every row count goes
     # through fused_gguf.fused_linear, the drop-in's choice of form with its workspace: the panel form in K slices at
-    # 128 rows, and at 32 rows for the deep ffn_down (K >= 2 N); the whole-rows form at one token (Q4_K / Q5_K for
-    # the 5120-wide outputs, Q6_K and Q8_0 for all six); the few-rows form otherwise.
+    # 128 rows (Q8_0 in 64-row panels), and at 32 rows for the K-quants' deep ffn_down (K >= 2 N); the whole-rows form
+    # at one token (Q4_K / Q5_K for the 5120-wide outputs, Q6_K and Q8_0 for all six); the few-rows form otherwise.
     fg = importlib.import_module(PKG + ".enhancers.fused_gguf")
     for rows in (128, 32, 1):
-        # (Q8_0 is fused at 1-64 rows only)
-        for qt, name in ((12, "q4_k"), (13, "q5_k"), (14, "q6_k")) + (((8, "q8_0"),) if rows <= 64 else ()):
+        for qt, name in ((12, "q4_k"), (13, "q5_k"), (14, "q6_k"), (8, "q8_0")):
             tf = tc = tu = 0.0
             wbytes = 0
             for lname, N, K in WAN_LINEARS:
