@@ -1216,7 +1216,9 @@ static void launch_skinny(const uint16_t* X, const uint8_t* W, const uint16_t* b
 // 12-byte block loads and d shared by a lane permute as in the whole-rows form; activations read per stage, which
 // measured faster than one super-block ahead: 124.0 against 148.0 us at 8 rows). Wan block against the two-step flow
 // (wf_dequant, then torch's GEMM), cold weights: 122 / 125 / 130 / 169 / 273 us at 5 / 9 / 16 / 32 / 64 rows against
-// 304-337. Every other Q8_0 shape is left to the caller's two-step flow (the entry points answer WF_EUNSUPPORTED).
+// 304-337. With a workspace (or the no-alloc scratch) the panel form's rule takes Q8_0 as it takes the K-quants, at
+// 33-64 rows and at 17-32 rows of deep products (Wan block at 48 / 64 rows 169 / 174 against 248 / 275 us, at 32 rows
+// 160 against 171). Beyond 512 rows Q8_0 is left to the caller's two-step flow (WF_EUNSUPPORTED).
 static bool q8_skinny_takes(int64_t M, int64_t N, int64_t K) {
     // (a workgroup's 32 weight rows addressed by 32-bit buffer offsets)
     return M >= 1 && M <= 64 && N >= 1 && 32 * (K / 256) * 272 < (1LL << 31);
@@ -1536,7 +1538,8 @@ extern "C" int wf_linear_gguf_ws(const void* x_bf16, int64_t M, int64_t K, const
     const int rc = check_gguf("wf_linear_gguf_ws", x_bf16, M, K, wq, wq_bytes, qtype, N, bias_bf16, out_bf16, mid_dt);
     if (rc != WF_OK || M == 0 || N == 0) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (qtype == 8 && M <= 64) {                      // the whole-rows or few-rows form: no workspace
+    // Q8_0 up to 64 rows: the whole-rows or few-rows form (no workspace) unless the panel form's rule below takes it
+    if (qtype == 8 && M <= 64 && !(panel_takes_ws(M, N, K) && panel_plan(M, N, K, INT64_MAX, 8).s > 1)) {
         run_gguf_q8(mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, s);
         WF_LAUNCH_CHECK("wf_linear_gguf_ws launch");
         return WF_OK;
@@ -1623,7 +1626,9 @@ extern "C" int wf_linear_gguf_noalloc(const void* x_bf16, int64_t M, int64_t K, 
                               mid_dt);
     if (rc != WF_OK || M == 0 || N == 0) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (qtype == 8 && M <= 64) {                      // the whole-rows or few-rows form: no scratch
+    // Q8_0 up to 64 rows: the whole-rows or few-rows form (no scratch) unless the panel form's rule below takes it
+    if (qtype == 8 && M <= 64 &&
+        !(panel_takes_ws(M, N, K) && panel_plan(M, N, K, kScratchBytes - kSplitCounterBytes, 8).s > 1)) {
         run_gguf_q8(mid_dt, x_bf16, wq, bias_bf16, out_bf16, (int)M, (int)N, (int)K, s);
         WF_LAUNCH_CHECK("wf_linear_gguf_noalloc launch");
         return WF_OK;
