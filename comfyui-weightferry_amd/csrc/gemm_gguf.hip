@@ -1358,6 +1358,11 @@ static int check_gguf(const char* who, const void* x_bf16, int64_t M, int64_t K,
         set_error("%s: sizes too large", who);
         return WF_EUNSUPPORTED;
     }
+    // a workgroup's activation rows (up to 512) through one buffer resource of at most 2^31 - 1 bytes
+    if (K > (1LL << 20)) {
+        set_error("%s: rows of %lld values, more than the 1048576 the kernels address", who, (long long)K);
+        return WF_EUNSUPPORTED;
+    }
     if (qtype == 8 && !q8_takes(M, N, K)) {
         set_error("%s: Q8_0 is fused at 1-512 rows only (%lld x %lld here)", who, (long long)M, (long long)N);
         return WF_EUNSUPPORTED;

@@ -93,17 +93,16 @@ int wf_linear_i8_residual(const int8_t* xq, const int8_t* wq, const float* xs, c
                           int64_t rows_per_group, void* stream);
 
 /* ------------------------------------------------------------------------------- fused dequant + bf16 GEMM
- * y[m, n] = bf16(sum_k x[m, k] * W[n, k] (+ bias[n])) with W given as GGUF K-quant blocks (qtype 12 Q4_K, 13 Q5_K,
- * 14 Q6_K; [N, K] row-major in 256-value super-blocks, wq_bytes = N * K / 256 * block bytes; also qtype 8 Q8_0, 34
- * bytes per 32 values, at 1-512 rows only, WF_EUNSUPPORTED elsewhere; its panels take 64 rows, and
- * wf_linear_gguf_ws and wf_linear_gguf_noalloc give it the panel form at the K-quants' rows) and dequantised inside
- * the kernel exactly as wf_dequant does with dequant dtype mid_dt and output bf16; float32 accumulation. No
- * reference function does this in one step: it replaces `dequantize` (enhancers/gguf_dequant.py:296-326) followed
- * by ComfyUI-GGUF's torch.nn.functional.linear on the bf16 weight. x: bf16 [M, K], 16-byte aligned; bias: bf16 [N]
- * or NULL; out: bf16 [M, N]. K % 256 == 0. M <= 64 runs the few-rows forms (the weight streamed once; at 1-3 rows
- * of N < 8192, Q6_K and Q8_0 1-4 rows of N < 16384: workgroups of whole 4-row quads), 65-512 rows the panel
- * form,
- * larger M the tiled form (256 x 320 tiles; Q6_K from 1024 rows 512 x 160). */
+ * y[m, n] = bf16(sum_k x[m, k] * W[n, k] (+ bias[n])) with W given as GGUF K-quant blocks (qtype 12 Q4_K, 13 Q5_K, 14
+ * Q6_K; [N, K] row-major in 256-value super-blocks, wq_bytes = N * K / 256 * block bytes; also qtype 8 Q8_0, 34 bytes
+ * per 32 values, at 1-512 rows only, WF_EUNSUPPORTED elsewhere; its panels take 64 rows, and wf_linear_gguf_ws and
+ * wf_linear_gguf_noalloc give it the panel form at the K-quants' rows) and dequantised inside the kernel exactly as
+ * wf_dequant does with dequant dtype mid_dt and output bf16; float32 accumulation. No reference function does this in
+ * one step: it replaces `dequantize` (enhancers/gguf_dequant.py:296-326) followed by ComfyUI-GGUF's
+ * torch.nn.functional.linear on the bf16 weight. x: bf16 [M, K], 16-byte aligned; bias: bf16 [N] or NULL; out: bf16
+ * [M, N]. K % 256 == 0, K <= 1048576. M <= 64 runs the few-rows forms (the weight streamed once; at 1-3 rows of N <
+ * 8192, Q6_K and Q8_0 1-4 rows of N < 16384: workgroups of whole 4-row quads), 65-512 rows the panel form, larger M
+ * the tiled form (256 x 320 tiles; Q6_K from 1024 rows 512 x 160). */
 int wf_linear_gguf(const void* x_bf16, int64_t M, int64_t K, const void* wq, int64_t wq_bytes, int qtype, int64_t N,
                    const void* bias_bf16, void* out_bf16, int mid_dt, void* stream);
 

@@ -130,6 +130,12 @@ def test_fused_gemm_q8_0_checks_without_gpu():
         assert rc == native.EUNSUPPORTED and "Q8_0" in native.last_error(), (M, n)
     # a block count that is not 34 bytes per 32 values
     assert lib.wf_linear_gguf(p16, 1, K, p16, N * (K // 256) * 256, 8, N, None, p16, 0, None) == native.EUNSUPPORTED
+    # rows longer than the kernels' buffer ranges address (any format)
+    Kl = (1 << 20) + 256
+    for qt, ts in ((8, 272), (12, 144)):
+        rc = lib.wf_linear_gguf(p16, 1, Kl, p16, N * (Kl // 256) * ts, qt, N, None, p16, 0, None)
+        assert rc == native.EUNSUPPORTED
+        assert "1048576" in native.last_error()
     # nothing to do
     assert lib.wf_linear_gguf(p16, 0, K, p16, N * (K // 256) * 272, 8, N, None, p16, 0, None) == native.OK
 
