@@ -211,7 +211,8 @@ def test_whole_rows_form_one_hot_rows_are_the_weight_bits(native, qtype, mid):
     # activation rows that are unit vectors e_k make every output the dequantised weight value w[n, k] itself (one
     # nonzero product, exact float32 sums, a bf16 value rounded to bf16 again): the whole-rows form's dequantisation
     # equals the oracle's bit for bit, columns at part and super-block edges and random ones, scales of realistic
-    # size and blocks with d in [1, 8)
+    # size and blocks with d in [1, 8); and so do the panel form's (65 rows, one slice: the 32 unit rows, then rows of
+    # zeros) and, for Q8_0, the few-rows kernel's
     N, K = 1000, 5120
     raw = encode.random_blocks(qtype, nblocks(qtype, N, K), seed=qtype, family="normal").reshape(N * K // 256, -1)
     rng = np.random.default_rng(qtype)
@@ -232,6 +233,10 @@ def test_whole_rows_form_one_hot_rows_are_the_weight_bits(native, qtype, mid):
         x[torch.arange(len(sel)), torch.from_numpy(sel)] = 1.0
         y = fused(native, x.cuda(), rd, qtype, N, mid=mid).cpu().float()
         assert torch.equal(y, w[:, torch.from_numpy(sel)].T), sel
+    x = torch.zeros((65, K), dtype=torch.bfloat16)
+    x[torch.arange(len(ks)), torch.from_numpy(ks)] = 1.0
+    y = fused(native, x.cuda(), rd, qtype, N, mid=mid).cpu().float()
+    assert torch.equal(y[:len(ks)], w[:, torch.from_numpy(ks)].T) and not y[len(ks):].any()
 
 
 def test_q8_0_drop_in_fuses_few_rows_and_falls_back_elsewhere(native):
