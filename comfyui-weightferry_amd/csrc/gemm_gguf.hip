@@ -1202,7 +1202,7 @@ static void launch_quad(const uint16_t* X, const uint8_t* W, const uint16_t* bia
 #ifndef WF_SKINNY_NR1_MAX_N
 #define WF_SKINNY_NR1_MAX_N 8191
 #endif
-static constexpr int kSkinnyNr1MaxN = WF_SKINNY_NR1_MAX_N;
+static constexpr int kSkinnyNr1MaxN = WF_SKINNY_NR1_MAX_N, kSkinnyNr1MaxRows = 7;
 
 template <int QT, int MID, int MT, int NR, int NW, bool AHEAD = false>
 static void launch_skinny(const uint16_t* X, const uint8_t* W, const uint16_t* bias, uint16_t* Y, int M, int N, int K,
@@ -1292,10 +1292,12 @@ static void launch(const uint16_t* X, const uint8_t* W, const uint16_t* bias, ui
     // reads at every row count: with its raw bytes through sk_load_q6w the 32-row, 8-wave form is the fastest one
     // (Wan shapes at 1-8 rows, per layer: 18.4 / 34.8 / 39.1 us against 20.3 / 37.2 / 47.4 for the 16-row, 4-wave
     // workgroups with activations ahead and the narrow loads).
-    // Up to 16 rows of a Q6_K product narrower than 256 workgroups of 32 rows, 16 weight rows per workgroup (NR = 1):
-    // more CUs wait on Q6_K's slower raw loads (Wan block at one row 129 against 147 us, cold weights, MI355X). For
-    // Q4_K / Q5_K the 64 CUs that then hold two workgroups set the time (88 against 82 us): their few-rows kernel is
-    // bound by the dequantisation's VALU work per CU, which the split does not shrink.
+    // Up to 7 rows of a Q6_K product narrower than 256 workgroups of 32 rows, 16 weight rows per workgroup (NR = 1):
+    // more CUs wait on Q6_K's raw loads (Wan block at 5 / 7 rows 115.2 / 118.9 against 118.7 / 119.4 us, cold
+    // weights, MI355X); from 8 rows the shared activation loads of 32-row workgroups win (120.0 against 122.1 us at 8,
+    // 122.1 against 134.1 at 12, 126.2 against 147.6 at 16). For Q4_K / Q5_K the 64 CUs that then hold two workgroups
+    // set the time (88 against 82 us at one row): their few-rows kernel is bound by the dequantisation's VALU work per
+    // CU, which the split does not shrink.
     if (quad_takes(M, N, K, QT)) {
         launch_quad<QT, MID>(X, W, bias, Y, M, N, K, s);
         return;
@@ -1305,7 +1307,8 @@ static void launch(const uint16_t* X, const uint8_t* W, const uint16_t* bias, ui
         return;
     }
     if (M <= 16) {
-        if (QT == 14 && N <= kSkinnyNr1MaxN) launch_skinny<QT, MID, 1, 1, 8>(X, W, bias, Y, M, N, K, s);
+        if (QT == 14 && M <= kSkinnyNr1MaxRows && N <= kSkinnyNr1MaxN)
+            launch_skinny<QT, MID, 1, 1, 8>(X, W, bias, Y, M, N, K, s);
         else launch_skinny<QT, MID, 1, 2, 8>(X, W, bias, Y, M, N, K, s);
         return;
     }
